@@ -1,0 +1,219 @@
+"""Benchmark of the fused LM-head linear + per-token cross-entropy on one MI355X.
+
+One step = the hot path of one training minibatch as train.py:97-104 drives
+it: forward (valid-row compaction + fused GEMM/online-LSE), the caller's
+sum + .item() sync, and the backward with the uniform upstream gradient
+1/N into an fp32 dW accumulator.  Inputs are seeded synthetic tensors of the
+named configuration, resident in HBM before timing starts.
+
+Prints ONE JSON line (driver contract) with, in addition:
+  roofline      the dominant kernel (fwd_kernel: 2*H*V*N MFMA flops per
+                launch) timed with HIP events through the C ABI on the
+                stream it is launched on, against the bf16 dense peak
+  cpu_baseline  the reference torch path (oracle/torch_path.py) on the host
+                cores over a bounded prefix of the same batch
+  north_star    6*H*V*N / t_step against the same peak, extra HBM, etc.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from mini_trainer_amd import _lib, synth  # noqa: E402
+from mini_trainer_amd.flce import (_dtype_code, _p, _stream, backward_plan,  # noqa: E402
+                                   fused_linear_cross_entropy, prepare_targets)
+
+PEAK_BF16 = 2.5166e15  # MI355X dense bf16 MFMA, 256 CU x 2.4 GHz x 4096 flop/clk
+PEAK_FP32 = 157.3e12
+METRIC = "fused linear-CE fwd+bwd tokens/s on 1 GPU; MFMA util % of peak; extra HBM GB"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(cfg, budget_s: float):
+    """Reference torch path on the CPU over a bounded prefix of the batch."""
+    from oracle.torch_path import torch_path
+
+    threads = torch.get_num_threads()
+    b = synth.make_batch(cfg, 0, with_tensors=False)
+    g = torch.Generator().manual_seed(cfg.key)
+    rows = 128
+    X = torch.randn(4096, cfg.H, generator=g).to(cfg.dtype)
+    W = synth.make_weight(cfg)
+    y = b["target"][:4096]
+    grad = torch.full((4096,), 1.0)
+    spent, done_rows, t_total = 0.0, 0, 0.0
+    while True:
+        t0 = time.perf_counter()
+        torch_path(X[:rows], W, y[:rows], grad=grad[:rows], chunk_rows=1024)
+        dt = time.perf_counter() - t0
+        done_rows, t_total = rows, dt
+        spent += dt
+        if dt * 2.5 > budget_s - spent or rows >= 4096:
+            break
+        rows *= 2
+    return {
+        "value": done_rows / t_total,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"reference torch path (F.linear {str(cfg.dtype).replace('torch.', '')} -> "
+                   f".float() -> F.cross_entropy(reduction='none') + autograd backward, "
+                   f"none_reduction_losses.py:35) on the first {done_rows} packed rows of "
+                   f"config {cfg.key} (T x V logits in 1024-row chunks), {t_total:.1f} s, "
+                   f"torch threads={threads}, host cpus={os.cpu_count()}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the dW reduce-scatter across ranks is design-only). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    cfg = synth.CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    lib = _lib.load()
+    t0 = time.perf_counter()
+    mbs = [synth.make_batch(cfg, j) for j in range(cfg.minibatches)]
+    log(f"inputs for config {cfg.key} generated in {time.perf_counter() - t0:.1f}s")
+    W = mbs[0]["W"].to(dev)
+    data = [(m["X"].to(dev), m["target"].to(dev)) for m in mbs]
+    del mbs
+    V, H = W.shape
+    T = data[0][0].shape[0]
+    dW = torch.zeros(V, H, dtype=torch.float32, device=dev)
+    Wl = W.requires_grad_(True)
+    n_valid = [int((y != -100).sum().item()) for _, y in data]
+    N_total = sum(n_valid)
+    T_total = T * len(data)
+
+    def step():
+        # one optimizer step's worth of minibatches (config 5: 4 grad-accum minibatches)
+        for X, y in data:
+            Xl = X.detach().requires_grad_(True)
+            loss = fused_linear_cross_entropy(Xl, Wl, y, dw_accumulator=dW)
+            s = loss.float().sum()
+            s.item()  # the caller's sync (train.py:99)
+            torch.autograd.grad(s * (1.0 / N_total), (Xl,))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # extra HBM of one step: allocator peak - live inputs/outputs
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(dev)
+    es = torch.finfo(cfg.dtype).bits // 8
+    outputs = T * 4 + T * H * es  # loss + dX of the live minibatch (dW fp32 is preallocated)
+    extra = peak - base - outputs
+    budget = 0.05 * T * V * es
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    t_step = ms / 1e3
+
+    # dominant kernel: fwd_kernel via mt_flce_forward on the current stream
+    X, y = data[0]
+    ri, rl, n = prepare_targets(y, V)
+    dt = _dtype_code(X.dtype)
+    loss = torch.empty(T, dtype=torch.float32, device=dev)
+    lse = torch.empty(n, dtype=torch.float32, device=dev)
+    wsb = lib.mt_flce_forward_workspace_bytes(T, n, H, V, dt)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    stream = _stream(dev)
+
+    def fwd_call():
+        _lib.check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt, 0.0,
+                                       _p(ri), _p(rl), n, _p(loss), _p(lse), _p(ws), wsb, stream),
+                   "mt_flce_forward")
+
+    fwd_call()
+    torch.cuda.synchronize()
+    reps = max(3, args.steps)
+    ev0.record()
+    for _ in range(reps):
+        fwd_call()
+    ev1.record()
+    torch.cuda.synchronize()
+    fwd_s = ev0.elapsed_time(ev1) / reps / 1e3
+    fwd_flops = 2.0 * H * V * n
+    peak_flops = PEAK_BF16 if cfg.dtype == torch.bfloat16 else PEAK_FP32
+    C, Cv, bws = backward_plan(T, n, H, V, cfg.dtype)
+
+    alg_flops = 6.0 * H * V * N_total
+    out = {
+        "metric": METRIC,
+        "value": T_total / t_step,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (seeded; X~N(0,1), W~N(0,%g), packed lognormal samples)" % cfg.w_std,
+        "config": {
+            "workload": f"config {cfg.key}: {cfg.name} fused LM-head linear + CE fwd+bwd",
+            "T": T, "H": H, "V": V, "minibatches": len(data), "n_valid": N_total,
+            "bwd_chunk_rows": C, "bwd_chunk_vocab": Cv,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "fwd_kernel (mt_flce_forward)",
+            "achieved": fwd_flops / fwd_s / 1e12,
+            "peak": peak_flops / 1e12,
+            "unit": "TFLOP/s",
+            "frac": fwd_flops / fwd_s / peak_flops,
+            "traffic": None,
+            "ms_per_launch": fwd_s * 1e3,
+            "flops_per_launch": fwd_flops,
+        },
+        "north_star": {
+            "alg_flops_6HVN": alg_flops,
+            "achieved_TFLOPs": alg_flops / t_step / 1e12,
+            "frac_of_peak": alg_flops / t_step / peak_flops,
+            "dense_convention_frac": 6.0 * H * V * T_total / t_step / peak_flops,
+            "extra_hbm_GB": extra / 1e9,
+            "extra_hbm_budget_GB": budget / 1e9,
+            "peak_memory_GB": peak / 1e9,
+        },
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget_s)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

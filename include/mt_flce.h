@@ -1,0 +1,181 @@
+/*
+ * mt_flce.h -- C ABI of the MI355X (gfx950) fused LM-head linear + per-token
+ * cross-entropy library (libmt_flce.so).
+ *
+ * The library replaces the arithmetic that mini_trainer reaches through
+ *   none_reduction_losses.py:5-25  liger_fixed_fused_linear_cross_entropy_none_reduction
+ *     -> liger_kernel.transformers.functional.liger_fused_linear_cross_entropy(
+ *            reduction='none', ignore_index, softcap)        (none_reduction_losses.py:16-23)
+ * i.e. loss[t] = logsumexp_v(x_t . w_v) - x_t . w_{y_t}, and +0.0 where
+ * y_t == ignore_index, without materialising the [T, V] logits, plus the
+ * gradients w.r.t. hidden states and lm_head weight for an arbitrary
+ * per-token upstream gradient (train.py:97-104 supplies a uniform one).
+ *
+ * Conventions
+ *   - Every tensor is owned by the caller (PyTorch).  Pointers are device
+ *     pointers; sizes are element counts.  The library never allocates and
+ *     never frees device memory: scratch space is a caller-provided
+ *     workspace whose size is returned by the *_workspace_bytes queries.
+ *   - Every entry point is asynchronous on the caller's stream and never
+ *     synchronises.  Errors found on the host come back as a non-zero status;
+ *     errors that can only be found on the device (labels out of range,
+ *     malformed cu_seqlens) are written to a caller-provided device word that
+ *     the caller reads when it next synchronises.
+ *   - Return value 0 == MT_OK.  mt_flce_last_error() returns a thread-local,
+ *     human-readable description of the last non-zero status.
+ *   - Layouts: X [T, H] with leading dimension ldx (elements), W [V, H] with
+ *     leading dimension ldw, both row-major with unit stride along H.
+ *     ldx and ldw must be multiples of 8 and the base pointers 16-byte aligned.
+ *     H must be a multiple of 64.  dtype selects bf16 (MFMA path) or fp32
+ *     inputs; loss / lse / dW are always fp32, dX has the dtype of X.
+ */
+#ifndef MT_FLCE_H
+#define MT_FLCE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MT_FLCE_ABI_VERSION 1
+
+typedef struct ihipStream_t* mt_stream_t; /* == hipStream_t */
+
+enum mt_dtype { MT_DTYPE_F32 = 0, MT_DTYPE_BF16 = 1 };
+
+enum mt_status {
+  MT_OK = 0,
+  MT_ERR_INVALID_ARGUMENT = 1,
+  MT_ERR_WORKSPACE_TOO_SMALL = 2,
+  MT_ERR_UNSUPPORTED = 3,
+  MT_ERR_HIP = 4
+};
+
+/* Library version of this header; mt_flce_abi_version() must equal it. */
+int mt_flce_abi_version(void);
+
+/* Thread-local text for the last non-zero status on this thread. */
+const char* mt_flce_last_error(void);
+
+/*
+ * Valid-row compaction and label check.
+ * Replaces the host-side pass of the reference's fused loss that counts the
+ * non-ignored targets ((target != ignore_index).sum().item() inside
+ * LIGER:ops/fused_linear_cross_entropy.py::fused_linear_cross_entropy_forward,
+ * reached from none_reduction_losses.py:16-23), and, with shift != 0, the
+ * label shift of TF/loss/loss_utils.py:61-64 (target[t] = labels[t+1],
+ * target[T-1] = ignore_index).
+ *   labels     int64 [T] (device)
+ *   row_index  int32 [T] out: positions t of valid rows, ascending, first N used
+ *   row_label  int32 [T] out: their labels
+ *   counts     int32 [4] out (device): {N, #labels outside [0,V), first bad t or -1, 0}
+ * One workgroup; no synchronisation.  The caller reads counts (one 16-byte
+ * device->host copy, the single sync of a training step) to size the rest.
+ */
+int mt_flce_prepare(const int64_t* labels, int64_t T, int64_t V,
+                    int64_t ignore_index, int shift, int32_t* row_index,
+                    int32_t* row_label, int32_t* counts, mt_stream_t stream);
+
+/* Workspace for mt_flce_forward (bytes). */
+size_t mt_flce_forward_workspace_bytes(int64_t T, int64_t n_valid, int64_t H,
+                                       int64_t V, int dtype);
+
+/*
+ * Forward: per-token loss and per-valid-row log-sum-exp.
+ * Replaces LIGER:ops/fused_linear_cross_entropy.py::fused_linear_cross_entropy_forward
+ * (chunk loop of X_c @ W^T + liger_cross_entropy_kernel, reduction='none'),
+ * called from none_reduction_losses.py:16-23, with the semantics of
+ * F.linear -> .float() -> F.cross_entropy(reduction='none')
+ * (none_reduction_losses.py:35, TF/loss/loss_utils.py:59).
+ *   loss  fp32 [T] out: lse_t - logit_{t,y_t}; exactly +0.0 at ignored rows
+ *   lse   fp32 [n_valid] out: log-sum-exp of valid row i = row_index[i]
+ *   softcap > 0 applies logits = softcap * tanh(logits / softcap)
+ *           (final_logit_softcapping, none_reduction_losses.py:11,22); 0 = off.
+ */
+int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H,
+                    int64_t V, int64_t ldx, int64_t ldw, int dtype,
+                    float softcap, const int32_t* row_index,
+                    const int32_t* row_label, int64_t n_valid, float* loss,
+                    float* lse, void* workspace, size_t workspace_bytes,
+                    mt_stream_t stream);
+
+/*
+ * Backward blocking plan.  The backward recomputes logit tiles block by
+ * block (chunk_rows valid tokens x chunk_vocab vocabulary entries); this
+ * picks the largest blocks whose workspace fits budget_bytes (0 = default:
+ * 5% of T*V*sizeof(dtype)).  Writes the block shape and workspace size.
+ */
+int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
+                          int dtype, size_t budget_bytes, int64_t* chunk_rows,
+                          int64_t* chunk_vocab, size_t* workspace_bytes);
+
+/*
+ * Backward: dX = G W and dW (+)= G^T X with
+ *   G[t, v] = g_t * (softmax(logits_t)[v] - [v == y_t]) (times the softcap
+ *   derivative when softcap > 0), G = 0 on ignored rows.
+ * Replaces LIGER:ops/fused_linear_cross_entropy.py::fused_linear_cross_entropy_backward
+ * (+ element_mul_kernel), which is exact only for a uniform grad_output;
+ * this one takes a per-token upstream gradient.
+ *   grad_loss    fp32, element t at grad_loss[t * grad_stride] (stride 0 = one
+ *                scalar broadcast to every token, as train.py:102 produces)
+ *   dX           [T, H] (dtype of X, leading dimension lddx) out; rows of
+ *                ignored tokens are written as zeros
+ *   dW           fp32 [V, H] (leading dimension lddw) out;
+ *                accumulate_dW != 0 adds into it, else it is overwritten
+ *   chunk_rows / chunk_vocab / workspace from mt_flce_backward_plan.
+ */
+int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H,
+                     int64_t V, int64_t ldx, int64_t ldw, int dtype,
+                     float softcap, const int32_t* row_index,
+                     const int32_t* row_label, int64_t n_valid,
+                     const float* lse, const float* grad_loss,
+                     int64_t grad_stride, void* dX, int64_t lddx, float* dW,
+                     int64_t lddw, int accumulate_dW, int64_t chunk_rows,
+                     int64_t chunk_vocab, void* workspace,
+                     size_t workspace_bytes, mt_stream_t stream);
+
+/*
+ * Per-sample sums over a packed batch (no counterpart in the reference, which
+ * only sums the whole minibatch at train.py:98; sample boundaries follow the
+ * packed layout of sampler.py:182-188 and the cu_seqlens derivation of
+ * TF/modeling_flash_attention_utils.py:458-481).
+ *   cu_seqlens int32 [S+1], non-decreasing, cu[0] = 0, cu[S] = T
+ *   seg_loss   fp32 [S] out: sum of loss over [cu[s], cu[s+1])
+ *   seg_count  int32 [S] out: number of t in that range with target != ignore_index
+ *   status     int32 [1] out (device): 0, or 1 if cu_seqlens is malformed
+ *              (then seg_loss / seg_count are zero)
+ */
+int mt_segment_sum(const float* loss, const int64_t* target, int64_t T,
+                   int64_t ignore_index, const int32_t* cu_seqlens, int64_t S,
+                   float* seg_loss, int32_t* seg_count, int32_t* status,
+                   mt_stream_t stream);
+
+/*
+ * Cross-entropy over materialised logits, reduction 'none' -- the HF slot of
+ * the reference, hf_fixed_cross_entropy_none_reduction
+ * (none_reduction_losses.py:27-36 -> F.cross_entropy(source, target,
+ * ignore_index, reduction='none') at :35), with source = logits.float()
+ * (TF/loss/loss_utils.py:59).
+ *   logits  [T, V] (dtype: fp32 or bf16, computed in fp32), leading dimension ld
+ *   loss    fp32 [T] out (+0.0 at ignored rows);  lse fp32 [T] out (0 at ignored)
+ *   status  int32 [1] out (device): 1 if some target lies outside [0, V) and is
+ *           not ignore_index (that row then gets loss 0)
+ */
+int mt_ce_forward(const void* logits, int64_t T, int64_t V, int64_t ld, int dtype,
+                  const int64_t* target, int64_t ignore_index, float* loss, float* lse,
+                  int32_t* status, mt_stream_t stream);
+
+/* dlogits[t, v] = g_t * (softmax(logits_t)[v] - [v == y_t]), 0 on ignored rows;
+ * written in the logits dtype with leading dimension ldd. */
+int mt_ce_backward(const void* logits, int64_t T, int64_t V, int64_t ld, int dtype,
+                   const int64_t* target, int64_t ignore_index, const float* lse,
+                   const float* grad_loss, int64_t grad_stride, void* dlogits, int64_t ldd,
+                   mt_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MT_FLCE_H */

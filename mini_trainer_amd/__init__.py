@@ -1,0 +1,29 @@
+"""mini_trainer_amd: MI355X-native (gfx950) fused LM-head linear + per-token
+cross-entropy for mini_trainer-style padding-free training.
+
+The compute lives in libmt_flce.so (hand-written HIP, C ABI in
+include/mt_flce.h); this package is the PyTorch-facing host side.
+"""
+from .flce import (
+    backward_plan,
+    cross_entropy_none,
+    fused_linear_cross_entropy,
+    per_sample_loss_sums,
+    prepare_targets,
+)
+from .none_reduction_losses import (
+    hf_fixed_cross_entropy_none_reduction,
+    liger_fixed_fused_linear_cross_entropy_none_reduction,
+)
+from .utils import patch_target_module
+
+__all__ = [
+    "backward_plan",
+    "cross_entropy_none",
+    "fused_linear_cross_entropy",
+    "per_sample_loss_sums",
+    "prepare_targets",
+    "hf_fixed_cross_entropy_none_reduction",
+    "liger_fixed_fused_linear_cross_entropy_none_reduction",
+    "patch_target_module",
+]

@@ -1,0 +1,494 @@
+// C ABI of libmt_flce.so: argument checking, planning and kernel launches.
+// Declarations and contracts: include/mt_flce.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/mt_flce.h"
+#include "flce_kernels.h"
+
+using namespace mtf;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return MT_OK;
+}
+
+#define MT_TRY(expr)             \
+  do {                           \
+    int _rc = (expr);            \
+    if (_rc != MT_OK) return _rc; \
+  } while (0)
+
+// Planning assumes the MI355X shape (256 CUs) so that the workspace queries
+// are pure functions of the problem size and can run without a device.
+constexpr int64_t kCUs = 256;
+constexpr size_t kAlign = 256;
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
+inline size_t align_up(size_t a) { return (a + kAlign - 1) / kAlign * kAlign; }
+
+int esize_of(int dtype) { return dtype == MT_DTYPE_BF16 ? 2 : (dtype == MT_DTYPE_F32 ? 4 : 0); }
+
+int check_common(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                 int64_t ldw, int dtype, float softcap) {
+  const int es = esize_of(dtype);
+  if (!es) return fail(MT_ERR_INVALID_ARGUMENT, "dtype %d is not MT_DTYPE_F32 or MT_DTYPE_BF16", dtype);
+  if (T < 0 || T > INT32_MAX) return fail(MT_ERR_INVALID_ARGUMENT, "T=%lld out of range", (long long)T);
+  if (V <= 0 || V > INT32_MAX) return fail(MT_ERR_INVALID_ARGUMENT, "V=%lld out of range", (long long)V);
+  if (H <= 0 || H > INT32_MAX) return fail(MT_ERR_INVALID_ARGUMENT, "H=%lld out of range", (long long)H);
+  const int64_t hmul = dtype == MT_DTYPE_BF16 ? 64 : 32;
+  if (H % hmul != 0)
+    return fail(MT_ERR_UNSUPPORTED, "H=%lld must be a multiple of %lld", (long long)H, (long long)hmul);
+  if (ldx < H || ldw < H)
+    return fail(MT_ERR_INVALID_ARGUMENT, "leading dimensions (ldx=%lld, ldw=%lld) must be >= H=%lld",
+                (long long)ldx, (long long)ldw, (long long)H);
+  if ((ldx * es) % 16 != 0 || (ldw * es) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "row pitches must be multiples of 16 bytes");
+  if (!W || (T > 0 && !X)) return fail(MT_ERR_INVALID_ARGUMENT, "null X or W");
+  if ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(W)) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "X and W must be 16-byte aligned");
+  if (!(softcap >= 0.f)) return fail(MT_ERR_INVALID_ARGUMENT, "softcap must be >= 0 (0 = off)");
+  return MT_OK;
+}
+
+// ---------------------------------------------------------------- forward
+struct FwdPlan {
+  int64_t tiles_m = 0, vt_total = 0, per = 0, splits = 0;
+};
+
+FwdPlan plan_forward(int64_t n_valid, int64_t V) {
+  FwdPlan p;
+  p.tiles_m = cdiv(n_valid, 256);
+  p.vt_total = cdiv(V, 256);
+  if (p.tiles_m == 0) return p;
+  int64_t best_cost = INT64_MAX, best_s = 1;
+  for (int64_t s = 1; s <= std::min<int64_t>(p.vt_total, 64); ++s) {
+    const int64_t per = cdiv(p.vt_total, s);
+    const int64_t s_eff = cdiv(p.vt_total, per);
+    const int64_t cost = cdiv(p.tiles_m * s_eff, kCUs) * per;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best_s = s_eff;
+    }
+  }
+  p.per = cdiv(p.vt_total, best_s);
+  p.splits = cdiv(p.vt_total, p.per);
+  return p;
+}
+
+size_t forward_ws(const FwdPlan& p, int64_t n_valid) {
+  return align_up((size_t)p.splits * n_valid * 2 * sizeof(float)) +
+         align_up((size_t)n_valid * sizeof(float));
+}
+
+// --------------------------------------------------------------- backward
+size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es) {
+  if (C == 0) return 0;
+  size_t g = align_up((size_t)C * Cv * es);
+  size_t acc = Cv < V ? align_up((size_t)C * H * sizeof(float)) : 0;
+  size_t xt = align_up((size_t)H * C * es);
+  return g + acc + xt;
+}
+
+// Modelled seconds for one backward with blocks of C x Cv.
+double backward_cost(int64_t N, int64_t H, int64_t V, int64_t C, int64_t Cv) {
+  const double tile_rate = 2.5e15 / kCUs * 0.7;  // flop/s of one CU
+  const double launch = 8e-6, bw = 5e12;
+  double t = 0, bytes = 0;
+  for (int64_t c0 = 0; c0 < N; c0 += C) {
+    const int64_t cn = std::min(C, N - c0);
+    const int64_t nv = cdiv(V, Cv);
+    for (int64_t v0 = 0; v0 < V; v0 += Cv) {
+      const int64_t cv = std::min(Cv, V - v0);
+      const double tile_flops_re = 2.0 * 256 * 256 * H;
+      const double tile_flops_dx = 2.0 * 256 * 256 * round_up(cv, 64);
+      const double tile_flops_dw = 2.0 * 256 * 256 * round_up(cn, 64);
+      t += cdiv(cdiv(cn, 256) * cdiv(cv, 256), kCUs) * tile_flops_re / tile_rate;
+      t += cdiv(cdiv(cn, 256) * cdiv(H, 256), kCUs) * tile_flops_dx / tile_rate;
+      t += cdiv(cdiv(cv, 256) * cdiv(H, 256), kCUs) * tile_flops_dw / tile_rate;
+      t += 3 * launch;
+    }
+    bytes += (double)V * H * 8;                        // dW read-modify-write
+    if (nv > 1) bytes += (double)(2 * nv - 2) * cn * H * 4;  // dX accumulator
+    t += launch;
+  }
+  return t + 0.5 * bytes / bw;
+}
+
+struct BwdPlan {
+  int64_t C = 0, Cv = 0;
+  size_t ws = 0;
+};
+
+BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t budget) {
+  BwdPlan best;
+  if (N <= 0) return best;
+  if (budget == 0) budget = (size_t)((double)T * V * es * 0.05);
+  double best_cost = 1e300;
+  BwdPlan smallest;
+  smallest.C = 256;
+  smallest.Cv = 256;
+  smallest.ws = backward_ws(256, 256, H, V, es);
+  const int64_t max_nt = std::min<int64_t>(cdiv(N, 256), 128);
+  const int64_t max_nv = std::min<int64_t>(cdiv(V, 256), 128);
+  for (int64_t nt = 1; nt <= max_nt; ++nt) {
+    const int64_t C = round_up(cdiv(N, nt), 256);
+    for (int64_t nv = 1; nv <= max_nv; ++nv) {
+      const int64_t Cv = round_up(cdiv(V, nv), 256);
+      const size_t ws = backward_ws(C, Cv, H, V, es);
+      if (ws > budget) continue;
+      const double cost = backward_cost(N, H, V, C, Cv);
+      if (cost < best_cost * 0.999) {
+        best_cost = cost;
+        best.C = C;
+        best.Cv = Cv;
+        best.ws = ws;
+      }
+      break;  // larger nv only shrinks blocks further
+    }
+  }
+  return best.C ? best : smallest;
+}
+
+template <typename T>
+int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx, int64_t ldw,
+                   float softcap, const int32_t* row_index, const int32_t* row_label,
+                   int64_t n_valid, float* loss, float* lse, const FwdPlan& p, char* ws,
+                   hipStream_t stream) {
+  constexpr int es = sizeof(T);
+  FwdArgs a;
+  a.X = static_cast<const char*>(X);
+  a.W = static_cast<const char*>(W);
+  a.ldx_b = ldx * es;
+  a.ldw_b = ldw * es;
+  a.H = (int32_t)H;
+  a.V = (int32_t)V;
+  a.N = (int32_t)n_valid;
+  a.row_index = row_index;
+  a.row_label = row_label;
+  a.softcap = softcap;
+  a.tiles_m = (int32_t)p.tiles_m;
+  a.splits = (int32_t)p.splits;
+  a.vt_total = (int32_t)p.vt_total;
+  a.vt_per_split = (int32_t)p.per;
+  a.part = reinterpret_cast<float*>(ws);
+  a.xy = reinterpret_cast<float*>(ws + align_up((size_t)p.splits * n_valid * 2 * sizeof(float)));
+  hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
+                     stream, a);
+  MT_TRY(check_launch("fwd_kernel"));
+  hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(n_valid, 256)), dim3(256), 0, stream,
+                     a.part, a.xy, a.N, a.splits, row_index, loss, lse);
+  return check_launch("fwd_finalize_kernel");
+}
+
+template <typename T>
+int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx, int64_t ldw,
+                    float softcap, const int32_t* row_index, const int32_t* row_label,
+                    int64_t N, const float* lse, const float* grad, int64_t gstride, void* dX,
+                    int64_t lddx, float* dW, int64_t lddw, int accumulate, int64_t C, int64_t Cv,
+                    char* ws, hipStream_t stream) {
+  constexpr int es = sizeof(T);
+  const int64_t nv = cdiv(V, Cv);
+  char* G = ws;
+  float* accbuf = nv > 1 ? reinterpret_cast<float*>(ws + align_up((size_t)C * Cv * es)) : nullptr;
+  char* XcT = ws + align_up((size_t)C * Cv * es) +
+              (nv > 1 ? align_up((size_t)C * H * sizeof(float)) : 0);
+  const int64_t ldg_b = Cv * es, ldxt_b = C * es;
+
+  for (int64_t c0 = 0; c0 < N; c0 += C) {
+    const int64_t cn = std::min(C, N - c0);
+    const int64_t cn_pad = round_up(cn, 256);
+    hipLaunchKernelGGL(gather_t_kernel<T>, dim3((uint32_t)(cn_pad / 64), (uint32_t)cdiv(H, 64)),
+                       dim3(256), 0, stream, static_cast<const char*>(X), ldx * es, row_index + c0,
+                       (int32_t)cn, (int32_t)H, XcT, ldxt_b);
+    MT_TRY(check_launch("gather_t_kernel"));
+    int64_t j = 0;
+    for (int64_t v0 = 0; v0 < V; v0 += Cv, ++j) {
+      const int64_t cv = std::min(Cv, V - v0);
+      RecompArgs r;
+      r.X = static_cast<const char*>(X);
+      r.W = static_cast<const char*>(W);
+      r.ldx_b = ldx * es;
+      r.ldw_b = ldw * es;
+      r.H = (int32_t)H;
+      r.V = (int32_t)V;
+      r.row_index = row_index + c0;
+      r.row_label = row_label + c0;
+      r.lse = lse + c0;
+      r.Cn = (int32_t)cn;
+      r.grad = grad;
+      r.gstride = gstride;
+      r.softcap = softcap;
+      r.v0 = (int32_t)v0;
+      r.cv = (int32_t)cv;
+      r.G = G;
+      r.ldg_b = ldg_b;
+      r.tiles_m = (int32_t)cdiv(cn, 256);
+      r.tiles_n = (int32_t)cdiv(cv, 256);
+      hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)), dim3(kThreads),
+                         0, stream, r);
+      MT_TRY(check_launch("recompute_kernel"));
+
+      DxArgs x;
+      x.G = G;
+      x.ldg_b = ldg_b;
+      x.W = static_cast<const char*>(W);
+      x.ldw_b = ldw * es;
+      x.V = (int32_t)V;
+      x.v0 = (int32_t)v0;
+      x.kv = (int32_t)cv;
+      x.H = (int32_t)H;
+      x.Cn = (int32_t)cn;
+      x.accbuf = accbuf;
+      x.ld_acc = H;
+      x.mode = nv == 1 ? kDxEmit : (j == 0 ? kDxStore : (j == nv - 1 ? kDxAddEmit : kDxAdd));
+      x.dX = static_cast<char*>(dX);
+      x.lddx_b = lddx * es;
+      x.row_index = row_index + c0;
+      x.tiles_m = (int32_t)cdiv(cn, 256);
+      x.tiles_n = (int32_t)cdiv(H, 256);
+      hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
+                         stream, x);
+      MT_TRY(check_launch("dx_kernel"));
+
+      DwArgs w;
+      w.G = G;
+      w.ldg_b = ldg_b;
+      w.g_rows = (int32_t)cn_pad;
+      w.g_cols = (int32_t)Cv;
+      w.XcT = XcT;
+      w.ldxt_b = ldxt_b;
+      w.kt_rows = (int32_t)cn;
+      w.H = (int32_t)H;
+      w.cv = (int32_t)cv;
+      w.v0 = (int32_t)v0;
+      w.dW = dW;
+      w.lddw = lddw;
+      w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
+      w.tiles_m = (int32_t)cdiv(cv, 256);
+      w.tiles_n = (int32_t)cdiv(H, 256);
+      hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
+                         stream, w);
+      MT_TRY(check_launch("dw_kernel"));
+    }
+  }
+  return MT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_flce_abi_version(void) { return MT_FLCE_ABI_VERSION; }
+
+const char* mt_flce_last_error(void) { return g_last_error.c_str(); }
+
+int mt_flce_prepare(const int64_t* labels, int64_t T, int64_t V, int64_t ignore_index, int shift,
+                    int32_t* row_index, int32_t* row_label, int32_t* counts, mt_stream_t stream) {
+  if (T < 0 || T > INT32_MAX) return fail(MT_ERR_INVALID_ARGUMENT, "T=%lld out of range", (long long)T);
+  if (V <= 0 || V > INT32_MAX) return fail(MT_ERR_INVALID_ARGUMENT, "V=%lld out of range", (long long)V);
+  if (!counts || (T > 0 && (!labels || !row_index || !row_label)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipLaunchKernelGGL(prepare_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, labels, T, V,
+                     ignore_index, shift, row_index, row_label, counts);
+  return check_launch("prepare_kernel");
+}
+
+size_t mt_flce_forward_workspace_bytes(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype) {
+  (void)T;
+  (void)H;
+  (void)dtype;
+  if (n_valid <= 0 || V <= 0) return 0;
+  return forward_ws(plan_forward(n_valid, V), n_valid);
+}
+
+int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                    int64_t ldw, int dtype, float softcap, const int32_t* row_index,
+                    const int32_t* row_label, int64_t n_valid, float* loss, float* lse,
+                    void* workspace, size_t workspace_bytes, mt_stream_t stream) {
+  MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
+  if (n_valid < 0 || n_valid > T)
+    return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
+  if (T == 0) return MT_OK;
+  if (!row_index || !loss || (n_valid > 0 && (!row_label || !lse)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const FwdPlan p = plan_forward(n_valid, V);
+  const size_t need = n_valid > 0 ? forward_ws(p, n_valid) : 0;
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(MT_ERR_WORKSPACE_TOO_SMALL, "forward workspace %zu bytes < required %zu",
+                workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (T - n_valid > 0) {
+    const int64_t n0 = T - n_valid;
+    hipLaunchKernelGGL(zero_scatter_f32_kernel, dim3((uint32_t)std::min<int64_t>(cdiv(n0, 256), 4096)),
+                       dim3(256), 0, s, loss, row_index + n_valid, n0);
+    MT_TRY(check_launch("zero_scatter_f32_kernel"));
+  }
+  if (n_valid == 0) return MT_OK;
+  if (dtype == MT_DTYPE_BF16)
+    return launch_forward<__bf16>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid,
+                                  loss, lse, p, static_cast<char*>(workspace), s);
+  return launch_forward<float>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, loss,
+                               lse, p, static_cast<char*>(workspace), s);
+}
+
+int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
+                          size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
+                          size_t* workspace_bytes) {
+  const int es = esize_of(dtype);
+  if (!es) return fail(MT_ERR_INVALID_ARGUMENT, "dtype %d is not MT_DTYPE_F32 or MT_DTYPE_BF16", dtype);
+  if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld n_valid=%lld H=%lld V=%lld", (long long)T,
+                (long long)n_valid, (long long)H, (long long)V);
+  if (!chunk_rows || !chunk_vocab || !workspace_bytes)
+    return fail(MT_ERR_INVALID_ARGUMENT, "null output pointer");
+  const BwdPlan p = plan_backward(T, n_valid, H, V, es, budget_bytes);
+  *chunk_rows = p.C;
+  *chunk_vocab = p.Cv;
+  *workspace_bytes = p.ws;
+  return MT_OK;
+}
+
+int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                     int64_t ldw, int dtype, float softcap, const int32_t* row_index,
+                     const int32_t* row_label, int64_t n_valid, const float* lse,
+                     const float* grad_loss, int64_t grad_stride, void* dX, int64_t lddx, float* dW,
+                     int64_t lddw, int accumulate_dW, int64_t chunk_rows, int64_t chunk_vocab,
+                     void* workspace, size_t workspace_bytes, mt_stream_t stream) {
+  MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
+  const int es = esize_of(dtype);
+  if (n_valid < 0 || n_valid > T)
+    return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
+  if (lddx < H || lddw < H)
+    return fail(MT_ERR_INVALID_ARGUMENT, "lddx=%lld / lddw=%lld must be >= H", (long long)lddx, (long long)lddw);
+  if ((lddx * es) % 16 != 0 || (lddw * 4) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dX / dW row pitches must be multiples of 16 bytes");
+  if (grad_stride < 0) return fail(MT_ERR_INVALID_ARGUMENT, "grad_stride must be >= 0");
+  if (!dW || (T > 0 && (!dX || !row_index)) ||
+      (n_valid > 0 && (!row_label || !lse || !grad_loss)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if ((reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(dW) |
+       reinterpret_cast<uintptr_t>(workspace)) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dX, dW and workspace must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (T - n_valid > 0) {
+    hipLaunchKernelGGL(zero_rows_kernel, dim3((uint32_t)std::min<int64_t>(T - n_valid, 8192)), dim3(256),
+                       0, s, static_cast<char*>(dX), lddx * es, row_index + n_valid, T - n_valid,
+                       H * es);
+    MT_TRY(check_launch("zero_rows_kernel"));
+  }
+  if (n_valid == 0) {
+    if (!accumulate_dW) {
+      hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
+                         s, dW, V, H, lddw);
+      MT_TRY(check_launch("zero_matrix_f32_kernel"));
+    }
+    return MT_OK;
+  }
+  if (chunk_rows <= 0 || chunk_rows % 256 != 0 || chunk_vocab <= 0 || chunk_vocab % 256 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "chunk_rows=%lld / chunk_vocab=%lld must be positive multiples of 256",
+                (long long)chunk_rows, (long long)chunk_vocab);
+  const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es);
+  if (workspace_bytes < need || !workspace)
+    return fail(MT_ERR_WORKSPACE_TOO_SMALL, "backward workspace %zu bytes < required %zu",
+                workspace_bytes, need);
+  if (dtype == MT_DTYPE_BF16)
+    return launch_backward<__bf16>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
+                                   grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW,
+                                   chunk_rows, chunk_vocab, static_cast<char*>(workspace), s);
+  return launch_backward<float>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
+                                grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, chunk_rows,
+                                chunk_vocab, static_cast<char*>(workspace), s);
+}
+
+int mt_segment_sum(const float* loss, const int64_t* target, int64_t T, int64_t ignore_index,
+                   const int32_t* cu_seqlens, int64_t S, float* seg_loss, int32_t* seg_count,
+                   int32_t* status, mt_stream_t stream) {
+  if (T < 0 || T > INT32_MAX || S < 0 || S > INT32_MAX)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld S=%lld", (long long)T, (long long)S);
+  if (!cu_seqlens || !status || (S > 0 && (!seg_loss || !seg_count)) || (T > 0 && (!loss || !target)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(segment_check_kernel, dim3(1), dim3(256), 0, s, cu_seqlens, S, T, status);
+  MT_TRY(check_launch("segment_check_kernel"));
+  if (S == 0) return MT_OK;
+  hipLaunchKernelGGL(segment_sum_kernel, dim3((uint32_t)S), dim3(256), 0, s, loss, target,
+                     ignore_index, cu_seqlens, status, seg_loss, seg_count);
+  return check_launch("segment_sum_kernel");
+}
+
+int mt_ce_forward(const void* logits, int64_t T, int64_t V, int64_t ld, int dtype,
+                  const int64_t* target, int64_t ignore_index, float* loss, float* lse,
+                  int32_t* status, mt_stream_t stream) {
+  const int es = esize_of(dtype);
+  if (!es) return fail(MT_ERR_INVALID_ARGUMENT, "dtype %d is not MT_DTYPE_F32 or MT_DTYPE_BF16", dtype);
+  if (T < 0 || T > INT32_MAX || V <= 0 || V > INT32_MAX || ld < V)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld V=%lld ld=%lld", (long long)T, (long long)V,
+                (long long)ld);
+  if ((ld * es) % 16 != 0 || reinterpret_cast<uintptr_t>(logits) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "logits rows must be 16-byte aligned");
+  if (!status || (T > 0 && (!logits || !target || !loss || !lse)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, status, 0);
+  if (T == 0) return check_launch("set_i32_kernel");
+  if (dtype == MT_DTYPE_BF16)
+    hipLaunchKernelGGL(ce_forward_kernel<__bf16>, dim3((uint32_t)T), dim3(256), 0, s,
+                       static_cast<const char*>(logits), V, ld * es, target, ignore_index, loss, lse,
+                       status);
+  else
+    hipLaunchKernelGGL(ce_forward_kernel<float>, dim3((uint32_t)T), dim3(256), 0, s,
+                       static_cast<const char*>(logits), V, ld * es, target, ignore_index, loss, lse,
+                       status);
+  return check_launch("ce_forward_kernel");
+}
+
+int mt_ce_backward(const void* logits, int64_t T, int64_t V, int64_t ld, int dtype,
+                   const int64_t* target, int64_t ignore_index, const float* lse,
+                   const float* grad_loss, int64_t grad_stride, void* dlogits, int64_t ldd,
+                   mt_stream_t stream) {
+  const int es = esize_of(dtype);
+  if (!es) return fail(MT_ERR_INVALID_ARGUMENT, "dtype %d is not MT_DTYPE_F32 or MT_DTYPE_BF16", dtype);
+  if (T < 0 || T > INT32_MAX || V <= 0 || V > INT32_MAX || ld < V || ldd < V || grad_stride < 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld V=%lld ld=%lld ldd=%lld", (long long)T,
+                (long long)V, (long long)ld, (long long)ldd);
+  if ((ldd * es) % 4 != 0 || reinterpret_cast<uintptr_t>(dlogits) % 4 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dlogits rows must be 4-byte aligned");
+  if (T == 0) return MT_OK;
+  if (!logits || !target || !lse || !grad_loss || !dlogits)
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == MT_DTYPE_BF16)
+    hipLaunchKernelGGL(ce_backward_kernel<__bf16>, dim3((uint32_t)T), dim3(256), 0, s,
+                       static_cast<const char*>(logits), V, ld * es, target, ignore_index, lse,
+                       grad_loss, grad_stride, static_cast<char*>(dlogits), ldd * es);
+  else
+    hipLaunchKernelGGL(ce_backward_kernel<float>, dim3((uint32_t)T), dim3(256), 0, s,
+                       static_cast<const char*>(logits), V, ld * es, target, ignore_index, lse,
+                       grad_loss, grad_stride, static_cast<char*>(dlogits), ldd * es);
+  return check_launch("ce_backward_kernel");
+}
+
+}  // extern "C"

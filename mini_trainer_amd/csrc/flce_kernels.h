@@ -1,0 +1,785 @@
+// Kernels of the fused LM-head linear + per-token cross-entropy path.
+//
+//   fwd_kernel       logits tile = X_rows . W_tile^T (MFMA), fused online
+//                    log-sum-exp over the vocabulary and label-logit capture;
+//                    no logits are written to memory.
+//   fwd_finalize     merge of the per-split (max, sum) partials -> lse, loss.
+//   recompute_kernel logits tile recomputed and turned into
+//                    G = g * (softmax - onehot) (bf16 / fp32) for one block.
+//   dx_kernel        dX_block (+)= G . W_block    (W consumed K-major)
+//   dw_kernel        dW_block (+)= G^T . X_block  (G consumed K-major)
+//   small kernels    valid-row compaction, gather-transpose of X rows,
+//                    zeroing of ignored rows, per-sample segment sums.
+#pragma once
+
+#include "flce_gemm.h"
+
+namespace mtf {
+
+#define MT_GEMM_KERNEL \
+  __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+
+struct EpiCoords {
+  uint32_t lane, wm, wn;
+  __device__ __forceinline__ EpiCoords() {
+    lane = lane_id();
+    uint32_t w = wave_id();
+    wm = w >> 1;
+    wn = w & 1u;
+  }
+  // Tile-local output row of fragment row fm held by this lane.
+  __device__ __forceinline__ int row(int fm) const { return wm * 128 + fm * 16 + (lane & 15u); }
+  // Tile-local output column of element 0 of fragment column fn.
+  __device__ __forceinline__ int col(int fn) const { return wn * 128 + fn * 16 + 4 * (lane >> 4); }
+};
+
+// Is column offset `rel` (label column minus this lane's column of fn = 0,
+// r = 0) one of the 32 columns this lane holds?
+__device__ __forceinline__ bool lane_holds(int rel) {
+  return rel >= 0 && rel < 128 && (rel & 12) == 0;
+}
+
+// ===========================================================================
+// Forward
+// ===========================================================================
+struct FwdArgs {
+  const char* X;
+  const char* W;
+  int64_t ldx_b, ldw_b;
+  int32_t H, V, N;
+  const int32_t* row_index;
+  const int32_t* row_label;
+  float softcap;
+  int32_t tiles_m, splits, vt_total, vt_per_split;
+  float* part;  // [splits][N][2] = (max in log2 units, scaled sum)
+  float* xy;    // [N] label logit
+};
+
+template <typename T, bool kTail, bool kCap>
+__device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][8], float (&m2)[8],
+                                                  float (&d)[8], const int32_t (&rel)[8],
+                                                  const int32_t (&rglob)[8], int32_t ncol0,
+                                                  const FwdArgs& a, bool any_hit) {
+  const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    float v[8][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[fn][r] = acc[fm][fn][r];
+      round_pair<T>(v[fn][0], v[fn][1]);
+      round_pair<T>(v[fn][2], v[fn][3]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = v[fn][r];
+        if (kCap) x = cap * tanh_approx(x * inv_cap);
+        if (kTail && ncol0 + fn * 16 + r >= a.V) x = -INFINITY;
+        v[fn][r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    }
+    const float mn = fmaxf(m2[fm], tmax * kLog2e);
+    float s = 0.f;
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s += fast_exp2(fmaf(v[fn][r], kLog2e, -mn));
+    d[fm] = fmaf(d[fm], fast_exp2(m2[fm] - mn), s);
+    m2[fm] = mn;
+    if (any_hit) {
+      const int rl = rel[fm];
+      if (lane_holds(rl) && rglob[fm] < a.N) {
+        float hitv = 0.f;
+#pragma unroll
+        for (int fn = 0; fn < 8; ++fn)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) hitv = (rl == fn * 16 + r) ? v[fn][r] : hitv;
+        a.xy[rglob[fm]] = hitv;
+      }
+    }
+  }
+}
+
+template <typename T>
+MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  uint32_t tm, ts;
+  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.splits, 4, tm, ts);
+  const EpiCoords ec;
+  FragOffsets fo;
+  fo.init();
+
+  const int32_t row0 = (int32_t)tm * 256;
+  DirectLoader la;
+  la.init([&](uint32_t r) {
+    int32_t rr = row0 + (int32_t)r;
+    rr = rr < a.N ? rr : a.N - 1;
+    return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
+  });
+
+  int32_t lbl[8], rglob[8];
+  float m2[8], d[8];
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    rglob[fm] = row0 + ec.row(fm);
+    lbl[fm] = rglob[fm] < a.N ? a.row_label[rglob[fm]] : -1;
+    m2[fm] = kNegBig;
+    d[fm] = 0.f;
+  }
+
+  const int KT = a.H / Elt<T>::kBK;
+  const int vt0 = (int)ts * a.vt_per_split;
+  const int vt1 = min(vt0 + a.vt_per_split, a.vt_total);
+  f32x4_t acc[8][8];
+  for (int vt = vt0; vt < vt1; ++vt) {
+    const int32_t vrow0 = vt * 256;
+    DirectLoader lb;
+    lb.init([&](uint32_t r) {
+      int32_t v = vrow0 + (int32_t)r;
+      v = v < a.V ? v : a.V - 1;
+      return a.W + (int64_t)v * a.ldw_b;
+    });
+    mainloop<T>(lds, acc, la, lb, KT, fo);
+
+    const int32_t ncol0 = vrow0 + ec.col(0);
+    int32_t rel[8];
+    bool hit = false;
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+      rel[fm] = lbl[fm] - ncol0;
+      hit |= lane_holds(rel[fm]);
+    }
+    const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
+    const bool tail = vrow0 + 256 > a.V;
+    if (a.softcap > 0.f) {
+      if (tail) fwd_tile_epilogue<T, true, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
+      else fwd_tile_epilogue<T, false, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
+    } else {
+      if (tail) fwd_tile_epilogue<T, true, false>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
+      else fwd_tile_epilogue<T, false, false>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
+    }
+  }
+
+  // Merge the four lanes that share a row, then the two waves (wn = 0, 1).
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    lse_merge(m2[fm], d[fm], __shfl_xor(m2[fm], 16), __shfl_xor(d[fm], 16));
+    lse_merge(m2[fm], d[fm], __shfl_xor(m2[fm], 32), __shfl_xor(d[fm], 32));
+  }
+  float* red = reinterpret_cast<float*>(lds);
+  __syncthreads();
+  if (ec.wn == 1 && (ec.lane >> 4) == 0) {
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+      red[ec.row(fm) * 2 + 0] = m2[fm];
+      red[ec.row(fm) * 2 + 1] = d[fm];
+    }
+  }
+  __syncthreads();
+  if (ec.wn == 0 && (ec.lane >> 4) == 0) {
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+      lse_merge(m2[fm], d[fm], red[ec.row(fm) * 2 + 0], red[ec.row(fm) * 2 + 1]);
+      if (rglob[fm] < a.N) {
+        int64_t o = ((int64_t)ts * a.N + rglob[fm]) * 2;
+        a.part[o + 0] = m2[fm];
+        a.part[o + 1] = d[fm];
+      }
+    }
+  }
+}
+
+__global__ void fwd_finalize_kernel(const float* part, const float* xy, int32_t N, int32_t splits,
+                                    const int32_t* row_index, float* loss, float* lse) {
+  int32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= N) return;
+  float m = kNegBig, d = 0.f;
+  for (int s = 0; s < splits; ++s) {
+    int64_t o = ((int64_t)s * N + r) * 2;
+    lse_merge(m, d, part[o], part[o + 1]);
+  }
+  const float L = (m + fast_log2(d)) * kLn2;
+  lse[r] = L;
+  loss[row_index[r]] = L - xy[r];
+}
+
+// ===========================================================================
+// Backward, step 1: G = g * (softmax(logits) - onehot) for one block.
+// ===========================================================================
+struct RecompArgs {
+  const char* X;
+  const char* W;
+  int64_t ldx_b, ldw_b;
+  int32_t H, V;
+  const int32_t* row_index;  // offset to the block's first valid row
+  const int32_t* row_label;
+  const float* lse;
+  int32_t Cn;  // valid rows in the block
+  const float* grad;
+  int64_t gstride;
+  float softcap;
+  int32_t v0, cv;  // vocabulary range [v0, v0 + cv)
+  char* G;         // [tiles_m * 256][>= tiles_n * 256], row pitch ldg_b
+  int64_t ldg_b;
+  int32_t tiles_m, tiles_n;
+};
+
+template <typename T>
+__device__ __forceinline__ void store4(char* p, const float (&o)[4]);
+template <>
+__device__ __forceinline__ void store4<__bf16>(char* p, const float (&o)[4]) {
+  u32x2_t w;
+  w.x = pack_bf16x2(o[0], o[1]);
+  w.y = pack_bf16x2(o[2], o[3]);
+  *reinterpret_cast<u32x2_t*>(p) = w;
+}
+template <>
+__device__ __forceinline__ void store4<float>(char* p, const float (&o)[4]) {
+  *reinterpret_cast<f32x4_t*>(p) = f32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+template <typename T, bool kCap>
+__device__ __forceinline__ void recompute_epilogue(const f32x4_t (&acc)[8][8], const RecompArgs& a,
+                                                   const EpiCoords& ec, uint32_t tm, uint32_t tn) {
+  const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
+  const int32_t ncol0 = (int32_t)tn * 256 + ec.col(0);  // block-local column of fn = 0, r = 0
+  int32_t rel[8], rowl[8];
+  float lse2[8], g[8];
+  bool hit = false;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    rowl[fm] = (int32_t)tm * 256 + ec.row(fm);
+    const bool rv = rowl[fm] < a.Cn;
+    const int32_t rr = rv ? rowl[fm] : 0;
+    lse2[fm] = a.lse[rr] * kLog2e;
+    g[fm] = rv ? a.grad[(int64_t)a.row_index[rr] * a.gstride] : 0.f;
+    rel[fm] = rv ? a.row_label[rr] - a.v0 - ncol0 : -1;
+    hit |= lane_holds(rel[fm]);
+  }
+  const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const bool rv = rowl[fm] < a.Cn;
+    char* grow = a.G + (int64_t)rowl[fm] * a.ldg_b;
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+      float o[4];
+      float xr[4] ={acc[fm][fn][0], acc[fm][fn][1], acc[fm][fn][2], acc[fm][fn][3]};
+      round_pair<T>(xr[0], xr[1]);
+      round_pair<T>(xr[2], xr[3]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = xr[r];
+        float dcap = 1.f;
+        if (kCap) {
+          const float t = tanh_approx(x * inv_cap);
+          x = cap * t;
+          dcap = 1.f - t * t;
+        }
+        float p = fast_exp2(fmaf(x, kLog2e, -lse2[fm]));
+        if (any_hit) p -= (rel[fm] == fn * 16 + r) ? 1.f : 0.f;
+        const bool ok = rv && (ncol0 + fn * 16 + r < a.cv);
+        o[r] = ok ? p * g[fm] * dcap : 0.f;
+      }
+      store4<T>(grow + (int64_t)(ncol0 + fn * 16) * Elt<T>::kBytes, o);
+    }
+  }
+}
+
+template <typename T>
+MT_GEMM_KERNEL void recompute_kernel(RecompArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  uint32_t tm, tn;
+  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
+  const EpiCoords ec;
+  FragOffsets fo;
+  fo.init();
+  const int32_t row0 = (int32_t)tm * 256;
+  DirectLoader la;
+  la.init([&](uint32_t r) {
+    int32_t rr = row0 + (int32_t)r;
+    rr = rr < a.Cn ? rr : a.Cn - 1;
+    return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
+  });
+  const int32_t vrow0 = a.v0 + (int32_t)tn * 256;
+  DirectLoader lb;
+  lb.init([&](uint32_t r) {
+    int32_t v = vrow0 + (int32_t)r;
+    v = v < a.V ? v : a.V - 1;
+    return a.W + (int64_t)v * a.ldw_b;
+  });
+  f32x4_t acc[8][8];
+  mainloop<T>(lds, acc, la, lb, a.H / Elt<T>::kBK, fo);
+  if (a.softcap > 0.f) recompute_epilogue<T, true>(acc, a, ec, tm, tn);
+  else recompute_epilogue<T, false>(acc, a, ec, tm, tn);
+}
+
+// ===========================================================================
+// Backward, step 2: dX rows of the block (+)= G . W[v0 : v0 + cv]
+// ===========================================================================
+enum DxMode : int32_t { kDxStore = 0, kDxAdd = 1, kDxAddEmit = 2, kDxEmit = 3 };
+
+struct DxArgs {
+  const char* G;
+  int64_t ldg_b;
+  const char* W;
+  int64_t ldw_b;
+  int32_t V, v0, kv;  // K = vocabulary entries v0 .. v0 + kv
+  int32_t H, Cn;
+  float* accbuf;  // fp32 [>= Cn][ld_acc]
+  int64_t ld_acc;
+  int32_t mode;
+  char* dX;
+  int64_t lddx_b;
+  const int32_t* row_index;  // offset to the block's first valid row
+  int32_t tiles_m, tiles_n;
+};
+
+template <typename T>
+MT_GEMM_KERNEL void dx_kernel(DxArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  uint32_t tm, tn;
+  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
+  const EpiCoords ec;
+  FragOffsets fo;
+  fo.init();
+  const int32_t row0 = (int32_t)tm * 256;
+  DirectLoader la;
+  la.init([&](uint32_t r) { return a.G + (int64_t)(row0 + (int32_t)r) * a.ldg_b; });
+  const int32_t h0 = (int32_t)tn * 256;
+  TransLoader<T> lb;
+  lb.init(a.W + (int64_t)a.v0 * a.ldw_b + (int64_t)h0 * Elt<T>::kBytes, a.ldw_b, a.V - a.v0,
+          a.H - h0);
+  f32x4_t acc[8][8];
+  const int KT = (a.kv + Elt<T>::kBK - 1) / Elt<T>::kBK;
+  mainloop<T>(lds, acc, la, lb, KT, fo);
+
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const int32_t rowl = row0 + ec.row(fm);
+    if (rowl >= a.Cn) continue;
+    float* arow = a.accbuf + (int64_t)rowl * a.ld_acc;
+    char* xrow = a.dX + (int64_t)a.row_index[rowl] * a.lddx_b;
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+      const int32_t h = h0 + ec.col(fn);
+      if (h >= a.H) continue;
+      f32x4_t v = acc[fm][fn];
+      if (a.mode == kDxStore) {
+        *reinterpret_cast<f32x4_t*>(arow + h) = v;
+      } else if (a.mode == kDxAdd) {
+        v += *reinterpret_cast<const f32x4_t*>(arow + h);
+        *reinterpret_cast<f32x4_t*>(arow + h) = v;
+      } else {
+        if (a.mode == kDxAddEmit) v += *reinterpret_cast<const f32x4_t*>(arow + h);
+        const float o[4] = {v[0], v[1], v[2], v[3]};
+        store4<T>(xrow + (int64_t)h * Elt<T>::kBytes, o);
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// Backward, step 3: dW[v0 : v0 + cv] (+)= G^T . X_block
+// ===========================================================================
+struct DwArgs {
+  const char* G;  // [K = tokens][vocab], row pitch ldg_b
+  int64_t ldg_b;
+  int32_t g_rows;  // rows of G that exist (>= K rounded up to the K slab)
+  int32_t g_cols;  // columns of G that exist
+  const char* XcT;  // [H][K] gathered + transposed X rows of the block
+  int64_t ldxt_b;
+  int32_t kt_rows;  // K extent (valid rows of the block)
+  int32_t H, cv, v0;
+  float* dW;
+  int64_t lddw;
+  int32_t accumulate;
+  int32_t tiles_m, tiles_n;
+};
+
+template <typename T>
+MT_GEMM_KERNEL void dw_kernel(DwArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  uint32_t tm, tn;
+  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
+  const EpiCoords ec;
+  FragOffsets fo;
+  fo.init();
+  const int32_t m0 = (int32_t)tm * 256;
+  TransLoader<T> la;
+  la.init(a.G + (int64_t)m0 * Elt<T>::kBytes, a.ldg_b, a.g_rows, a.g_cols - m0);
+  const int32_t h0 = (int32_t)tn * 256;
+  DirectLoader lb;
+  lb.init([&](uint32_t r) {
+    int32_t h = h0 + (int32_t)r;
+    h = h < a.H ? h : a.H - 1;
+    return a.XcT + (int64_t)h * a.ldxt_b;
+  });
+  f32x4_t acc[8][8];
+  const int KT = (a.kt_rows + Elt<T>::kBK - 1) / Elt<T>::kBK;
+  mainloop<T>(lds, acc, la, lb, KT, fo);
+
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const int32_t vl = m0 + ec.row(fm);
+    if (vl >= a.cv) continue;
+    float* wrow = a.dW + (int64_t)(a.v0 + vl) * a.lddw;
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+      const int32_t h = h0 + ec.col(fn);
+      if (h >= a.H) continue;
+      f32x4_t v = acc[fm][fn];
+      if (a.accumulate) v += *reinterpret_cast<const f32x4_t*>(wrow + h);
+      *reinterpret_cast<f32x4_t*>(wrow + h) = v;
+    }
+  }
+}
+
+// ===========================================================================
+// Small kernels
+// ===========================================================================
+
+// XcT[h][t] = X[row_index[t]][h] for t < Cn, 0 for Cn <= t < t_pad.
+// 64 x 64 element tiles; 16-byte loads along h, 16-byte stores along t.
+template <typename T>
+__global__ __launch_bounds__(256) void gather_t_kernel(const char* X, int64_t ldx_b,
+                                                       const int32_t* row_index, int32_t Cn,
+                                                       int32_t H, char* XcT, int64_t ldxt_b) {
+  constexpr int E = Elt<T>::kBytes;
+  constexpr int PER = 16 / E;  // elements per 16-byte vector
+  __shared__ T tile[64][64 + 1];
+  const int32_t t0 = blockIdx.x * 64, hb = blockIdx.y * 64;
+  // load 64 rows (t) x 64 h
+  for (int v = threadIdx.x; v < 64 * 64 / PER; v += 256) {
+    const int tr = v / (64 / PER), hc = (v % (64 / PER)) * PER;
+    const int32_t t = t0 + tr;
+    u32x4_t val = {0u, 0u, 0u, 0u};
+    if (t < Cn && hb + hc < H)
+      val = *reinterpret_cast<const u32x4_t*>(X + (int64_t)row_index[t] * ldx_b +
+                                              (int64_t)(hb + hc) * E);
+    const T* e = reinterpret_cast<const T*>(&val);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) tile[tr][hc + j] = e[j];
+  }
+  __syncthreads();
+  for (int v = threadIdx.x; v < 64 * 64 / PER; v += 256) {
+    const int hr = v / (64 / PER), tc = (v % (64 / PER)) * PER;
+    if (hb + hr >= H) continue;
+    u32x4_t val;
+    T* e = reinterpret_cast<T*>(&val);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) e[j] = tile[tc + j][hr];
+    *reinterpret_cast<u32x4_t*>(XcT + (int64_t)(hb + hr) * ldxt_b + (int64_t)(t0 + tc) * E) = val;
+  }
+}
+
+// Zero `nrows` rows (ids from rows[]) of a row-major matrix, row_bytes each
+// (a multiple of 16).
+__global__ __launch_bounds__(256) void zero_rows_kernel(char* base, int64_t ld_b,
+                                                        const int32_t* rows, int64_t nrows,
+                                                        int64_t row_bytes) {
+  const int64_t nvec = row_bytes / 16;
+  for (int64_t r = blockIdx.x; r < nrows; r += gridDim.x) {
+    char* p = base + (int64_t)rows[r] * ld_b;
+    for (int64_t v = threadIdx.x; v < nvec; v += blockDim.x)
+      reinterpret_cast<u32x4_t*>(p)[v] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+}
+
+// Zero a dense [rows][cols] fp32 matrix with leading dimension ld.
+__global__ __launch_bounds__(256) void zero_matrix_f32_kernel(float* p, int64_t rows, int64_t cols,
+                                                              int64_t ld) {
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x)
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) p[r * ld + c] = 0.f;
+}
+
+__global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
+
+// loss[rows[i]] = +0.0 for i < n.
+__global__ __launch_bounds__(256) void zero_scatter_f32_kernel(float* loss, const int32_t* rows,
+                                                               int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    loss[rows[i]] = 0.0f;
+}
+
+// Valid-row compaction in one workgroup of 1024 threads.
+//   row_index[0 .. N)    positions t with a valid label, ascending
+//   row_index[N .. T)    every other position (descending from the end)
+//   row_label[0 .. N)    their labels
+//   counts = {N, #labels outside [0, V), first such t or -1, 0}
+__global__ __launch_bounds__(1024) void prepare_kernel(const int64_t* labels, int64_t T, int64_t V,
+                                                       int64_t ignore, int shift, int32_t* row_index,
+                                                       int32_t* row_label, int32_t* counts) {
+  constexpr int kItems = 4;
+  __shared__ int32_t wsum_v[16], wsum_m[16];
+  __shared__ int32_t s_base_v, s_base_m, s_bad, s_first_bad;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  if (tid == 0) {
+    s_base_v = 0;
+    s_base_m = 0;
+    s_bad = 0;
+    s_first_bad = INT32_MAX;
+  }
+  __syncthreads();
+  for (int64_t start = 0; start < T; start += 1024 * kItems) {
+    int32_t y[kItems];
+    uint32_t vmask = 0, mmask = 0;
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+      const int64_t t = start + tid * kItems + j;
+      y[j] = 0;
+      if (t >= T) continue;
+      int64_t lab;
+      if (shift) lab = (t + 1 < T) ? labels[t + 1] : ignore;
+      else lab = labels[t];
+      if (lab == ignore) {
+        mmask |= 1u << j;
+      } else if (lab < 0 || lab >= V) {
+        mmask |= 1u << j;
+        atomicAdd(&s_bad, 1);
+        atomicMin(&s_first_bad, (int32_t)t);
+      } else {
+        vmask |= 1u << j;
+        y[j] = (int32_t)lab;
+      }
+    }
+    const int cv = __builtin_popcount(vmask), cm = __builtin_popcount(mmask);
+    // inclusive wave scans
+    int sv = cv, sm = cm;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      int tv = __shfl_up(sv, o), tmm = __shfl_up(sm, o);
+      if (lane >= o) {
+        sv += tv;
+        sm += tmm;
+      }
+    }
+    if (lane == 63) {
+      wsum_v[wid] = sv;
+      wsum_m[wid] = sm;
+    }
+    __syncthreads();
+    int pv = 0, pm = 0, tv_all = 0, tm_all = 0;
+    for (int w = 0; w < 16; ++w) {
+      if (w < wid) {
+        pv += wsum_v[w];
+        pm += wsum_m[w];
+      }
+      tv_all += wsum_v[w];
+      tm_all += wsum_m[w];
+    }
+    int ov = s_base_v + pv + sv - cv;
+    int om = s_base_m + pm + sm - cm;
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+      const int64_t t = start + tid * kItems + j;
+      if (vmask & (1u << j)) {
+        row_index[ov] = (int32_t)t;
+        row_label[ov] = y[j];
+        ++ov;
+      } else if (mmask & (1u << j)) {
+        row_index[T - 1 - om] = (int32_t)t;
+        ++om;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      s_base_v += tv_all;
+      s_base_m += tm_all;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    counts[0] = s_base_v;
+    counts[1] = s_bad;
+    counts[2] = s_bad ? s_first_bad : -1;
+    counts[3] = 0;
+  }
+}
+
+// status = 1 if cu_seqlens is not a valid partition of [0, T).
+__global__ __launch_bounds__(256) void segment_check_kernel(const int32_t* cu, int64_t S, int64_t T,
+                                                            int32_t* status) {
+  __shared__ int32_t bad;
+  if (threadIdx.x == 0) bad = (cu[0] != 0 || (int64_t)cu[S] != T) ? 1 : 0;
+  __syncthreads();
+  for (int64_t s = threadIdx.x; s < S; s += blockDim.x)
+    if (cu[s + 1] < cu[s]) atomicOr(&bad, 1);
+  __syncthreads();
+  if (threadIdx.x == 0) *status = bad;
+}
+
+// One workgroup per sample: fixed-order tree sum of loss and count of valid
+// targets over [cu[s], cu[s+1]).
+__global__ __launch_bounds__(256) void segment_sum_kernel(const float* loss, const int64_t* target,
+                                                          int64_t ignore, const int32_t* cu,
+                                                          const int32_t* status, float* seg_loss,
+                                                          int32_t* seg_count) {
+  __shared__ float sl[256];
+  __shared__ int32_t sc[256];
+  const int64_t s = blockIdx.x;
+  float acc = 0.f;
+  int32_t cnt = 0;
+  if (*status == 0) {
+    for (int64_t t = cu[s] + threadIdx.x; t < cu[s + 1]; t += 256) {
+      acc += loss[t];
+      cnt += target[t] != ignore ? 1 : 0;
+    }
+  }
+  sl[threadIdx.x] = acc;
+  sc[threadIdx.x] = cnt;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      sl[threadIdx.x] += sl[threadIdx.x + o];
+      sc[threadIdx.x] += sc[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    seg_loss[s] = sl[0];
+    seg_count[s] = sc[0];
+  }
+}
+
+// ===========================================================================
+// Cross-entropy over materialised logits [T, V] (reduction 'none').
+// One workgroup of 256 threads per row; 16-byte loads along V.
+// ===========================================================================
+template <typename T>
+__device__ __forceinline__ void load_vec(const char* p, float (&x)[16 / sizeof(T)]);
+template <>
+__device__ __forceinline__ void load_vec<float>(const char* p, float (&x)[4]) {
+  f32x4_t v = *reinterpret_cast<const f32x4_t*>(p);
+  x[0] = v[0];
+  x[1] = v[1];
+  x[2] = v[2];
+  x[3] = v[3];
+}
+template <>
+__device__ __forceinline__ void load_vec<__bf16>(const char* p, float (&x)[8]) {
+  u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __builtin_bit_cast(float, v[i] << 16);
+    x[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
+  }
+}
+template <typename T>
+__device__ __forceinline__ float load_one(const char* p) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const float*>(p);
+  } else {
+    return __builtin_bit_cast(float, (uint32_t)*reinterpret_cast<const uint16_t*>(p) << 16);
+  }
+}
+
+// Block-wide merge of per-thread (m, d) states; result valid in all threads.
+__device__ __forceinline__ void block_lse_merge(float& m, float& d, float* sm) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) lse_merge(m, d, __shfl_xor(m, o), __shfl_xor(d, o));
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    sm[2 * w] = m;
+    sm[2 * w + 1] = d;
+  }
+  __syncthreads();
+  m = kNegBig;
+  d = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) lse_merge(m, d, sm[2 * i], sm[2 * i + 1]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void ce_forward_kernel(const char* logits, int64_t V, int64_t ld_b,
+                                                         const int64_t* target, int64_t ignore,
+                                                         float* loss, float* lse, int32_t* status) {
+  constexpr int E = sizeof(T), VEC = 16 / E;
+  __shared__ float sm[16];
+  const int64_t t = blockIdx.x;
+  const int64_t y = target[t];
+  if (y == ignore) {
+    if (threadIdx.x == 0) {
+      loss[t] = 0.0f;
+      lse[t] = 0.0f;
+    }
+    return;
+  }
+  if (y < 0 || y >= V) {
+    if (threadIdx.x == 0) {
+      atomicOr(status, 1);
+      loss[t] = 0.0f;
+      lse[t] = 0.0f;
+    }
+    return;
+  }
+  const char* row = logits + t * ld_b;
+  float m = kNegBig, d = 0.f;
+  const int64_t nvec = V / VEC;
+  for (int64_t i = threadIdx.x; i < nvec; i += 256) {
+    float x[VEC];
+    load_vec<T>(row + i * 16, x);
+    float mx = x[0];
+#pragma unroll
+    for (int j = 1; j < VEC; ++j) mx = fmaxf(mx, x[j]);
+    const float mn = fmaxf(m, mx * kLog2e);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) s += fast_exp2(fmaf(x[j], kLog2e, -mn));
+    d = fmaf(d, fast_exp2(m - mn), s);
+    m = mn;
+  }
+  for (int64_t v = nvec * VEC + threadIdx.x; v < V; v += 256) {
+    const float x = load_one<T>(row + v * E) * kLog2e;
+    lse_merge(m, d, x, 1.0f);
+  }
+  block_lse_merge(m, d, sm);
+  if (threadIdx.x == 0) {
+    const float L = (m + fast_log2(d)) * kLn2;
+    lse[t] = L;
+    loss[t] = L - load_one<T>(row + y * E);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void ce_backward_kernel(const char* logits, int64_t V, int64_t ld_b,
+                                                          const int64_t* target, int64_t ignore,
+                                                          const float* lse, const float* grad,
+                                                          int64_t gstride, char* dlogits,
+                                                          int64_t ldd_b) {
+  constexpr int E = sizeof(T);
+  const int64_t t = blockIdx.x;
+  const int64_t y = target[t];
+  const bool valid = y != ignore && y >= 0 && y < V;
+  const float g = valid ? grad[t * gstride] : 0.f;
+  const float l2 = valid ? lse[t] * kLog2e : 0.f;
+  const char* row = logits + t * ld_b;
+  char* drow = dlogits + t * ldd_b;
+  // pairs of elements so bf16 rows are written 4 bytes at a time
+  for (int64_t v = 2 * threadIdx.x; v < V; v += 512) {
+    float o[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t c = v + j;
+      float r = 0.f;
+      if (valid && c < V) {
+        const float p = fast_exp2(fmaf(load_one<T>(row + c * E), kLog2e, -l2));
+        r = g * (p - (c == y ? 1.f : 0.f));
+      }
+      o[j] = r;
+    }
+    if constexpr (E == 4) {
+      reinterpret_cast<float*>(drow)[v] = o[0];
+      if (v + 1 < V) reinterpret_cast<float*>(drow)[v + 1] = o[1];
+    } else {
+      const uint32_t pk = pack_bf16x2(o[0], o[1]);
+      if (v + 1 < V) *reinterpret_cast<uint32_t*>(drow + v * 2) = pk;
+      else *reinterpret_cast<uint16_t*>(drow + v * 2) = (uint16_t)(pk & 0xffffu);
+    }
+  }
+}
+
+}  // namespace mtf

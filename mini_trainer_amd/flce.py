@@ -1,0 +1,295 @@
+"""Host side of the fused LM-head linear + per-token cross-entropy.
+
+Mirrors the reference's loss boundary (none_reduction_losses.py:5-36): the
+functions here take PyTorch tensors on a ROCm device, hand raw pointers and
+the current HIP stream to libmt_flce.so (include/mt_flce.h) and return
+PyTorch tensors.  There is no CPU or eager-PyTorch fallback: non-device
+tensors or a missing library raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import MT_DTYPE_BF16, MT_DTYPE_F32, check, load
+
+__all__ = [
+    "fused_linear_cross_entropy",
+    "cross_entropy_none",
+    "prepare_targets",
+    "per_sample_loss_sums",
+    "backward_plan",
+    "BACKWARD_BUDGET_ENV",
+]
+
+# Optional override of the backward workspace budget in bytes (default: 5% of
+# the materialised-logits size T * V * sizeof(dtype)).
+BACKWARD_BUDGET_ENV = "MT_FLCE_BWD_BUDGET_BYTES"
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return MT_DTYPE_BF16
+    if dt == torch.float32:
+        return MT_DTYPE_F32
+    raise TypeError(f"fused linear cross-entropy supports bfloat16 and float32, got {dt}")
+
+
+def _p(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_device(name: str, t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"{name} must be a ROCm device tensor; the fused linear cross-entropy has no CPU path"
+        )
+
+
+def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    """2-D view with unit stride along the last dim and a 16-byte row pitch."""
+    t2 = t.reshape(-1, t.shape[-1])
+    es = t2.element_size()
+    if (t2.stride(1) != 1 or (t2.stride(0) * es) % 16 != 0 or t2.data_ptr() % 16 != 0
+            or t2.stride(0) < t2.shape[1]):
+        t2 = t2.contiguous()
+    return t2
+
+
+def prepare_targets(target: torch.Tensor, vocab_size: int, ignore_index: int = -100,
+                    shift: bool = False) -> Tuple[torch.Tensor, torch.Tensor, int]:
+    """Valid-row compaction (mt_flce_prepare) plus the one host sync of a call.
+
+    Returns (row_index int32 [T], row_label int32 [T], n_valid).  row_index
+    lists the valid positions first (ascending), then every ignored one.
+    Raises IndexError, like F.cross_entropy, for a target outside
+    [0, vocab_size) that is not ignore_index.
+    """
+    _require_device("target", target)
+    lib = load()
+    tgt = target.reshape(-1)
+    if tgt.dtype != torch.int64:
+        tgt = tgt.to(torch.int64)
+    tgt = tgt.contiguous()
+    T = tgt.numel()
+    dev = tgt.device
+    row_index = torch.empty(T, dtype=torch.int32, device=dev)
+    row_label = torch.empty(T, dtype=torch.int32, device=dev)
+    counts = torch.empty(4, dtype=torch.int32, device=dev)
+    check(lib.mt_flce_prepare(_p(tgt), T, int(vocab_size), int(ignore_index), int(bool(shift)),
+                              _p(row_index), _p(row_label), _p(counts), _stream(dev)),
+          "mt_flce_prepare")
+    c = counts.cpu().tolist()
+    if c[1] > 0:
+        pos = c[2]
+        src = pos + 1 if shift else pos
+        bad = int(tgt[src].item())
+        raise IndexError(f"Target {bad} is out of bounds (vocabulary size {vocab_size}, "
+                         f"position {pos}, {c[1]} such targets).")
+    return row_index, row_label, int(c[0])
+
+
+def backward_plan(T: int, n_valid: int, H: int, V: int, dtype: torch.dtype,
+                  budget_bytes: Optional[int] = None) -> Tuple[int, int, int]:
+    """(chunk_rows, chunk_vocab, workspace_bytes) of the backward blocking."""
+    lib = load()
+    if budget_bytes is None:
+        budget_bytes = int(os.environ.get(BACKWARD_BUDGET_ENV, "0"))
+    c, cv, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_size_t()
+    check(lib.mt_flce_backward_plan(T, n_valid, H, V, _dtype_code(dtype), budget_bytes,
+                                    ctypes.byref(c), ctypes.byref(cv), ctypes.byref(ws)),
+          "mt_flce_backward_plan")
+    return c.value, cv.value, ws.value
+
+
+def _grad_vector(grad: torch.Tensor, T: int) -> Tuple[torch.Tensor, int]:
+    g = grad.reshape(-1) if grad.dim() != 1 else grad
+    if g.dtype != torch.float32:
+        g = g.float()
+    if g.numel() == 1:
+        return g, 0
+    if g.stride(0) == 0:  # a scalar expanded over the tokens (sum().backward())
+        return g, 0
+    if g.stride(0) != 1:
+        g = g.contiguous()
+    if g.numel() != T:
+        raise ValueError(f"grad of the loss has {g.numel()} elements, expected {T}")
+    return g, 1
+
+
+class _FusedLinearCrossEntropyNone(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden, weight, target, ignore_index, softcap, shift, dw_accumulator):
+        _require_device("hidden_states", hidden)
+        _require_device("lm_head_weight", weight)
+        if weight.dim() != 2:
+            raise ValueError(f"lm_head_weight must be [V, H], got {tuple(weight.shape)}")
+        if hidden.dtype != weight.dtype:
+            raise TypeError(f"hidden_states ({hidden.dtype}) and lm_head_weight ({weight.dtype}) "
+                            "must have the same dtype")
+        dt = _dtype_code(hidden.dtype)
+        V, H = weight.shape
+        if hidden.shape[-1] != H:
+            raise ValueError(f"hidden size mismatch: hidden_states {tuple(hidden.shape)}, "
+                             f"lm_head_weight {tuple(weight.shape)}")
+        X = _rows(hidden, "hidden_states")
+        W = _rows(weight, "lm_head_weight")
+        T = X.shape[0]
+        if target.numel() != T:
+            raise ValueError(f"target has {target.numel()} elements, expected {T}")
+        lib = load()
+        dev = X.device
+        row_index, row_label, n = prepare_targets(target, V, ignore_index, shift)
+        loss = torch.empty(T, dtype=torch.float32, device=dev)
+        lse = torch.empty(n, dtype=torch.float32, device=dev)
+        ws_bytes = lib.mt_flce_forward_workspace_bytes(T, n, H, V, dt)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
+                                  float(softcap), _p(row_index), _p(row_label), n, _p(loss),
+                                  _p(lse), _p(ws), ws_bytes, _stream(dev)), "mt_flce_forward")
+        del ws
+        ctx.save_for_backward(X, W, row_index, row_label, lse)
+        ctx.meta = (n, float(softcap), hidden.shape, dt)
+        ctx.dw_accumulator = dw_accumulator
+        return loss.view(hidden.shape[:-1])
+
+    @staticmethod
+    def backward(ctx, grad_loss):
+        X, W, row_index, row_label, lse = ctx.saved_tensors
+        n, softcap, hshape, dt = ctx.meta
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        acc = ctx.dw_accumulator
+        if not need_x and not need_w and acc is None:
+            return None, None, None, None, None, None, None
+        lib = load()
+        T, H = X.shape
+        V = W.shape[0]
+        dev = X.device
+        g, gstride = _grad_vector(grad_loss, T)
+        dX = torch.empty((T, H), dtype=X.dtype, device=dev)
+        if acc is not None:
+            dW, accumulate = acc, 1
+        else:
+            dW, accumulate = torch.empty((V, H), dtype=torch.float32, device=dev), 0
+        C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt, softcap,
+                                   _p(row_index), _p(row_label), n, _p(lse), _p(g), gstride,
+                                   _p(dX), dX.stride(0), _p(dW), dW.stride(0), accumulate, C, Cv,
+                                   _p(ws), ws_bytes, _stream(dev)), "mt_flce_backward")
+        grad_x = dX.view(hshape) if need_x else None
+        grad_w = dW if (need_w and acc is None) else None
+        return grad_x, grad_w, None, None, None, None, None
+
+
+def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torch.Tensor,
+                               target: torch.Tensor, ignore_index: int = -100,
+                               softcap: Optional[float] = None, shift_labels: bool = False,
+                               dw_accumulator: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Per-token loss of hidden_states @ lm_head_weight.T against target.
+
+    loss[t] = logsumexp(logits[t]) - logits[t, target[t]], +0.0 where
+    target[t] == ignore_index; logits are rounded to the input dtype as
+    F.linear would produce them, then evaluated in fp32.  Differentiable in
+    hidden_states and lm_head_weight; the gradient of the weight is formed in
+    fp32.  With dw_accumulator (fp32 [V, H]) the weight gradient is added into
+    that tensor instead of being returned to autograd.  shift_labels applies
+    the causal shift (target[t] = labels[t + 1]) on the device.
+    """
+    if dw_accumulator is not None:
+        V, H = lm_head_weight.shape
+        if (dw_accumulator.dtype != torch.float32 or tuple(dw_accumulator.shape) != (V, H)
+                or dw_accumulator.stride(1) != 1 or not dw_accumulator.is_cuda):
+            raise ValueError("dw_accumulator must be a float32 device tensor of shape [V, H] "
+                             "with unit stride along H")
+    cap = 0.0 if softcap is None else float(softcap)
+    if cap < 0:
+        raise ValueError("softcap must be positive (or None)")
+    return _FusedLinearCrossEntropyNone.apply(hidden_states, lm_head_weight, target,
+                                              int(ignore_index), cap, bool(shift_labels),
+                                              dw_accumulator)
+
+
+class _CrossEntropyNone(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, source, target, ignore_index):
+        _require_device("source", source)
+        _require_device("target", target)
+        dt = _dtype_code(source.dtype)
+        L = _rows(source, "source")
+        T, V = L.shape
+        tgt = target.reshape(-1).to(torch.int64).contiguous()
+        if tgt.numel() != T:
+            raise ValueError(f"target has {tgt.numel()} elements, expected {T}")
+        lib = load()
+        dev = L.device
+        loss = torch.empty(T, dtype=torch.float32, device=dev)
+        lse = torch.empty(T, dtype=torch.float32, device=dev)
+        status = torch.empty(1, dtype=torch.int32, device=dev)
+        check(lib.mt_ce_forward(_p(L), T, V, L.stride(0), dt, _p(tgt), int(ignore_index), _p(loss),
+                                _p(lse), _p(status), _stream(dev)), "mt_ce_forward")
+        if int(status.item()) != 0:
+            bad = tgt[(tgt != ignore_index) & ((tgt < 0) | (tgt >= V))][0].item()
+            raise IndexError(f"Target {bad} is out of bounds.")
+        ctx.save_for_backward(L, tgt, lse)
+        ctx.meta = (int(ignore_index), dt, source.shape, source.dtype)
+        out = loss.view(source.shape[:-1])
+        return out if source.dtype == torch.float32 else out.to(source.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_loss):
+        L, tgt, lse = ctx.saved_tensors
+        ignore_index, dt, shape, dtype = ctx.meta
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        T, V = L.shape
+        g, gstride = _grad_vector(grad_loss, T)
+        d = torch.empty((T, V), dtype=dtype, device=L.device)
+        check(load().mt_ce_backward(_p(L), T, V, L.stride(0), dt, _p(tgt), ignore_index, _p(lse),
+                                    _p(g), gstride, _p(d), d.stride(0), _stream(L.device)),
+              "mt_ce_backward")
+        return d.view(shape), None, None
+
+
+def cross_entropy_none(source: torch.Tensor, target: torch.Tensor,
+                       ignore_index: int = -100) -> torch.Tensor:
+    """F.cross_entropy(source, target, ignore_index, reduction='none') on the device."""
+    return _CrossEntropyNone.apply(source, target, int(ignore_index))
+
+
+def per_sample_loss_sums(loss: torch.Tensor, target: torch.Tensor, cu_seqlens: torch.Tensor,
+                         ignore_index: int = -100,
+                         validate: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-sample (sum of loss, number of counted tokens) over a packed batch.
+
+    cu_seqlens (int32 [S+1]) partitions the T packed positions into samples.
+    With validate, a malformed cu_seqlens raises ValueError (one sync).
+    """
+    for name, t in (("loss", loss), ("target", target), ("cu_seqlens", cu_seqlens)):
+        _require_device(name, t)
+    lib = load()
+    ls = loss.reshape(-1).float().contiguous()
+    tgt = target.reshape(-1).to(torch.int64).contiguous()
+    cu = cu_seqlens.reshape(-1).to(torch.int32).contiguous()
+    T, S = ls.numel(), cu.numel() - 1
+    if tgt.numel() != T or S < 0:
+        raise ValueError("loss and target must have the same number of elements; "
+                         "cu_seqlens needs at least one entry")
+    dev = ls.device
+    seg_loss = torch.empty(S, dtype=torch.float32, device=dev)
+    seg_cnt = torch.empty(S, dtype=torch.int32, device=dev)
+    status = torch.empty(1, dtype=torch.int32, device=dev)
+    check(lib.mt_segment_sum(_p(ls), _p(tgt), T, int(ignore_index), _p(cu), S, _p(seg_loss),
+                             _p(seg_cnt), _p(status), _stream(dev)), "mt_segment_sum")
+    if validate and int(status.item()) != 0:
+        raise ValueError(f"cu_seqlens is not a partition of [0, {T}): must start at 0, be "
+                         f"non-decreasing and end at {T}")
+    return seg_loss, seg_cnt
