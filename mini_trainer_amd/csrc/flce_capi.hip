@@ -392,6 +392,16 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
   if ((reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(dW) |
        reinterpret_cast<uintptr_t>(workspace)) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "dX, dW and workspace must be 16-byte aligned");
+  if (n_valid > 0) {
+    if (chunk_rows <= 0 || chunk_rows % 256 != 0 || chunk_vocab <= 0 || chunk_vocab % 256 != 0)
+      return fail(MT_ERR_INVALID_ARGUMENT,
+                  "chunk_rows=%lld / chunk_vocab=%lld must be positive multiples of 256",
+                  (long long)chunk_rows, (long long)chunk_vocab);
+    const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es);
+    if (workspace_bytes < need || !workspace)
+      return fail(MT_ERR_WORKSPACE_TOO_SMALL, "backward workspace %zu bytes < required %zu",
+                  workspace_bytes, need);
+  }
   hipStream_t s = (hipStream_t)stream;
   if (T - n_valid > 0) {
     hipLaunchKernelGGL(zero_rows_kernel, dim3((uint32_t)std::min<int64_t>(T - n_valid, 8192)), dim3(256),
@@ -407,13 +417,6 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
     }
     return MT_OK;
   }
-  if (chunk_rows <= 0 || chunk_rows % 256 != 0 || chunk_vocab <= 0 || chunk_vocab % 256 != 0)
-    return fail(MT_ERR_INVALID_ARGUMENT, "chunk_rows=%lld / chunk_vocab=%lld must be positive multiples of 256",
-                (long long)chunk_rows, (long long)chunk_vocab);
-  const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es);
-  if (workspace_bytes < need || !workspace)
-    return fail(MT_ERR_WORKSPACE_TOO_SMALL, "backward workspace %zu bytes < required %zu",
-                workspace_bytes, need);
   if (dtype == MT_DTYPE_BF16)
     return launch_backward<__bf16>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                    grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW,
@@ -447,8 +450,8 @@ int mt_ce_forward(const void* logits, int64_t T, int64_t V, int64_t ld, int dtyp
   if (T < 0 || T > INT32_MAX || V <= 0 || V > INT32_MAX || ld < V)
     return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld V=%lld ld=%lld", (long long)T, (long long)V,
                 (long long)ld);
-  if ((ld * es) % 16 != 0 || reinterpret_cast<uintptr_t>(logits) % 16 != 0)
-    return fail(MT_ERR_INVALID_ARGUMENT, "logits rows must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(logits) % es != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "logits must be aligned to its element size");
   if (!status || (T > 0 && (!logits || !target || !loss || !lse)))
     return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
   hipStream_t s = (hipStream_t)stream;
@@ -474,8 +477,8 @@ int mt_ce_backward(const void* logits, int64_t T, int64_t V, int64_t ld, int dty
   if (T < 0 || T > INT32_MAX || V <= 0 || V > INT32_MAX || ld < V || ldd < V || grad_stride < 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld V=%lld ld=%lld ldd=%lld", (long long)T,
                 (long long)V, (long long)ld, (long long)ldd);
-  if ((ldd * es) % 4 != 0 || reinterpret_cast<uintptr_t>(dlogits) % 4 != 0)
-    return fail(MT_ERR_INVALID_ARGUMENT, "dlogits rows must be 4-byte aligned");
+  if (reinterpret_cast<uintptr_t>(dlogits) % es != 0 || reinterpret_cast<uintptr_t>(logits) % es != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "logits / dlogits must be aligned to their element size");
   if (T == 0) return MT_OK;
   if (!logits || !target || !lse || !grad_loss || !dlogits)
     return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");

@@ -88,14 +88,14 @@ __device__ __forceinline__ f32x4_t mma_chunk<__bf16>(u32x4_t a, u32x4_t b, f32x4
 }
 template <>
 __device__ __forceinline__ f32x4_t mma_chunk<float>(u32x4_t a, u32x4_t b, f32x4_t c) {
-  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.x),
-                                           __builtin_bit_cast(float, b.x), c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.y),
-                                           __builtin_bit_cast(float, b.y), c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.z),
-                                           __builtin_bit_cast(float, b.z), c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.w),
-                                           __builtin_bit_cast(float, b.w), c, 0, 0, 0);
+  // Bit-cast whole vectors, then index: a bit-cast of a single vector element
+  // (e.g. __builtin_bit_cast(float, a.y)) is read from element 0 by this
+  // compiler.
+  const f32x4_t af = __builtin_bit_cast(f32x4_t, a), bf = __builtin_bit_cast(f32x4_t, b);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[0], bf[0], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[1], bf[1], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[2], bf[2], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[3], bf[3], c, 0, 0, 0);
   return c;
 }
 

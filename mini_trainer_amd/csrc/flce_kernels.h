@@ -664,8 +664,9 @@ __device__ __forceinline__ void load_vec<__bf16>(const char* p, float (&x)[8]) {
   u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    x[2 * i] = __builtin_bit_cast(float, v[i] << 16);
-    x[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
+    const uint32_t w = v[i];
+    x[2 * i] = __builtin_bit_cast(float, w << 16);
+    x[2 * i + 1] = __builtin_bit_cast(float, w & 0xffff0000u);
   }
 }
 template <typename T>
@@ -718,10 +719,14 @@ __global__ __launch_bounds__(256) void ce_forward_kernel(const char* logits, int
   }
   const char* row = logits + t * ld_b;
   float m = kNegBig, d = 0.f;
-  const int64_t nvec = V / VEC;
+  // scalar head up to 16-byte alignment, 16-byte vectors, scalar tail
+  const int64_t mis = (int64_t)(reinterpret_cast<uintptr_t>(row) & 15u) / E;
+  const int64_t head = mis ? min<int64_t>(VEC - mis, V) : 0;
+  const int64_t nvec = (V - head) / VEC;
+  const char* vrow = row + head * E;
   for (int64_t i = threadIdx.x; i < nvec; i += 256) {
     float x[VEC];
-    load_vec<T>(row + i * 16, x);
+    load_vec<T>(vrow + i * 16, x);
     float mx = x[0];
 #pragma unroll
     for (int j = 1; j < VEC; ++j) mx = fmaxf(mx, x[j]);
@@ -732,10 +737,9 @@ __global__ __launch_bounds__(256) void ce_forward_kernel(const char* logits, int
     d = fmaf(d, fast_exp2(m - mn), s);
     m = mn;
   }
-  for (int64_t v = nvec * VEC + threadIdx.x; v < V; v += 256) {
-    const float x = load_one<T>(row + v * E) * kLog2e;
-    lse_merge(m, d, x, 1.0f);
-  }
+  for (int64_t v = threadIdx.x; v < head; v += 256) lse_merge(m, d, load_one<T>(row + v * E) * kLog2e, 1.0f);
+  for (int64_t v = head + nvec * VEC + threadIdx.x; v < V; v += 256)
+    lse_merge(m, d, load_one<T>(row + v * E) * kLog2e, 1.0f);
   block_lse_merge(m, d, sm);
   if (threadIdx.x == 0) {
     const float L = (m + fast_log2(d)) * kLn2;
@@ -776,8 +780,13 @@ __global__ __launch_bounds__(256) void ce_backward_kernel(const char* logits, in
       if (v + 1 < V) reinterpret_cast<float*>(drow)[v + 1] = o[1];
     } else {
       const uint32_t pk = pack_bf16x2(o[0], o[1]);
-      if (v + 1 < V) *reinterpret_cast<uint32_t*>(drow + v * 2) = pk;
-      else *reinterpret_cast<uint16_t*>(drow + v * 2) = (uint16_t)(pk & 0xffffu);
+      char* p = drow + v * 2;
+      if (v + 1 < V && (reinterpret_cast<uintptr_t>(p) & 3u) == 0) {
+        *reinterpret_cast<uint32_t*>(p) = pk;
+      } else {
+        *reinterpret_cast<uint16_t*>(p) = (uint16_t)(pk & 0xffffu);
+        if (v + 1 < V) *reinterpret_cast<uint16_t*>(p + 2) = (uint16_t)(pk >> 16);
+      }
     }
   }
 }

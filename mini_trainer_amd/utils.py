@@ -15,7 +15,6 @@ def patch_target_module(to_patch: str, replace_with: Any) -> None:
     TF/loss/loss_utils.py:70 does) then reach the replacement.
     """
     parts = to_patch.split(".")
-    if len(parts) <= 1:
-        raise ValueError("must have an object to patch")
+    assert len(parts) > 1, "must have an object to patch"
     module = importlib.import_module(".".join(parts[:-1]))
     setattr(module, parts[-1], replace_with)

@@ -1,0 +1,118 @@
+"""C-ABI surface without a GPU: the library loads, exports every symbol the
+header declares, and its host-only logic (argument checks, planners) behaves.
+No call here launches a kernel."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from mini_trainer_amd import _lib, backward_plan, synth
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mt_flce.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mt_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/mt_flce.h but not exported"
+    assert sorted(_lib.SIGNATURES) == names, "ctypes signatures must mirror the header"
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define MT_FLCE_ABI_VERSION (\d+)", HEADER.read_text())
+    assert _lib.load().mt_flce_abi_version() == int(m.group(1)) == _lib.ABI_VERSION
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
+    with pytest.raises(_lib.FlceError):
+        _lib.load()
+
+
+def call_forward(**kw):
+    lib = _lib.load()
+    a = dict(X=16, W=16, T=8, H=64, V=100, ldx=64, ldw=64, dtype=1, softcap=0.0, ri=16, rl=16,
+             n=4, loss=16, lse=16, ws=16, wsb=1 << 20, stream=None)
+    a.update(kw)
+    return lib.mt_flce_forward(a["X"], a["W"], a["T"], a["H"], a["V"], a["ldx"], a["ldw"],
+                               a["dtype"], a["softcap"], a["ri"], a["rl"], a["n"], a["loss"],
+                               a["lse"], a["ws"], a["wsb"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=7), 1),            # unknown dtype
+    (dict(H=96, ldx=96, ldw=96), 3),  # H not a multiple of 64 (bf16)
+    (dict(ldx=32), 1),             # ldx < H
+    (dict(ldx=68), 1),             # row pitch not a multiple of 16 bytes
+    (dict(X=18), 1),               # misaligned X
+    (dict(n=9), 1),                # n_valid > T
+    (dict(T=-1), 1),
+    (dict(V=0), 1),
+    (dict(softcap=-1.0), 1),
+    (dict(wsb=0), 2),              # workspace too small
+    (dict(W=None), 1),
+])
+def test_forward_host_checks(kw, code):
+    assert call_forward(**kw) == code
+    assert _lib.load().mt_flce_last_error()
+
+
+def test_backward_and_misc_host_checks():
+    lib = _lib.load()
+    args = [16, 16, 8, 64, 100, 64, 64, 1, 0.0, 16, 16, 4, 16, 16, 1, 16, 64, 16, 64, 0]
+    # chunk sizes must be positive multiples of 256
+    assert lib.mt_flce_backward(*args, 100, 256, 16, 1 << 30, None) == 1
+    # workspace too small for the requested blocks
+    assert lib.mt_flce_backward(*args, 256, 256, 16, 10, None) == 2
+    # negative grad stride
+    bad = list(args)
+    bad[14] = -1
+    assert lib.mt_flce_backward(*bad, 256, 256, 16, 1 << 30, None) == 1
+    assert lib.mt_flce_prepare(None, -1, 10, -100, 0, None, None, None, None) == 1
+    assert lib.mt_segment_sum(None, None, 4, -100, None, 1, None, None, None, None) == 1
+    assert lib.mt_ce_forward(None, 4, 10, 5, 1, None, -100, None, None, None, None) == 1
+
+
+@pytest.mark.parametrize("key", [1, 2, 3, 4, 5])
+def test_backward_plan_fits_budget(key):
+    cfg = synth.CONFIGS[key]
+    n = int((synth.make_batch(cfg, 0, with_tensors=False)["target"] != -100).sum())
+    C, Cv, ws = backward_plan(cfg.T, n, cfg.H, cfg.V, cfg.dtype)
+    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    assert C % 256 == 0 and Cv % 256 == 0 and C >= 256 and Cv >= 256
+    assert ws <= 0.05 * cfg.T * cfg.V * es
+    # the workspace formula: G block + fp32 dX accumulator (if V is split) + X^T block
+    al = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    expect = al(C * Cv * es) + (al(C * cfg.H * 4) if Cv < cfg.V else 0) + al(cfg.H * C * es)
+    assert ws == expect
+
+
+def test_backward_plan_budget_override_and_degenerate():
+    C, Cv, ws = backward_plan(1000, 700, 128, 5000, torch.bfloat16, budget_bytes=1)
+    assert (C, Cv) == (256, 256)  # smallest blocks when nothing fits
+    C, Cv, ws = backward_plan(1000, 0, 128, 5000, torch.bfloat16)
+    assert (C, Cv, ws) == (0, 0, 0)
+    C, Cv, ws = backward_plan(4096, 3000, 128, 5000, torch.bfloat16, budget_bytes=1 << 40)
+    assert Cv >= 5000 and C >= 3000  # everything in one block
+
+
+def test_forward_workspace_is_small():
+    lib = _lib.load()
+    for key in (2, 3, 4, 5):
+        cfg = synth.CONFIGS[key]
+        ws = lib.mt_flce_forward_workspace_bytes(cfg.T, cfg.T, cfg.H, cfg.V, 1)
+        assert 0 < ws < 0.01 * cfg.T * cfg.V * 2
+    assert lib.mt_flce_forward_workspace_bytes(10, 0, 64, 100, 1) == 0

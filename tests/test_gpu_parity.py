@@ -210,11 +210,15 @@ def test_cross_entropy_none_materialised(gpu, dtype):
     out = cross_entropy_none(src, y.to(gpu))
     gr = torch.rand(333, generator=g)
     out.float().backward(gr.to(gpu))
+    # torch's own call on the same dtype (bf16 logits give a bf16 loss there too)
     ref_src = logits.clone().requires_grad_(True)
-    ref_out = torch.nn.functional.cross_entropy(ref_src.float(), y, reduction="none")
-    ref_out.backward(gr)
-    tol = 1e-5 if dtype == torch.float32 else 2e-3
-    torch.testing.assert_close(out.float().cpu(), ref_out, rtol=tol, atol=tol)
+    ref_out = torch.nn.functional.cross_entropy(ref_src, y, reduction="none")
+    ref_out.float().backward(gr)
+    assert out.dtype == ref_out.dtype
+    if dtype == torch.float32:
+        torch.testing.assert_close(out.cpu(), ref_out, rtol=1e-5, atol=1e-5)
+    else:  # both round an fp32 result to bf16: at most one bf16 ulp apart
+        torch.testing.assert_close(out.float().cpu(), ref_out.float(), rtol=2 ** -7, atol=1e-3)
     assert torch.equal(out.float().cpu()[::5], torch.zeros(67))
     assert rel_fro(src.grad.float().cpu(), ref_src.grad.float()) <= 1e-2
 
