@@ -9,6 +9,7 @@
 
 #include "../../include/mt_flce.h"
 #include "flce_kernels.h"
+#include "flce_kernels3.h"
 
 using namespace mtf;
 
@@ -71,21 +72,31 @@ int check_common(const void* X, const void* W, int64_t T, int64_t H, int64_t V, 
   return MT_OK;
 }
 
+// Output tile shapes: bf16 kernels run 256 x 128 tiles, two workgroups per
+// CU; the fp32 kernels 256 x 256 tiles, one per CU.
+struct Geometry {
+  int64_t tile_m, tile_n, slots;
+};
+inline Geometry geometry(int es) {
+  return es == 2 ? Geometry{256, 128, 2 * kCUs} : Geometry{256, 256, kCUs};
+}
+
 // ---------------------------------------------------------------- forward
 struct FwdPlan {
   int64_t tiles_m = 0, vt_total = 0, per = 0, splits = 0;
 };
 
-FwdPlan plan_forward(int64_t n_valid, int64_t V) {
+FwdPlan plan_forward(int64_t n_valid, int64_t V, int es) {
+  const Geometry geo = geometry(es);
   FwdPlan p;
-  p.tiles_m = cdiv(n_valid, 256);
-  p.vt_total = cdiv(V, 256);
+  p.tiles_m = cdiv(n_valid, geo.tile_m);
+  p.vt_total = cdiv(V, geo.tile_n);
   if (p.tiles_m == 0) return p;
   int64_t best_cost = INT64_MAX, best_s = 1;
-  for (int64_t s = 1; s <= std::min<int64_t>(p.vt_total, 64); ++s) {
+  for (int64_t s = 1; s <= std::min<int64_t>(p.vt_total, 128); ++s) {
     const int64_t per = cdiv(p.vt_total, s);
     const int64_t s_eff = cdiv(p.vt_total, per);
-    const int64_t cost = cdiv(p.tiles_m * s_eff, kCUs) * per;
+    const int64_t cost = cdiv(p.tiles_m * s_eff, geo.slots) * per;
     if (cost < best_cost) {
       best_cost = cost;
       best_s = s_eff;
@@ -111,21 +122,23 @@ size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es) {
 }
 
 // Modelled seconds for one backward with blocks of C x Cv.
-double backward_cost(int64_t N, int64_t H, int64_t V, int64_t C, int64_t Cv) {
-  const double tile_rate = 2.5e15 / kCUs * 0.7;  // flop/s of one CU
+double backward_cost(int64_t N, int64_t H, int64_t V, int64_t C, int64_t Cv, int es) {
+  const Geometry geo = geometry(es);
+  const double tile_rate = 2.5e15 * 0.7 / geo.slots;  // flop/s of one resident tile
   const double launch = 8e-6, bw = 5e12;
+  const double tmn = 2.0 * geo.tile_m * geo.tile_n;
   double t = 0, bytes = 0;
   for (int64_t c0 = 0; c0 < N; c0 += C) {
     const int64_t cn = std::min(C, N - c0);
     const int64_t nv = cdiv(V, Cv);
     for (int64_t v0 = 0; v0 < V; v0 += Cv) {
       const int64_t cv = std::min(Cv, V - v0);
-      const double tile_flops_re = 2.0 * 256 * 256 * H;
-      const double tile_flops_dx = 2.0 * 256 * 256 * round_up(cv, 64);
-      const double tile_flops_dw = 2.0 * 256 * 256 * round_up(cn, 64);
-      t += cdiv(cdiv(cn, 256) * cdiv(cv, 256), kCUs) * tile_flops_re / tile_rate;
-      t += cdiv(cdiv(cn, 256) * cdiv(H, 256), kCUs) * tile_flops_dx / tile_rate;
-      t += cdiv(cdiv(cv, 256) * cdiv(H, 256), kCUs) * tile_flops_dw / tile_rate;
+      const double tile_flops_re = tmn * H;
+      const double tile_flops_dx = tmn * round_up(cv, 64);
+      const double tile_flops_dw = tmn * round_up(cn, 64);
+      t += cdiv(cdiv(cn, geo.tile_m) * cdiv(cv, geo.tile_n), geo.slots) * tile_flops_re / tile_rate;
+      t += cdiv(cdiv(cn, geo.tile_m) * cdiv(H, geo.tile_n), geo.slots) * tile_flops_dx / tile_rate;
+      t += cdiv(cdiv(cv, geo.tile_m) * cdiv(H, geo.tile_n), geo.slots) * tile_flops_dw / tile_rate;
       t += 3 * launch;
     }
     bytes += (double)V * H * 8;                        // dW read-modify-write
@@ -157,7 +170,7 @@ BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t
       const int64_t Cv = round_up(cdiv(V, nv), 256);
       const size_t ws = backward_ws(C, Cv, H, V, es);
       if (ws > budget) continue;
-      const double cost = backward_cost(N, H, V, C, Cv);
+      const double cost = backward_cost(N, H, V, C, Cv, es);
       if (cost < best_cost * 0.999) {
         best_cost = cost;
         best.C = C;
@@ -193,8 +206,12 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
   a.vt_per_split = (int32_t)p.per;
   a.part = reinterpret_cast<float*>(ws);
   a.xy = reinterpret_cast<float*>(ws + align_up((size_t)p.splits * n_valid * 2 * sizeof(float)));
-  hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
-                     stream, a);
+  if constexpr (sizeof(T) == 2)
+    hipLaunchKernelGGL(fwd3_kernel, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
+                       stream, a);
   MT_TRY(check_launch("fwd_kernel"));
   hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(n_valid, 256)), dim3(256), 0, stream,
                      a.part, a.xy, a.N, a.splits, row_index, loss, lse);
@@ -208,6 +225,7 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
                     int64_t lddx, float* dW, int64_t lddw, int accumulate, int64_t C, int64_t Cv,
                     char* ws, hipStream_t stream) {
   constexpr int es = sizeof(T);
+  const Geometry geo = geometry(es);
   const int64_t nv = cdiv(V, Cv);
   char* G = ws;
   float* accbuf = nv > 1 ? reinterpret_cast<float*>(ws + align_up((size_t)C * Cv * es)) : nullptr;
@@ -243,10 +261,14 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       r.cv = (int32_t)cv;
       r.G = G;
       r.ldg_b = ldg_b;
-      r.tiles_m = (int32_t)cdiv(cn, 256);
-      r.tiles_n = (int32_t)cdiv(cv, 256);
-      hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)), dim3(kThreads),
-                         0, stream, r);
+      r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
+      r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
+      if constexpr (sizeof(T) == 2)
+        hipLaunchKernelGGL(recompute3_kernel, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
+                           dim3(kThreads), 0, stream, r);
+      else
+        hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
+                           dim3(kThreads), 0, stream, r);
       MT_TRY(check_launch("recompute_kernel"));
 
       DxArgs x;
@@ -265,10 +287,14 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       x.dX = static_cast<char*>(dX);
       x.lddx_b = lddx * es;
       x.row_index = row_index + c0;
-      x.tiles_m = (int32_t)cdiv(cn, 256);
-      x.tiles_n = (int32_t)cdiv(H, 256);
-      hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
-                         stream, x);
+      x.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
+      x.tiles_n = (int32_t)cdiv(H, geo.tile_n);
+      if constexpr (sizeof(T) == 2)
+        hipLaunchKernelGGL(dx3_kernel, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
+                           stream, x);
+      else
+        hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
+                           stream, x);
       MT_TRY(check_launch("dx_kernel"));
 
       DwArgs w;
@@ -285,10 +311,14 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       w.dW = dW;
       w.lddw = lddw;
       w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
-      w.tiles_m = (int32_t)cdiv(cv, 256);
-      w.tiles_n = (int32_t)cdiv(H, 256);
-      hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
-                         stream, w);
+      w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
+      w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
+      if constexpr (sizeof(T) == 2)
+        hipLaunchKernelGGL(dw3_kernel, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
+                           stream, w);
+      else
+        hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
+                           stream, w);
       MT_TRY(check_launch("dw_kernel"));
     }
   }
@@ -317,9 +347,8 @@ int mt_flce_prepare(const int64_t* labels, int64_t T, int64_t V, int64_t ignore_
 size_t mt_flce_forward_workspace_bytes(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype) {
   (void)T;
   (void)H;
-  (void)dtype;
-  if (n_valid <= 0 || V <= 0) return 0;
-  return forward_ws(plan_forward(n_valid, V), n_valid);
+  if (n_valid <= 0 || V <= 0 || !esize_of(dtype)) return 0;
+  return forward_ws(plan_forward(n_valid, V, esize_of(dtype)), n_valid);
 }
 
 int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
@@ -332,7 +361,7 @@ int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H, int64_t 
   if (T == 0) return MT_OK;
   if (!row_index || !loss || (n_valid > 0 && (!row_label || !lse)))
     return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
-  const FwdPlan p = plan_forward(n_valid, V);
+  const FwdPlan p = plan_forward(n_valid, V, esize_of(dtype));
   const size_t need = n_valid > 0 ? forward_ws(p, n_valid) : 0;
   if (workspace_bytes < need || (need && !workspace))
     return fail(MT_ERR_WORKSPACE_TOO_SMALL, "forward workspace %zu bytes < required %zu",

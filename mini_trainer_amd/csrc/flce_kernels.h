@@ -19,9 +19,13 @@ namespace mtf {
 #define MT_GEMM_KERNEL \
   __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 
-struct EpiCoords {
+// Output coordinates of this lane's accumulators for a wave tile of
+// 128 rows x (NFN * 16) columns (NFN = 8: 256-wide tiles, 4: 128-wide).
+template <int NFN>
+struct EpiCoordsT {
+  static constexpr int kNF = NFN;
   uint32_t lane, wm, wn;
-  __device__ __forceinline__ EpiCoords() {
+  __device__ __forceinline__ EpiCoordsT() {
     lane = lane_id();
     uint32_t w = wave_id();
     wm = w >> 1;
@@ -30,13 +34,17 @@ struct EpiCoords {
   // Tile-local output row of fragment row fm held by this lane.
   __device__ __forceinline__ int row(int fm) const { return wm * 128 + fm * 16 + (lane & 15u); }
   // Tile-local output column of element 0 of fragment column fn.
-  __device__ __forceinline__ int col(int fn) const { return wn * 128 + fn * 16 + 4 * (lane >> 4); }
+  __device__ __forceinline__ int col(int fn) const {
+    return wn * (NFN * 16) + fn * 16 + 4 * (lane >> 4);
+  }
 };
+typedef EpiCoordsT<8> EpiCoords;
 
 // Is column offset `rel` (label column minus this lane's column of fn = 0,
-// r = 0) one of the 32 columns this lane holds?
+// r = 0) one of the NFN * 4 columns this lane holds?
+template <int NFN>
 __device__ __forceinline__ bool lane_holds(int rel) {
-  return rel >= 0 && rel < 128 && (rel & 12) == 0;
+  return rel >= 0 && rel < NFN * 16 && (rel & 12) == 0;
 }
 
 // ===========================================================================
@@ -55,18 +63,18 @@ struct FwdArgs {
   float* xy;    // [N] label logit
 };
 
-template <typename T, bool kTail, bool kCap>
-__device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][8], float (&m2)[8],
+template <typename T, int NFN, bool kTail, bool kCap>
+__device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][NFN], float (&m2)[8],
                                                   float (&d)[8], const int32_t (&rel)[8],
                                                   const int32_t (&rglob)[8], int32_t ncol0,
                                                   const FwdArgs& a, bool any_hit) {
   const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
-    float v[8][4];
+    float v[NFN][4];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int fn = 0; fn < 8; ++fn) {
+    for (int fn = 0; fn < NFN; ++fn) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[fn][r] = acc[fm][fn][r];
       round_pair<T>(v[fn][0], v[fn][1]);
@@ -83,17 +91,17 @@ __device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][8], fl
     const float mn = fmaxf(m2[fm], tmax * kLog2e);
     float s = 0.f;
 #pragma unroll
-    for (int fn = 0; fn < 8; ++fn)
+    for (int fn = 0; fn < NFN; ++fn)
 #pragma unroll
       for (int r = 0; r < 4; ++r) s += fast_exp2(fmaf(v[fn][r], kLog2e, -mn));
     d[fm] = fmaf(d[fm], fast_exp2(m2[fm] - mn), s);
     m2[fm] = mn;
     if (any_hit) {
       const int rl = rel[fm];
-      if (lane_holds(rl) && rglob[fm] < a.N) {
+      if (lane_holds<NFN>(rl) && rglob[fm] < a.N) {
         float hitv = 0.f;
 #pragma unroll
-        for (int fn = 0; fn < 8; ++fn)
+        for (int fn = 0; fn < NFN; ++fn)
 #pragma unroll
           for (int r = 0; r < 4; ++r) hitv = (rl == fn * 16 + r) ? v[fn][r] : hitv;
         a.xy[rglob[fm]] = hitv;
@@ -102,67 +110,38 @@ __device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][8], fl
   }
 }
 
-template <typename T>
-MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
-  uint32_t tm, ts;
-  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.splits, 4, tm, ts);
-  const EpiCoords ec;
-  FragOffsets fo;
-  fo.init();
-
-  const int32_t row0 = (int32_t)tm * 256;
-  DirectLoader la;
-  la.init([&](uint32_t r) {
-    int32_t rr = row0 + (int32_t)r;
-    rr = rr < a.N ? rr : a.N - 1;
-    return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
-  });
-
-  int32_t lbl[8], rglob[8];
-  float m2[8], d[8];
+// Online-LSE update of one finished 256 x 256 logits tile (vocabulary rows
+// vrow0 .. vrow0 + 255) plus label-logit capture.
+template <typename T, int NFN>
+__device__ __forceinline__ void fwd_tile_update(const f32x4_t (&acc)[8][NFN], float (&m2)[8],
+                                                float (&d)[8], const int32_t (&lbl)[8],
+                                                const int32_t (&rglob)[8], int32_t vrow0,
+                                                const EpiCoordsT<NFN>& ec, const FwdArgs& a) {
+  const int32_t ncol0 = vrow0 + ec.col(0);
+  int32_t rel[8];
+  bool hit = false;
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
-    rglob[fm] = row0 + ec.row(fm);
-    lbl[fm] = rglob[fm] < a.N ? a.row_label[rglob[fm]] : -1;
-    m2[fm] = kNegBig;
-    d[fm] = 0.f;
+    rel[fm] = lbl[fm] - ncol0;
+    hit |= lane_holds<NFN>(rel[fm]);
   }
-
-  const int KT = a.H / Elt<T>::kBK;
-  const int vt0 = (int)ts * a.vt_per_split;
-  const int vt1 = min(vt0 + a.vt_per_split, a.vt_total);
-  f32x4_t acc[8][8];
-  for (int vt = vt0; vt < vt1; ++vt) {
-    const int32_t vrow0 = vt * 256;
-    DirectLoader lb;
-    lb.init([&](uint32_t r) {
-      int32_t v = vrow0 + (int32_t)r;
-      v = v < a.V ? v : a.V - 1;
-      return a.W + (int64_t)v * a.ldw_b;
-    });
-    mainloop<T>(lds, acc, la, lb, KT, fo);
-
-    const int32_t ncol0 = vrow0 + ec.col(0);
-    int32_t rel[8];
-    bool hit = false;
-#pragma unroll
-    for (int fm = 0; fm < 8; ++fm) {
-      rel[fm] = lbl[fm] - ncol0;
-      hit |= lane_holds(rel[fm]);
-    }
-    const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
-    const bool tail = vrow0 + 256 > a.V;
-    if (a.softcap > 0.f) {
-      if (tail) fwd_tile_epilogue<T, true, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
-      else fwd_tile_epilogue<T, false, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
-    } else {
-      if (tail) fwd_tile_epilogue<T, true, false>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
-      else fwd_tile_epilogue<T, false, false>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
-    }
+  const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
+  const bool tail = vrow0 + NFN * 32 > a.V;
+  if (a.softcap > 0.f) {
+    if (tail) fwd_tile_epilogue<T, NFN, true, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
+    else fwd_tile_epilogue<T, NFN, false, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
+  } else {
+    if (tail) fwd_tile_epilogue<T, NFN, true, false>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
+    else fwd_tile_epilogue<T, NFN, false, false>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
   }
+}
 
-  // Merge the four lanes that share a row, then the two waves (wn = 0, 1).
+// Merge the four lanes that share a row, then the two waves (wn = 0, 1)
+// through LDS, and write this split's (max, sum) partial of every row.
+template <int NFN>
+__device__ __forceinline__ void fwd_final_merge(char* lds, float (&m2)[8], float (&d)[8],
+                                                const int32_t (&rglob)[8], uint32_t ts,
+                                                const EpiCoordsT<NFN>& ec, const FwdArgs& a) {
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     lse_merge(m2[fm], d[fm], __shfl_xor(m2[fm], 16), __shfl_xor(d[fm], 16));
@@ -189,6 +168,52 @@ MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
       }
     }
   }
+}
+
+template <typename T>
+MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  uint32_t tm, ts;
+  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.splits, 4, tm, ts);
+  const EpiCoords ec;
+  FragOffsets fo;
+  fo.init();
+
+  const int32_t row0 = (int32_t)tm * 256;
+  DirectLoader la;
+  la.init([&](uint32_t r) __attribute__((always_inline)) {
+    int32_t rr = row0 + (int32_t)r;
+    rr = rr < a.N ? rr : a.N - 1;
+    return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
+  });
+
+  int32_t lbl[8], rglob[8];
+  float m2[8], d[8];
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    rglob[fm] = row0 + ec.row(fm);
+    lbl[fm] = rglob[fm] < a.N ? a.row_label[rglob[fm]] : -1;
+    m2[fm] = kNegBig;
+    d[fm] = 0.f;
+  }
+
+  const int KT = a.H / Elt<T>::kBK;
+  const int vt0 = (int)ts * a.vt_per_split;
+  const int vt1 = min(vt0 + a.vt_per_split, a.vt_total);
+  f32x4_t acc[8][8];
+  for (int vt = vt0; vt < vt1; ++vt) {
+    const int32_t vrow0 = vt * 256;
+    DirectLoader lb;
+    lb.init([&](uint32_t r) __attribute__((always_inline)) {
+      int32_t v = vrow0 + (int32_t)r;
+      v = v < a.V ? v : a.V - 1;
+      return a.W + (int64_t)v * a.ldw_b;
+    });
+    mainloop<T>(lds, acc, la, lb, KT, fo);
+
+    fwd_tile_update<T, 8>(acc, m2, d, lbl, rglob, vrow0, ec, a);
+  }
+  fwd_final_merge(lds, m2, d, rglob, ts, ec, a);
 }
 
 __global__ void fwd_finalize_kernel(const float* part, const float* xy, int32_t N, int32_t splits,
@@ -240,23 +265,24 @@ __device__ __forceinline__ void store4<float>(char* p, const float (&o)[4]) {
   *reinterpret_cast<f32x4_t*>(p) = f32x4_t{o[0], o[1], o[2], o[3]};
 }
 
-template <typename T, bool kCap>
-__device__ __forceinline__ void recompute_epilogue(const f32x4_t (&acc)[8][8], const RecompArgs& a,
-                                                   const EpiCoords& ec, uint32_t tm, uint32_t tn) {
+template <typename T, int NFN, bool kCap>
+__device__ __forceinline__ void recompute_epilogue(const f32x4_t (&acc)[8][NFN], const RecompArgs& a,
+                                                   const EpiCoordsT<NFN>& ec, int32_t row0,
+                                                   int32_t col0) {
   const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
-  const int32_t ncol0 = (int32_t)tn * 256 + ec.col(0);  // block-local column of fn = 0, r = 0
+  const int32_t ncol0 = col0 + ec.col(0);  // block-local column of fn = 0, r = 0
   int32_t rel[8], rowl[8];
   float lse2[8], g[8];
   bool hit = false;
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
-    rowl[fm] = (int32_t)tm * 256 + ec.row(fm);
+    rowl[fm] = row0 + ec.row(fm);
     const bool rv = rowl[fm] < a.Cn;
     const int32_t rr = rv ? rowl[fm] : 0;
     lse2[fm] = a.lse[rr] * kLog2e;
     g[fm] = rv ? a.grad[(int64_t)a.row_index[rr] * a.gstride] : 0.f;
     rel[fm] = rv ? a.row_label[rr] - a.v0 - ncol0 : -1;
-    hit |= lane_holds(rel[fm]);
+    hit |= lane_holds<NFN>(rel[fm]);
   }
   const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
 #pragma unroll
@@ -264,7 +290,7 @@ __device__ __forceinline__ void recompute_epilogue(const f32x4_t (&acc)[8][8], c
     const bool rv = rowl[fm] < a.Cn;
     char* grow = a.G + (int64_t)rowl[fm] * a.ldg_b;
 #pragma unroll
-    for (int fn = 0; fn < 8; ++fn) {
+    for (int fn = 0; fn < NFN; ++fn) {
       float o[4];
       float xr[4] ={acc[fm][fn][0], acc[fm][fn][1], acc[fm][fn][2], acc[fm][fn][3]};
       round_pair<T>(xr[0], xr[1]);
@@ -298,22 +324,22 @@ MT_GEMM_KERNEL void recompute_kernel(RecompArgs a) {
   fo.init();
   const int32_t row0 = (int32_t)tm * 256;
   DirectLoader la;
-  la.init([&](uint32_t r) {
+  la.init([&](uint32_t r) __attribute__((always_inline)) {
     int32_t rr = row0 + (int32_t)r;
     rr = rr < a.Cn ? rr : a.Cn - 1;
     return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
   });
   const int32_t vrow0 = a.v0 + (int32_t)tn * 256;
   DirectLoader lb;
-  lb.init([&](uint32_t r) {
+  lb.init([&](uint32_t r) __attribute__((always_inline)) {
     int32_t v = vrow0 + (int32_t)r;
     v = v < a.V ? v : a.V - 1;
     return a.W + (int64_t)v * a.ldw_b;
   });
   f32x4_t acc[8][8];
   mainloop<T>(lds, acc, la, lb, a.H / Elt<T>::kBK, fo);
-  if (a.softcap > 0.f) recompute_epilogue<T, true>(acc, a, ec, tm, tn);
-  else recompute_epilogue<T, false>(acc, a, ec, tm, tn);
+  if (a.softcap > 0.f) recompute_epilogue<T, 8, true>(acc, a, ec, row0, (int32_t)tn * 256);
+  else recompute_epilogue<T, 8, false>(acc, a, ec, row0, (int32_t)tn * 256);
 }
 
 // ===========================================================================
@@ -337,25 +363,9 @@ struct DxArgs {
   int32_t tiles_m, tiles_n;
 };
 
-template <typename T>
-MT_GEMM_KERNEL void dx_kernel(DxArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
-  uint32_t tm, tn;
-  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
-  const EpiCoords ec;
-  FragOffsets fo;
-  fo.init();
-  const int32_t row0 = (int32_t)tm * 256;
-  DirectLoader la;
-  la.init([&](uint32_t r) { return a.G + (int64_t)(row0 + (int32_t)r) * a.ldg_b; });
-  const int32_t h0 = (int32_t)tn * 256;
-  TransLoader<T> lb;
-  lb.init(a.W + (int64_t)a.v0 * a.ldw_b + (int64_t)h0 * Elt<T>::kBytes, a.ldw_b, a.V - a.v0,
-          a.H - h0);
-  f32x4_t acc[8][8];
-  const int KT = (a.kv + Elt<T>::kBK - 1) / Elt<T>::kBK;
-  mainloop<T>(lds, acc, la, lb, KT, fo);
-
+template <typename T, int NFN>
+__device__ __forceinline__ void dx_epilogue(const f32x4_t (&acc)[8][NFN], const DxArgs& a,
+                                            const EpiCoordsT<NFN>& ec, int32_t row0, int32_t h0) {
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     const int32_t rowl = row0 + ec.row(fm);
@@ -363,7 +373,7 @@ MT_GEMM_KERNEL void dx_kernel(DxArgs a) {
     float* arow = a.accbuf + (int64_t)rowl * a.ld_acc;
     char* xrow = a.dX + (int64_t)a.row_index[rowl] * a.lddx_b;
 #pragma unroll
-    for (int fn = 0; fn < 8; ++fn) {
+    for (int fn = 0; fn < NFN; ++fn) {
       const int32_t h = h0 + ec.col(fn);
       if (h >= a.H) continue;
       f32x4_t v = acc[fm][fn];
@@ -379,6 +389,27 @@ MT_GEMM_KERNEL void dx_kernel(DxArgs a) {
       }
     }
   }
+}
+
+template <typename T>
+MT_GEMM_KERNEL void dx_kernel(DxArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  uint32_t tm, tn;
+  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
+  const EpiCoords ec;
+  FragOffsets fo;
+  fo.init();
+  const int32_t row0 = (int32_t)tm * 256;
+  DirectLoader la;
+  la.init([&](uint32_t r) __attribute__((always_inline)) { return a.G + (int64_t)(row0 + (int32_t)r) * a.ldg_b; });
+  const int32_t h0 = (int32_t)tn * 256;
+  TransLoader<T> lb;
+  lb.init(a.W + (int64_t)a.v0 * a.ldw_b + (int64_t)h0 * Elt<T>::kBytes, a.ldw_b, a.V - a.v0,
+          a.H - h0);
+  f32x4_t acc[8][8];
+  const int KT = (a.kv + Elt<T>::kBK - 1) / Elt<T>::kBK;
+  mainloop<T>(lds, acc, la, lb, KT, fo);
+  dx_epilogue<T, 8>(acc, a, ec, row0, h0);
 }
 
 // ===========================================================================
@@ -399,6 +430,25 @@ struct DwArgs {
   int32_t tiles_m, tiles_n;
 };
 
+template <int NFN>
+__device__ __forceinline__ void dw_epilogue(const f32x4_t (&acc)[8][NFN], const DwArgs& a,
+                                            const EpiCoordsT<NFN>& ec, int32_t m0, int32_t h0) {
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const int32_t vl = m0 + ec.row(fm);
+    if (vl >= a.cv) continue;
+    float* wrow = a.dW + (int64_t)(a.v0 + vl) * a.lddw;
+#pragma unroll
+    for (int fn = 0; fn < NFN; ++fn) {
+      const int32_t h = h0 + ec.col(fn);
+      if (h >= a.H) continue;
+      f32x4_t v = acc[fm][fn];
+      if (a.accumulate) v += *reinterpret_cast<const f32x4_t*>(wrow + h);
+      *reinterpret_cast<f32x4_t*>(wrow + h) = v;
+    }
+  }
+}
+
 template <typename T>
 MT_GEMM_KERNEL void dw_kernel(DwArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
@@ -412,7 +462,7 @@ MT_GEMM_KERNEL void dw_kernel(DwArgs a) {
   la.init(a.G + (int64_t)m0 * Elt<T>::kBytes, a.ldg_b, a.g_rows, a.g_cols - m0);
   const int32_t h0 = (int32_t)tn * 256;
   DirectLoader lb;
-  lb.init([&](uint32_t r) {
+  lb.init([&](uint32_t r) __attribute__((always_inline)) {
     int32_t h = h0 + (int32_t)r;
     h = h < a.H ? h : a.H - 1;
     return a.XcT + (int64_t)h * a.ldxt_b;
@@ -420,21 +470,7 @@ MT_GEMM_KERNEL void dw_kernel(DwArgs a) {
   f32x4_t acc[8][8];
   const int KT = (a.kt_rows + Elt<T>::kBK - 1) / Elt<T>::kBK;
   mainloop<T>(lds, acc, la, lb, KT, fo);
-
-#pragma unroll
-  for (int fm = 0; fm < 8; ++fm) {
-    const int32_t vl = m0 + ec.row(fm);
-    if (vl >= a.cv) continue;
-    float* wrow = a.dW + (int64_t)(a.v0 + vl) * a.lddw;
-#pragma unroll
-    for (int fn = 0; fn < 8; ++fn) {
-      const int32_t h = h0 + ec.col(fn);
-      if (h >= a.H) continue;
-      f32x4_t v = acc[fm][fn];
-      if (a.accumulate) v += *reinterpret_cast<const f32x4_t*>(wrow + h);
-      *reinterpret_cast<f32x4_t*>(wrow + h) = v;
-    }
-  }
+  dw_epilogue<8>(acc, a, ec, m0, h0);
 }
 
 // ===========================================================================
