@@ -76,6 +76,19 @@ def cpu_baseline(cfg, budget_s: float):
     }
 
 
+def copy_calibration():
+    """One device-to-device copy of exactly 1 GiB: under rocprofv3 --pmc its
+    FETCH_SIZE / WRITE_SIZE readings (KiB per dispatch) against 1048576 KiB
+    give the factor that turns those counters into bytes."""
+    n = 1 << 28
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": 4 * n}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -84,7 +97,13 @@ def main():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (the reference point that scales "
+                         "FETCH_SIZE / WRITE_SIZE counter readings to bytes) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the dW reduce-scatter across ranks is design-only). Run with --gpus 1.",

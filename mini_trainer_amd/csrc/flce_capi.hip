@@ -9,7 +9,7 @@
 
 #include "../../include/mt_flce.h"
 #include "flce_kernels.h"
-#include "flce_kernels3.h"
+#include "flce_kernels4.h"
 
 using namespace mtf;
 
@@ -72,13 +72,14 @@ int check_common(const void* X, const void* W, int64_t T, int64_t H, int64_t V, 
   return MT_OK;
 }
 
-// Output tile shapes: bf16 kernels run 256 x 128 tiles, two workgroups per
-// CU; the fp32 kernels 256 x 256 tiles, one per CU.
+// Output tiles are 256 x 256 with one workgroup per CU (eight waves for the
+// bf16 kernels, four for fp32); threads = workgroup size.
 struct Geometry {
   int64_t tile_m, tile_n, slots;
+  int threads;
 };
 inline Geometry geometry(int es) {
-  return es == 2 ? Geometry{256, 128, 2 * kCUs} : Geometry{256, 256, kCUs};
+  return es == 2 ? Geometry{256, 256, kCUs, kThreads4} : Geometry{256, 256, kCUs, kThreads};
 }
 
 // ---------------------------------------------------------------- forward
@@ -207,7 +208,7 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
   a.part = reinterpret_cast<float*>(ws);
   a.xy = reinterpret_cast<float*>(ws + align_up((size_t)p.splits * n_valid * 2 * sizeof(float)));
   if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL(fwd3_kernel, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
+    hipLaunchKernelGGL(fwd4_kernel, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads4), 0,
                        stream, a);
   else
     hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
@@ -264,8 +265,8 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(recompute3_kernel, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
-                           dim3(kThreads), 0, stream, r);
+        hipLaunchKernelGGL(recompute4_kernel, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
+                           dim3(kThreads4), 0, stream, r);
       else
         hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
                            dim3(kThreads), 0, stream, r);
@@ -290,7 +291,7 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       x.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       x.tiles_n = (int32_t)cdiv(H, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(dx3_kernel, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
+        hipLaunchKernelGGL(dx4_kernel, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads4), 0,
                            stream, x);
       else
         hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
@@ -314,7 +315,7 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
       w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(dw3_kernel, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
+        hipLaunchKernelGGL(dw4_kernel, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads4), 0,
                            stream, w);
       else
         hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,

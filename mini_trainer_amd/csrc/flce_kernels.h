@@ -20,16 +20,20 @@ namespace mtf {
   __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 
 // Output coordinates of this lane's accumulators for a wave tile of
-// 128 rows x (NFN * 16) columns (NFN = 8: 256-wide tiles, 4: 128-wide).
-template <int NFN>
+// 128 rows x (NFN * 16) columns, WC waves across the tile's columns (tile
+// width NFN * 16 * WC: 8 x 16 x 2 for the four-wave fp32 kernels, 4 x 16 x 4
+// for the eight-wave bf16 kernels).
+template <int NFN, int WC = 2>
 struct EpiCoordsT {
   static constexpr int kNF = NFN;
+  static constexpr int kWC = WC;
+  static constexpr int kTileN = NFN * 16 * WC;
   uint32_t lane, wm, wn;
   __device__ __forceinline__ EpiCoordsT() {
     lane = lane_id();
     uint32_t w = wave_id();
-    wm = w >> 1;
-    wn = w & 1u;
+    wm = w / WC;
+    wn = w % WC;
   }
   // Tile-local output row of fragment row fm held by this lane.
   __device__ __forceinline__ int row(int fm) const { return wm * 128 + fm * 16 + (lane & 15u); }
@@ -112,11 +116,11 @@ __device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][NFN], 
 
 // Online-LSE update of one finished 256 x 256 logits tile (vocabulary rows
 // vrow0 .. vrow0 + 255) plus label-logit capture.
-template <typename T, int NFN>
+template <typename T, int NFN, int WC>
 __device__ __forceinline__ void fwd_tile_update(const f32x4_t (&acc)[8][NFN], float (&m2)[8],
                                                 float (&d)[8], const int32_t (&lbl)[8],
                                                 const int32_t (&rglob)[8], int32_t vrow0,
-                                                const EpiCoordsT<NFN>& ec, const FwdArgs& a) {
+                                                const EpiCoordsT<NFN, WC>& ec, const FwdArgs& a) {
   const int32_t ncol0 = vrow0 + ec.col(0);
   int32_t rel[8];
   bool hit = false;
@@ -126,7 +130,7 @@ __device__ __forceinline__ void fwd_tile_update(const f32x4_t (&acc)[8][NFN], fl
     hit |= lane_holds<NFN>(rel[fm]);
   }
   const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
-  const bool tail = vrow0 + NFN * 32 > a.V;
+  const bool tail = vrow0 + EpiCoordsT<NFN, WC>::kTileN > a.V;
   if (a.softcap > 0.f) {
     if (tail) fwd_tile_epilogue<T, NFN, true, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
     else fwd_tile_epilogue<T, NFN, false, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
@@ -136,31 +140,37 @@ __device__ __forceinline__ void fwd_tile_update(const f32x4_t (&acc)[8][NFN], fl
   }
 }
 
-// Merge the four lanes that share a row, then the two waves (wn = 0, 1)
-// through LDS, and write this split's (max, sum) partial of every row.
-template <int NFN>
+// Merge the four lanes that share a row, then the WC waves (wn = 0 .. WC - 1)
+// that share the row through LDS, and write this split's (max, sum) partial
+// of every row.
+template <int NFN, int WC>
 __device__ __forceinline__ void fwd_final_merge(char* lds, float (&m2)[8], float (&d)[8],
                                                 const int32_t (&rglob)[8], uint32_t ts,
-                                                const EpiCoordsT<NFN>& ec, const FwdArgs& a) {
+                                                const EpiCoordsT<NFN, WC>& ec, const FwdArgs& a) {
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     lse_merge(m2[fm], d[fm], __shfl_xor(m2[fm], 16), __shfl_xor(d[fm], 16));
     lse_merge(m2[fm], d[fm], __shfl_xor(m2[fm], 32), __shfl_xor(d[fm], 32));
   }
-  float* red = reinterpret_cast<float*>(lds);
+  float* red = reinterpret_cast<float*>(lds);  // [WC - 1][256 rows][2]
   __syncthreads();
-  if (ec.wn == 1 && (ec.lane >> 4) == 0) {
+  if (ec.wn != 0 && (ec.lane >> 4) == 0) {
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm) {
-      red[ec.row(fm) * 2 + 0] = m2[fm];
-      red[ec.row(fm) * 2 + 1] = d[fm];
+      float* r = red + ((ec.wn - 1) * 256 + ec.row(fm)) * 2;
+      r[0] = m2[fm];
+      r[1] = d[fm];
     }
   }
   __syncthreads();
   if (ec.wn == 0 && (ec.lane >> 4) == 0) {
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm) {
-      lse_merge(m2[fm], d[fm], red[ec.row(fm) * 2 + 0], red[ec.row(fm) * 2 + 1]);
+#pragma unroll
+      for (int w = 0; w < WC - 1; ++w) {
+        const float* r = red + (w * 256 + ec.row(fm)) * 2;
+        lse_merge(m2[fm], d[fm], r[0], r[1]);
+      }
       if (rglob[fm] < a.N) {
         int64_t o = ((int64_t)ts * a.N + rglob[fm]) * 2;
         a.part[o + 0] = m2[fm];
@@ -265,9 +275,9 @@ __device__ __forceinline__ void store4<float>(char* p, const float (&o)[4]) {
   *reinterpret_cast<f32x4_t*>(p) = f32x4_t{o[0], o[1], o[2], o[3]};
 }
 
-template <typename T, int NFN, bool kCap>
+template <typename T, int NFN, bool kCap, int WC>
 __device__ __forceinline__ void recompute_epilogue(const f32x4_t (&acc)[8][NFN], const RecompArgs& a,
-                                                   const EpiCoordsT<NFN>& ec, int32_t row0,
+                                                   const EpiCoordsT<NFN, WC>& ec, int32_t row0,
                                                    int32_t col0) {
   const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
   const int32_t ncol0 = col0 + ec.col(0);  // block-local column of fn = 0, r = 0
@@ -363,9 +373,9 @@ struct DxArgs {
   int32_t tiles_m, tiles_n;
 };
 
-template <typename T, int NFN>
+template <typename T, int NFN, int WC>
 __device__ __forceinline__ void dx_epilogue(const f32x4_t (&acc)[8][NFN], const DxArgs& a,
-                                            const EpiCoordsT<NFN>& ec, int32_t row0, int32_t h0) {
+                                            const EpiCoordsT<NFN, WC>& ec, int32_t row0, int32_t h0) {
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     const int32_t rowl = row0 + ec.row(fm);
@@ -430,9 +440,9 @@ struct DwArgs {
   int32_t tiles_m, tiles_n;
 };
 
-template <int NFN>
+template <int NFN, int WC>
 __device__ __forceinline__ void dw_epilogue(const f32x4_t (&acc)[8][NFN], const DwArgs& a,
-                                            const EpiCoordsT<NFN>& ec, int32_t m0, int32_t h0) {
+                                            const EpiCoordsT<NFN, WC>& ec, int32_t m0, int32_t h0) {
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     const int32_t vl = m0 + ec.row(fm);

@@ -1,28 +1,29 @@
-// bf16 kernels on the two-workgroups-per-CU main loop (flce_gemm3.h): output
-// tiles of 256 x 128, wave tiles 128 x 64.  Arguments, accumulation order and
-// epilogues are those of the generic kernels in flce_kernels.h (the fp32 path).
+// bf16 kernels on the eight-wave main loop (flce_gemm4.h): output tiles of
+// 256 x 256, wave tiles 128 x 64.  Arguments, accumulation order and
+// epilogues are those of the generic kernels in flce_kernels.h (the fp32
+// path).
 #pragma once
 
-#include "flce_gemm3.h"
+#include "flce_gemm4.h"
 #include "flce_kernels.h"
 
 namespace mtf {
 
-#define MT_GEMM3_KERNEL \
-  __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+#define MT_GEMM4_KERNEL \
+  __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 
-typedef EpiCoordsT<4> EpiCoords3;
+typedef EpiCoordsT<4, 4> EpiCoords4;
 
-// Forward: A = gathered X rows (256 tokens), B = W rows (128 vocabulary
-// entries per tile), streaming over this workgroup's vocabulary tiles.
-MT_GEMM3_KERNEL void fwd3_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLds3];
+// Forward: A = gathered X rows (256 valid tokens), B = W rows (256
+// vocabulary entries per tile), streaming over this workgroup's vocabulary
+// tiles with the online (max, sum) state held in registers.
+MT_GEMM4_KERNEL void fwd4_kernel(FwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLds4];
   uint32_t tm, ts;
   grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.splits, 4, tm, ts);
-  const EpiCoords3 ec;
-  const int32_t row0 = (int32_t)tm * kRowsA3;
-  KcOp<kRowsA3> A;
-  KcOp<kRowsB3> B;
+  const EpiCoords4 ec;
+  const int32_t row0 = (int32_t)tm * 256;
+  Kc4 A, B;
   A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
     int32_t rr = row0 + (int32_t)r;
     rr = rr < a.N ? rr : a.N - 1;
@@ -31,21 +32,30 @@ MT_GEMM3_KERNEL void fwd3_kernel(FwdArgs a) {
   A.init_frag(ec.wm * 128);
   B.init_frag(ec.wn * 64);
 
-  int32_t lbl[8], rglob[8];
+  // labels and row ids are re-derived in every tile epilogue (an opaque
+  // copy of the label pointer keeps them from being hoisted into registers
+  // that would stay live across the main loop)
   float m2[8], d[8];
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
-    rglob[fm] = row0 + ec.row(fm);
-    lbl[fm] = rglob[fm] < a.N ? a.row_label[rglob[fm]] : -1;
     m2[fm] = kNegBig;
     d[fm] = 0.f;
   }
+  auto rows_and_labels = [&](int32_t(&rglob)[8], int32_t(&lbl)[8]) __attribute__((always_inline)) {
+    const int32_t* labels = a.row_label;
+    asm volatile("" : "+v"(labels));
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+      rglob[fm] = row0 + ec.row(fm);
+      lbl[fm] = rglob[fm] < a.N ? labels[rglob[fm]] : -1;
+    }
+  };
   const int vt0 = (int)ts * a.vt_per_split;
   const int ntiles = min(vt0 + a.vt_per_split, a.vt_total) - vt0;
-  mainloop3(
-      lds, A, B, a.H / kBK3, ntiles,
+  mainloop4(
+      lds, A, B, a.H / kBK4, ntiles,
       [&](int tile) __attribute__((always_inline)) {
-        const int32_t vrow0 = (vt0 + tile) * kRowsB3;
+        const int32_t vrow0 = (vt0 + tile) * 256;
         B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
           int32_t v = vrow0 + (int32_t)r;
           v = v < a.V ? v : a.V - 1;
@@ -53,22 +63,25 @@ MT_GEMM3_KERNEL void fwd3_kernel(FwdArgs a) {
         });
       },
       [&](int tile, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
-        fwd_tile_update<__bf16, 4>(acc, m2, d, lbl, rglob, (vt0 + tile) * kRowsB3, ec, a);
+        int32_t rglob[8], lbl[8];
+        rows_and_labels(rglob, lbl);
+        fwd_tile_update<__bf16>(acc, m2, d, lbl, rglob, (vt0 + tile) * 256, ec, a);
       });
-  fwd_final_merge<4>(lds, m2, d, rglob, ts, ec, a);
+  int32_t rglob[8], lbl[8];
+  rows_and_labels(rglob, lbl);
+  fwd_final_merge(lds, m2, d, rglob, ts, ec, a);
 }
 
-// Backward step 1: A = X rows of the block (256 tokens), B = W rows (128
-// vocabulary entries); epilogue writes G.
-MT_GEMM3_KERNEL void recompute3_kernel(RecompArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLds3];
+// Backward step 1: A = X rows of the block (256 tokens), B = W rows (256
+// vocabulary entries); the epilogue writes G.
+MT_GEMM4_KERNEL void recompute4_kernel(RecompArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLds4];
   uint32_t tm, tn;
   grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
-  const EpiCoords3 ec;
-  const int32_t row0 = (int32_t)tm * kRowsA3, col0 = (int32_t)tn * kRowsB3;
+  const EpiCoords4 ec;
+  const int32_t row0 = (int32_t)tm * 256, col0 = (int32_t)tn * 256;
   const int32_t vrow0 = a.v0 + col0;
-  KcOp<kRowsA3> A;
-  KcOp<kRowsB3> B;
+  Kc4 A, B;
   A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
     int32_t rr = row0 + (int32_t)r;
     rr = rr < a.Cn ? rr : a.Cn - 1;
@@ -81,7 +94,7 @@ MT_GEMM3_KERNEL void recompute3_kernel(RecompArgs a) {
   });
   A.init_frag(ec.wm * 128);
   B.init_frag(ec.wn * 64);
-  mainloop3(lds, A, B, a.H / kBK3, 1, [](int) __attribute__((always_inline)) {},
+  mainloop4(lds, A, B, a.H / kBK4, 1, [](int) __attribute__((always_inline)) {},
             [&](int, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
               if (a.softcap > 0.f) recompute_epilogue<__bf16, 4, true>(acc, a, ec, row0, col0);
               else recompute_epilogue<__bf16, 4, false>(acc, a, ec, row0, col0);
@@ -89,47 +102,47 @@ MT_GEMM3_KERNEL void recompute3_kernel(RecompArgs a) {
 }
 
 // Backward step 2: A = G rows (256 tokens, K = vocabulary), B = W read
-// K-major (128 hidden columns).
-MT_GEMM3_KERNEL void dx3_kernel(DxArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLds3];
+// K-major (256 hidden columns).
+MT_GEMM4_KERNEL void dx4_kernel(DxArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLds4];
   uint32_t tm, tn;
   grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
-  const EpiCoords3 ec;
-  const int32_t row0 = (int32_t)tm * kRowsA3, h0 = (int32_t)tn * kRowsB3;
-  KcOp<kRowsA3> A;
+  const EpiCoords4 ec;
+  const int32_t row0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
+  Kc4 A;
   A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
     return a.G + (int64_t)(row0 + (int32_t)r) * a.ldg_b;
   });
   A.init_frag(ec.wm * 128);
-  TrOp<kRowsB3> B;
+  Tr4 B;
   B.init(a.W + (int64_t)a.v0 * a.ldw_b + (int64_t)h0 * 2, a.ldw_b, a.V - a.v0, a.H - h0,
          ec.wn * 64);
-  mainloop3(lds, A, B, (a.kv + kBK3 - 1) / kBK3, 1, [](int) __attribute__((always_inline)) {},
+  mainloop4(lds, A, B, (a.kv + kBK4 - 1) / kBK4, 1, [](int) __attribute__((always_inline)) {},
             [&](int, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
-              dx_epilogue<__bf16, 4>(acc, a, ec, row0, h0);
+              dx_epilogue<__bf16>(acc, a, ec, row0, h0);
             });
 }
 
 // Backward step 3: A = G read K-major (256 vocabulary columns, K = tokens),
-// B = X^T rows of the block (128 hidden rows).
-MT_GEMM3_KERNEL void dw3_kernel(DwArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLds3];
+// B = X^T rows of the block (256 hidden rows).
+MT_GEMM4_KERNEL void dw4_kernel(DwArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLds4];
   uint32_t tm, tn;
   grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
-  const EpiCoords3 ec;
-  const int32_t m0 = (int32_t)tm * kRowsA3, h0 = (int32_t)tn * kRowsB3;
-  TrOp<kRowsA3> A;
+  const EpiCoords4 ec;
+  const int32_t m0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
+  Tr4 A;
   A.init(a.G + (int64_t)m0 * 2, a.ldg_b, a.g_rows, a.g_cols - m0, ec.wm * 128);
-  KcOp<kRowsB3> B;
+  Kc4 B;
   B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
     int32_t h = h0 + (int32_t)r;
     h = h < a.H ? h : a.H - 1;
     return a.XcT + (int64_t)h * a.ldxt_b;
   });
   B.init_frag(ec.wn * 64);
-  mainloop3(lds, A, B, (a.kt_rows + kBK3 - 1) / kBK3, 1, [](int) __attribute__((always_inline)) {},
+  mainloop4(lds, A, B, (a.kt_rows + kBK4 - 1) / kBK4, 1, [](int) __attribute__((always_inline)) {},
             [&](int, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
-              dw_epilogue<4>(acc, a, ec, m0, h0);
+              dw_epilogue(acc, a, ec, m0, h0);
             });
 }
 
