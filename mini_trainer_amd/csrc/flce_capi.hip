@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -45,6 +46,24 @@ constexpr int64_t kCUs = 256;
 constexpr size_t kAlign = 256;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Compute units of the current device (cached per device id): the grid size
+// of the persistent GEMM kernels.
+int64_t device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kCUs;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = (int)kCUs;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Grid of a persistent kernel over `tiles` output tiles.
+inline uint32_t persistent_grid(int64_t tiles) { return (uint32_t)std::min(tiles, device_cus()); }
 inline int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 inline size_t align_up(size_t a) { return (a + kAlign - 1) / kAlign * kAlign; }
 
@@ -265,7 +284,7 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(recompute4_kernel, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
+        hipLaunchKernelGGL(recompute4_kernel, dim3(persistent_grid(r.tiles_m * r.tiles_n)),
                            dim3(kThreads4), 0, stream, r);
       else
         hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
@@ -291,7 +310,7 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       x.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       x.tiles_n = (int32_t)cdiv(H, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(dx4_kernel, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads4), 0,
+        hipLaunchKernelGGL(dx4_kernel, dim3(persistent_grid(x.tiles_m * x.tiles_n)), dim3(kThreads4), 0,
                            stream, x);
       else
         hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
@@ -315,7 +334,7 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
       w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(dw4_kernel, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads4), 0,
+        hipLaunchKernelGGL(dw4_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)), dim3(kThreads4), 0,
                            stream, w);
       else
         hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,

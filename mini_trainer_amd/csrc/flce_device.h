@@ -141,10 +141,13 @@ __device__ __forceinline__ void lse_merge(float& m, float& d, float m2, float d2
 
 // Workgroup id -> logical tile id such that the workgroups resident on one
 // XCD (hardware dispatches id i to XCD i % 8) get a contiguous logical range.
+// A bijection of [0, nwg) for any nwg: XCD x < nwg % 8 owns one id more than
+// the others, and the ranges are laid out XCD after XCD.
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t nwg) {
   const uint32_t kXcd = 8;
-  if (nwg % kXcd != 0) return bid;
-  return (bid % kXcd) * (nwg / kXcd) + bid / kXcd;
+  const uint32_t q = nwg / kXcd, r = nwg % kXcd;
+  const uint32_t x = bid % kXcd, i = bid / kXcd;
+  return x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
 }
 
 // Logical tile id -> (tile_m, tile_n) walking groups of `group_m` tile rows

@@ -14,6 +14,24 @@ namespace mtf {
 
 typedef EpiCoordsT<4, 4> EpiCoords4;
 
+// Persistent schedule of the single-pass GEMM kernels: the grid holds
+// P <= #tiles workgroups (one per CU) and workgroup b takes the logical tiles
+// k * P + xcd_remap(b, P), k = 0, 1, ...  In every round the workgroups of one
+// XCD therefore hold a contiguous logical range (neighbouring tiles share
+// operand panels in that XCD's L2), and a tile's epilogue overlaps the first
+// operand loads of the workgroup's next tile.
+struct TileSeq {
+  uint32_t first, stride, total;
+  __device__ __forceinline__ explicit TileSeq(uint32_t total_) : total(total_) {
+    stride = gridDim.x;
+    first = xcd_remap(blockIdx.x, gridDim.x);
+  }
+  __device__ __forceinline__ int count() const {
+    return first < total ? (int)((total - first + stride - 1) / stride) : 0;
+  }
+  __device__ __forceinline__ uint32_t logical(int k) const { return first + (uint32_t)k * stride; }
+};
+
 // Forward: A = gathered X rows (256 valid tokens), B = W rows (256
 // vocabulary entries per tile), streaming over this workgroup's vocabulary
 // tiles with the online (max, sum) state held in registers.
@@ -76,74 +94,92 @@ MT_GEMM4_KERNEL void fwd4_kernel(FwdArgs a) {
 // vocabulary entries); the epilogue writes G.
 MT_GEMM4_KERNEL void recompute4_kernel(RecompArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLds4];
-  uint32_t tm, tn;
-  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
+  const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
   const EpiCoords4 ec;
-  const int32_t row0 = (int32_t)tm * 256, col0 = (int32_t)tn * 256;
-  const int32_t vrow0 = a.v0 + col0;
   Kc4 A, B;
-  A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
-    int32_t rr = row0 + (int32_t)r;
-    rr = rr < a.Cn ? rr : a.Cn - 1;
-    return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
-  });
-  B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
-    int32_t v = vrow0 + (int32_t)r;
-    v = v < a.V ? v : a.V - 1;
-    return a.W + (int64_t)v * a.ldw_b;
-  });
   A.init_frag(ec.wm * 128);
   B.init_frag(ec.wn * 64);
-  mainloop4(lds, A, B, a.H / kBK4, 1, [](int) __attribute__((always_inline)) {},
-            [&](int, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
-              if (a.softcap > 0.f) recompute_epilogue<__bf16, 4, true>(acc, a, ec, row0, col0);
-              else recompute_epilogue<__bf16, 4, false>(acc, a, ec, row0, col0);
-            });
+  mainloop4(
+      lds, A, B, a.H / kBK4, seq.count(),
+      [&](int k) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        const int32_t row0 = (int32_t)tm * 256, vrow0 = a.v0 + (int32_t)tn * 256;
+        A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
+          int32_t rr = row0 + (int32_t)r;
+          rr = rr < a.Cn ? rr : a.Cn - 1;
+          return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
+        });
+        B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
+          int32_t v = vrow0 + (int32_t)r;
+          v = v < a.V ? v : a.V - 1;
+          return a.W + (int64_t)v * a.ldw_b;
+        });
+      },
+      [&](int k, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        const int32_t row0 = (int32_t)tm * 256, col0 = (int32_t)tn * 256;
+        if (a.softcap > 0.f) recompute_epilogue<__bf16, 4, true>(acc, a, ec, row0, col0);
+        else recompute_epilogue<__bf16, 4, false>(acc, a, ec, row0, col0);
+      });
 }
 
 // Backward step 2: A = G rows (256 tokens, K = vocabulary), B = W read
 // K-major (256 hidden columns).
 MT_GEMM4_KERNEL void dx4_kernel(DxArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLds4];
-  uint32_t tm, tn;
-  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
+  const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
   const EpiCoords4 ec;
-  const int32_t row0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
   Kc4 A;
-  A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
-    return a.G + (int64_t)(row0 + (int32_t)r) * a.ldg_b;
-  });
-  A.init_frag(ec.wm * 128);
   Tr4 B;
-  B.init(a.W + (int64_t)a.v0 * a.ldw_b + (int64_t)h0 * 2, a.ldw_b, a.V - a.v0, a.H - h0,
-         ec.wn * 64);
-  mainloop4(lds, A, B, (a.kv + kBK4 - 1) / kBK4, 1, [](int) __attribute__((always_inline)) {},
-            [&](int, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
-              dx_epilogue<__bf16>(acc, a, ec, row0, h0);
-            });
+  A.init_frag(ec.wm * 128);
+  mainloop4(
+      lds, A, B, (a.kv + kBK4 - 1) / kBK4, seq.count(),
+      [&](int k) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        const int32_t row0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
+        A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
+          return a.G + (int64_t)(row0 + (int32_t)r) * a.ldg_b;
+        });
+        B.init(a.W + (int64_t)a.v0 * a.ldw_b + (int64_t)h0 * 2, a.ldw_b, a.V - a.v0, a.H - h0,
+               ec.wn * 64);
+      },
+      [&](int k, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        dx_epilogue<__bf16>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
+      });
 }
 
 // Backward step 3: A = G read K-major (256 vocabulary columns, K = tokens),
 // B = X^T rows of the block (256 hidden rows).
 MT_GEMM4_KERNEL void dw4_kernel(DwArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLds4];
-  uint32_t tm, tn;
-  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.tiles_n, 4, tm, tn);
+  const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
   const EpiCoords4 ec;
-  const int32_t m0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
   Tr4 A;
-  A.init(a.G + (int64_t)m0 * 2, a.ldg_b, a.g_rows, a.g_cols - m0, ec.wm * 128);
   Kc4 B;
-  B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
-    int32_t h = h0 + (int32_t)r;
-    h = h < a.H ? h : a.H - 1;
-    return a.XcT + (int64_t)h * a.ldxt_b;
-  });
   B.init_frag(ec.wn * 64);
-  mainloop4(lds, A, B, (a.kt_rows + kBK4 - 1) / kBK4, 1, [](int) __attribute__((always_inline)) {},
-            [&](int, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
-              dw_epilogue(acc, a, ec, m0, h0);
-            });
+  mainloop4(
+      lds, A, B, (a.kt_rows + kBK4 - 1) / kBK4, seq.count(),
+      [&](int k) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        const int32_t m0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
+        A.init(a.G + (int64_t)m0 * 2, a.ldg_b, a.g_rows, a.g_cols - m0, ec.wm * 128);
+        B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
+          int32_t h = h0 + (int32_t)r;
+          h = h < a.H ? h : a.H - 1;
+          return a.XcT + (int64_t)h * a.ldxt_b;
+        });
+      },
+      [&](int k, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        dw_epilogue(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
+      });
 }
 
 }  // namespace mtf
