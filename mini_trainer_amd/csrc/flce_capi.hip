@@ -44,6 +44,7 @@ int check_launch(const char* what) {
 // are pure functions of the problem size and can run without a device.
 constexpr int64_t kCUs = 256;
 constexpr size_t kAlign = 256;
+constexpr uint64_t kMaxBufferBytes = 0xffffffffull;  // reach of a 32-bit buffer offset
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -88,6 +89,11 @@ int check_common(const void* X, const void* W, int64_t T, int64_t H, int64_t V, 
   if ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(W)) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "X and W must be 16-byte aligned");
   if (!(softcap >= 0.f)) return fail(MT_ERR_INVALID_ARGUMENT, "softcap must be >= 0 (0 = off)");
+  // bf16 kernels address X and W rows with 32-bit buffer offsets
+  if (es == 2 && ((uint64_t)T * ldx * es > kMaxBufferBytes || (uint64_t)V * ldw * es > kMaxBufferBytes))
+    return fail(MT_ERR_UNSUPPORTED,
+                "bf16 X (T x ldx) and W (V x ldw) must each span at most 4 GiB - 1; split the call "
+                "over row ranges");
   return MT_OK;
 }
 
@@ -112,6 +118,12 @@ FwdPlan plan_forward(int64_t n_valid, int64_t V, int es) {
   p.tiles_m = cdiv(n_valid, geo.tile_m);
   p.vt_total = cdiv(V, geo.tile_n);
   if (p.tiles_m == 0) return p;
+  if (es == 2) {
+    // bf16: one partial per (vocabulary tile, row), tiles scheduled persistently
+    p.per = 1;
+    p.splits = p.vt_total;
+    return p;
+  }
   int64_t best_cost = INT64_MAX, best_s = 1;
   for (int64_t s = 1; s <= std::min<int64_t>(p.vt_total, 128); ++s) {
     const int64_t per = cdiv(p.vt_total, s);
@@ -189,6 +201,8 @@ BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t
     for (int64_t nv = 1; nv <= max_nv; ++nv) {
       const int64_t Cv = round_up(cdiv(V, nv), 256);
       const size_t ws = backward_ws(C, Cv, H, V, es);
+      // G and X^T are read through 32-bit buffer offsets
+      if ((uint64_t)C * Cv * es > kMaxBufferBytes || (uint64_t)H * C * es > kMaxBufferBytes) continue;
       if (ws > budget) continue;
       const double cost = backward_cost(N, H, V, C, Cv, es);
       if (cost < best_cost * 0.999) {
@@ -227,8 +241,8 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
   a.part = reinterpret_cast<float*>(ws);
   a.xy = reinterpret_cast<float*>(ws + align_up((size_t)p.splits * n_valid * 2 * sizeof(float)));
   if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL(fwd4_kernel, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads4), 0,
-                       stream, a);
+    hipLaunchKernelGGL(softcap > 0.f ? fwd4_kernel<true> : fwd4_kernel<false>,
+                       dim3(persistent_grid(p.tiles_m * p.vt_total)), dim3(kThreads4), 0, stream, a);
   else
     hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
                        stream, a);
@@ -284,7 +298,8 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(recompute4_kernel, dim3(persistent_grid(r.tiles_m * r.tiles_n)),
+        hipLaunchKernelGGL(softcap > 0.f ? recompute4_kernel<true> : recompute4_kernel<false>,
+                           dim3(persistent_grid(r.tiles_m * r.tiles_n)),
                            dim3(kThreads4), 0, stream, r);
       else
         hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)),

@@ -68,13 +68,31 @@ __device__ __forceinline__ void wait_vm0() {
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 }
 
+// Raw buffer resource over `bytes` bytes from `base` (stride 0, dword 3 =
+// the gfx9 raw-buffer format word).  Operand loads go through buffer
+// instructions so that a lane's address is a 32-bit offset (one VGPR instead
+// of two) and the K advance of a stage is a scalar offset; every access is
+// kept in range by the callers, the resource bound only backs that up.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+constexpr uint32_t kWholeRange = 0xffffffffu;
+
+// 16-byte LDS DMA of one lane: LDS[dst + 16 lane] = mem[rsrc + voff + soff].
+__device__ __forceinline__ void dma16(rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)dst, 16, voff, soff, 0, 0);
+}
+
 // Operand whose rows are contiguous along K.  The 32 KiB tile is filled by
 // 32 DMA instructions of 1 KiB (4 per wave); lane l of instruction q lands at
 // q * 1024 + 16 l, so the lane -> (row, chunk) assignment is the inverse of
 // tile_off().
 struct Kc4 {
   static constexpr bool kTr = false;
-  const char* p[4];
+  rsrc_t rsrc;
+  uint32_t off[4];
   uint32_t frag[2];  // LDS offset of this lane's fragment 0 for K halves 0, 1
 
   __device__ __forceinline__ static uint32_t row_of(uint32_t i) {
@@ -85,11 +103,12 @@ struct Kc4 {
     const uint32_t l = lane_id(), q = wave_id() * 4 + i;
     return (l & 7u) ^ ((q & 1u) * 4 + (l >> 4));
   }
-  // row_ptr(r) = byte address of K element 0 of tile row r.
-  template <class RowPtr>
-  __device__ __forceinline__ void set_rows(RowPtr row_ptr) {
+  // row_off(r) = byte offset from the resource base of K element 0 of tile row r.
+  template <class RowOff>
+  __device__ __forceinline__ void set_rows(rsrc_t r, RowOff row_off) {
+    rsrc = r;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) p[i] = row_ptr(row_of(i)) + chunk_of(i) * 16u;
+    for (uint32_t i = 0; i < 4; ++i) off[i] = row_off(row_of(i)) + chunk_of(i) * 16u;
   }
   // wave_row0: first tile row of this wave's fragments.
   __device__ __forceinline__ void init_frag(uint32_t wave_row0) {
@@ -99,11 +118,8 @@ struct Kc4 {
   }
   __device__ __forceinline__ void issue(char* tile, int kt) const {
     const uint32_t w = wave_id();
-    const int64_t koff = (int64_t)kt * 128;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(p[i] + koff, (lds_void_t*)(tile + (w * 4 + i) * 1024u), 16,
-                                       0, 0);
+    for (uint32_t i = 0; i < 4; ++i) dma16(rsrc, tile + (w * 4 + i) * 1024u, off[i], (uint32_t)kt * 128u);
   }
   __device__ __forceinline__ u32x4_t read(const char* tile, int kk, int f) const {
     return lds_read16(tile, frag[kk] + (uint32_t)f * 2048u);
@@ -115,20 +131,21 @@ struct Kc4 {
 // K row 2 q + (l >> 5) and so loads global chunk (l & 31) ^ tr4_swz(k).
 struct Tr4 {
   static constexpr bool kTr = true;
-  const char* base;
-  int64_t ld_b;
+  rsrc_t rsrc;
+  uint32_t base, ld_b;
   int32_t k_limit;
   uint32_t moff[4];
   uint32_t krow[4];
   uint32_t fbase[2][2], fxor[2][2];  // [kk][h]
 
-  // base: (K row 0, column 0 of the tile); k_limit: K rows that exist (rows
-  // at or beyond it read row k_limit - 1, whose products the caller
-  // discards or multiplies by zero); m_valid: tile columns that exist (the
-  // others read column 0 and are discarded later); wave_col0: first tile
-  // column of this wave's fragments.
-  __device__ __forceinline__ void init(const char* base_, int64_t ld_b_, int32_t k_limit_,
+  // r, base: resource and byte offset of (K row 0, column 0) of the tile;
+  // k_limit: K rows that exist (rows at or beyond it read row k_limit - 1,
+  // whose products the caller discards or multiplies by zero); m_valid: tile
+  // columns that exist (the others read column 0 and are discarded later);
+  // wave_col0: first tile column of this wave's fragments.
+  __device__ __forceinline__ void init(rsrc_t r, uint32_t base_, uint32_t ld_b_, int32_t k_limit_,
                                        int32_t m_valid, uint32_t wave_col0) {
+    rsrc = r;
     base = base_;
     ld_b = ld_b_;
     k_limit = k_limit_;
@@ -160,8 +177,7 @@ struct Tr4 {
     for (uint32_t i = 0; i < 4; ++i) {
       int32_t k = kt * kBK4 + (int32_t)krow[i];
       k = k < k_limit ? k : k_limit - 1;
-      __builtin_amdgcn_global_load_lds(base + (int64_t)k * ld_b + moff[i],
-                                       (lds_void_t*)(tile + (w * 4 + i) * 1024u), 16, 0, 0);
+      dma16(rsrc, tile + (w * 4 + i) * 1024u, base + (uint32_t)k * ld_b + moff[i], 0u);
     }
   }
   // Two transposing reads into one 128-bit register tuple (inline asm; the

@@ -67,7 +67,9 @@ struct FwdArgs {
   float* xy;    // [N] label logit
 };
 
-template <typename T, int NFN, bool kTail, bool kCap>
+// Columns at or beyond V are masked with a select (no separate tail variant:
+// one code path keeps the epilogue's register footprint small).
+template <typename T, int NFN, bool kCap>
 __device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][NFN], float (&m2)[8],
                                                   float (&d)[8], const int32_t (&rel)[8],
                                                   const int32_t (&rglob)[8], int32_t ncol0,
@@ -87,7 +89,7 @@ __device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][NFN], 
       for (int r = 0; r < 4; ++r) {
         float x = v[fn][r];
         if (kCap) x = cap * tanh_approx(x * inv_cap);
-        if (kTail && ncol0 + fn * 16 + r >= a.V) x = -INFINITY;
+        x = ncol0 + fn * 16 + r < a.V ? x : -INFINITY;
         v[fn][r] = x;
         tmax = fmaxf(tmax, x);
       }
@@ -116,7 +118,7 @@ __device__ __forceinline__ void fwd_tile_epilogue(const f32x4_t (&acc)[8][NFN], 
 
 // Online-LSE update of one finished 256 x 256 logits tile (vocabulary rows
 // vrow0 .. vrow0 + 255) plus label-logit capture.
-template <typename T, int NFN, int WC>
+template <typename T, bool kCap, int NFN, int WC>
 __device__ __forceinline__ void fwd_tile_update(const f32x4_t (&acc)[8][NFN], float (&m2)[8],
                                                 float (&d)[8], const int32_t (&lbl)[8],
                                                 const int32_t (&rglob)[8], int32_t vrow0,
@@ -130,14 +132,7 @@ __device__ __forceinline__ void fwd_tile_update(const f32x4_t (&acc)[8][NFN], fl
     hit |= lane_holds<NFN>(rel[fm]);
   }
   const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
-  const bool tail = vrow0 + EpiCoordsT<NFN, WC>::kTileN > a.V;
-  if (a.softcap > 0.f) {
-    if (tail) fwd_tile_epilogue<T, NFN, true, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
-    else fwd_tile_epilogue<T, NFN, false, true>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
-  } else {
-    if (tail) fwd_tile_epilogue<T, NFN, true, false>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
-    else fwd_tile_epilogue<T, NFN, false, false>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
-  }
+  fwd_tile_epilogue<T, NFN, kCap>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
 }
 
 // Merge the four lanes that share a row, then the WC waves (wn = 0 .. WC - 1)
@@ -221,7 +216,8 @@ MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
     });
     mainloop<T>(lds, acc, la, lb, KT, fo);
 
-    fwd_tile_update<T, 8>(acc, m2, d, lbl, rglob, vrow0, ec, a);
+    if (a.softcap > 0.f) fwd_tile_update<T, true>(acc, m2, d, lbl, rglob, vrow0, ec, a);
+    else fwd_tile_update<T, false>(acc, m2, d, lbl, rglob, vrow0, ec, a);
   }
   fwd_final_merge(lds, m2, d, rglob, ts, ec, a);
 }

@@ -32,66 +32,61 @@ struct TileSeq {
   __device__ __forceinline__ uint32_t logical(int k) const { return first + (uint32_t)k * stride; }
 };
 
-// Forward: A = gathered X rows (256 valid tokens), B = W rows (256
-// vocabulary entries per tile), streaming over this workgroup's vocabulary
-// tiles with the online (max, sum) state held in registers.
+// Forward: one 256 x 256 logits tile per work unit (A = gathered X rows, B =
+// W rows), persistent over the (row tile, vocabulary tile) grid.  The
+// epilogue reduces the tile to a (max, sum) partial per row -- lanes that
+// share a row through shuffles, the four wave columns through a 6 KiB LDS
+// region beside the stage buffers -- and writes it to part[vocab tile][row];
+// the lane that holds a row's label logit writes it to xy[row].  Nothing is
+// carried in registers from one tile to the next.
+constexpr int kFwdRed4 = 3 * 256 * 2 * (int)sizeof(float);
+
+template <bool kCap>
 MT_GEMM4_KERNEL void fwd4_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLds4];
-  uint32_t tm, ts;
-  grouped_tile(xcd_remap(blockIdx.x, gridDim.x), a.tiles_m, a.splits, 4, tm, ts);
+  __shared__ __attribute__((aligned(1024))) char lds[kLds4 + kFwdRed4];
+  const TileSeq seq((uint32_t)(a.tiles_m * a.vt_total));
   const EpiCoords4 ec;
-  const int32_t row0 = (int32_t)tm * 256;
   Kc4 A, B;
-  A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
-    int32_t rr = row0 + (int32_t)r;
-    rr = rr < a.N ? rr : a.N - 1;
-    return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
-  });
   A.init_frag(ec.wm * 128);
   B.init_frag(ec.wn * 64);
-
-  // labels and row ids are re-derived in every tile epilogue (an opaque
-  // copy of the label pointer keeps them from being hoisted into registers
-  // that would stay live across the main loop)
-  float m2[8], d[8];
-#pragma unroll
-  for (int fm = 0; fm < 8; ++fm) {
-    m2[fm] = kNegBig;
-    d[fm] = 0.f;
-  }
-  auto rows_and_labels = [&](int32_t(&rglob)[8], int32_t(&lbl)[8]) __attribute__((always_inline)) {
-    const int32_t* labels = a.row_label;
-    asm volatile("" : "+v"(labels));
-#pragma unroll
-    for (int fm = 0; fm < 8; ++fm) {
-      rglob[fm] = row0 + ec.row(fm);
-      lbl[fm] = rglob[fm] < a.N ? labels[rglob[fm]] : -1;
-    }
-  };
-  const int vt0 = (int)ts * a.vt_per_split;
-  const int ntiles = min(vt0 + a.vt_per_split, a.vt_total) - vt0;
   mainloop4(
-      lds, A, B, a.H / kBK4, ntiles,
-      [&](int tile) __attribute__((always_inline)) {
-        const int32_t vrow0 = (vt0 + tile) * 256;
-        B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
+      lds, A, B, a.H / kBK4, seq.count(),
+      [&](int k) __attribute__((always_inline)) {
+        uint32_t tm, tv;
+        grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, 4, tm, tv);
+        const int32_t row0 = (int32_t)tm * 256, vrow0 = (int32_t)tv * 256;
+        A.set_rows(make_rsrc(a.X, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+          int32_t rr = row0 + (int32_t)r;
+          rr = rr < a.N ? rr : a.N - 1;
+          return (uint32_t)a.row_index[rr] * (uint32_t)a.ldx_b;
+        });
+        B.set_rows(make_rsrc(a.W, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t v = vrow0 + (int32_t)r;
           v = v < a.V ? v : a.V - 1;
-          return a.W + (int64_t)v * a.ldw_b;
+          return (uint32_t)v * (uint32_t)a.ldw_b;
         });
       },
-      [&](int tile, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+        uint32_t tm, tv;
+        grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, 4, tm, tv);
+        const int32_t row0 = (int32_t)tm * 256;
         int32_t rglob[8], lbl[8];
-        rows_and_labels(rglob, lbl);
-        fwd_tile_update<__bf16>(acc, m2, d, lbl, rglob, (vt0 + tile) * 256, ec, a);
+        float m2[8], d[8];
+#pragma unroll
+        for (int fm = 0; fm < 8; ++fm) {
+          rglob[fm] = row0 + ec.row(fm);
+          lbl[fm] = rglob[fm] < a.N ? a.row_label[rglob[fm]] : -1;
+          m2[fm] = kNegBig;
+          d[fm] = 0.f;
+        }
+        fwd_tile_update<__bf16, kCap>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
+        fwd_final_merge(lds + kLds4, m2, d, rglob, tv, ec, a);
       });
-  int32_t rglob[8], lbl[8];
-  rows_and_labels(rglob, lbl);
-  fwd_final_merge(lds, m2, d, rglob, ts, ec, a);
 }
 
 // Backward step 1: A = X rows of the block (256 tokens), B = W rows (256
 // vocabulary entries); the epilogue writes G.
+template <bool kCap>
 MT_GEMM4_KERNEL void recompute4_kernel(RecompArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLds4];
   const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
@@ -105,23 +100,22 @@ MT_GEMM4_KERNEL void recompute4_kernel(RecompArgs a) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t row0 = (int32_t)tm * 256, vrow0 = a.v0 + (int32_t)tn * 256;
-        A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
+        A.set_rows(make_rsrc(a.X, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t rr = row0 + (int32_t)r;
           rr = rr < a.Cn ? rr : a.Cn - 1;
-          return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
+          return (uint32_t)a.row_index[rr] * (uint32_t)a.ldx_b;
         });
-        B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
+        B.set_rows(make_rsrc(a.W, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t v = vrow0 + (int32_t)r;
           v = v < a.V ? v : a.V - 1;
-          return a.W + (int64_t)v * a.ldw_b;
+          return (uint32_t)v * (uint32_t)a.ldw_b;
         });
       },
       [&](int k, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t row0 = (int32_t)tm * 256, col0 = (int32_t)tn * 256;
-        if (a.softcap > 0.f) recompute_epilogue<__bf16, 4, true>(acc, a, ec, row0, col0);
-        else recompute_epilogue<__bf16, 4, false>(acc, a, ec, row0, col0);
+        recompute_epilogue<__bf16, 4, kCap>(acc, a, ec, row0, col0);
       });
 }
 
@@ -140,11 +134,11 @@ MT_GEMM4_KERNEL void dx4_kernel(DxArgs a) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t row0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
-        A.set_rows([&](uint32_t r) __attribute__((always_inline)) {
-          return a.G + (int64_t)(row0 + (int32_t)r) * a.ldg_b;
+        A.set_rows(make_rsrc(a.G, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+          return (uint32_t)(row0 + (int32_t)r) * (uint32_t)a.ldg_b;
         });
-        B.init(a.W + (int64_t)a.v0 * a.ldw_b + (int64_t)h0 * 2, a.ldw_b, a.V - a.v0, a.H - h0,
-               ec.wn * 64);
+        B.init(make_rsrc(a.W, kWholeRange), (uint32_t)a.v0 * (uint32_t)a.ldw_b + (uint32_t)h0 * 2u,
+               (uint32_t)a.ldw_b, a.V - a.v0, a.H - h0, ec.wn * 64);
       },
       [&](int k, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
         uint32_t tm, tn;
@@ -168,11 +162,12 @@ MT_GEMM4_KERNEL void dw4_kernel(DwArgs a) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t m0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
-        A.init(a.G + (int64_t)m0 * 2, a.ldg_b, a.g_rows, a.g_cols - m0, ec.wm * 128);
-        B.set_rows([&](uint32_t r) __attribute__((always_inline)) {
+        A.init(make_rsrc(a.G, kWholeRange), (uint32_t)m0 * 2u, (uint32_t)a.ldg_b, a.g_rows,
+               a.g_cols - m0, ec.wm * 128);
+        B.set_rows(make_rsrc(a.XcT, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t h = h0 + (int32_t)r;
           h = h < a.H ? h : a.H - 1;
-          return a.XcT + (int64_t)h * a.ldxt_b;
+          return (uint32_t)h * (uint32_t)a.ldxt_b;
         });
       },
       [&](int k, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
