@@ -7,9 +7,11 @@ sum + .item() sync, and the backward with the uniform upstream gradient
 named configuration, resident in HBM before timing starts.
 
 Prints ONE JSON line (driver contract) with, in addition:
-  roofline      the dominant kernel (fwd_kernel: 2*H*V*N MFMA flops per
+  roofline      the dominant kernel (fwd4_kernel: 2*H*V*N MFMA flops per
                 launch) timed with HIP events through the C ABI on the
-                stream it is launched on, against the bf16 dense peak
+                stream it is launched on, against the bf16 dense peak;
+                traffic = HBM bytes per launch from the committed rocprofv3
+                FETCH_SIZE / WRITE_SIZE summary (profiles/)
   cpu_baseline  the reference torch path (oracle/torch_path.py) on the host
                 cores over a bounded prefix of the same batch
   north_star    6*H*V*N / t_step against the same peak, extra HBM, etc.
@@ -74,6 +76,21 @@ def cpu_baseline(cfg, budget_s: float):
                    f"config {cfg.key} (T x V logits in 1024-row chunks), {t_total:.1f} s, "
                    f"torch threads={threads}, host cpus={os.cpu_count()}"),
     }
+
+
+def measured_traffic(key: int, kernel: str):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload (calibrated
+    against a 1 GiB device copy), or None when no summary covers it."""
+    path = os.path.join(ROOT, "profiles", f"flce_cfg{key}_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel:
+        return None
+    return t.get("traffic_bytes")
 
 
 def copy_calibration():
@@ -189,6 +206,9 @@ def main():
     peak_flops = PEAK_BF16 if cfg.dtype == torch.bfloat16 else PEAK_FP32
     C, Cv, bws = backward_plan(T, n, H, V, cfg.dtype)
 
+    fwd_kernel_name = "fwd4_kernel" if cfg.dtype == torch.bfloat16 else "fwd_kernel"
+    traffic = measured_traffic(cfg.key, fwd_kernel_name)
+
     alg_flops = 6.0 * H * V * N_total
     out = {
         "metric": METRIC,
@@ -210,12 +230,12 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "fwd_kernel (mt_flce_forward)",
+            "kernel": f"{fwd_kernel_name} (mt_flce_forward)",
             "achieved": fwd_flops / fwd_s / 1e12,
             "peak": peak_flops / 1e12,
             "unit": "TFLOP/s",
             "frac": fwd_flops / fwd_s / peak_flops,
-            "traffic": None,
+            "traffic": traffic,
             "ms_per_launch": fwd_s * 1e3,
             "flops_per_launch": fwd_flops,
         },

@@ -182,17 +182,25 @@ def test_prepare_bit_exact(gpu, shift):
 def test_segment_sums(gpu):
     rng = np.random.default_rng(6)
     L = rng.integers(1, 300, 77)
+    L[[3, 40, 76]] = 0  # empty samples, the last one included
     T = int(L.sum())
     cu = np.concatenate([[0], np.cumsum(L)]).astype(np.int32)
     loss = rng.random(T).astype(np.float32)
     tgt = rng.integers(0, 10, T)
     tgt[rng.random(T) < 0.5] = -100
+    tgt[cu[10]:cu[11]] = -100  # a fully masked sample (config 5 has five)
+    loss[tgt == -100] = 0.0
     sl, sc = per_sample_loss_sums(torch.from_numpy(loss).to(gpu), torch.from_numpy(tgt).to(gpu),
                                   torch.from_numpy(cu).to(gpu))
     esl, esc, st = ref.segment_sum(loss, tgt, cu)
     assert st == 0
     assert np.array_equal(sc.cpu().numpy(), esc)
     np.testing.assert_allclose(sl.cpu().numpy(), esl, rtol=1e-5)
+    assert sc[3].item() == 0 and sc[40].item() == 0 and sc[76].item() == 0 and sc[10].item() == 0
+    assert sl[10].item() == 0.0
+    # a checksum of checksums: the per-sample sums add up to the whole-batch sum
+    np.testing.assert_allclose(sl.sum().item(), float(loss.astype(np.float64).sum()), rtol=1e-5)
+    assert int(sc.sum().item()) == int((tgt != -100).sum())
     bad = cu.copy()
     bad[5], bad[6] = bad[6], bad[5]
     with pytest.raises(ValueError):
