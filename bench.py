@@ -1,15 +1,20 @@
 """Benchmark of the fused LM-head linear + per-token cross-entropy on one MI355X.
 
 One step = the hot path of one training minibatch as train.py:97-104 drives
-it: forward (valid-row compaction + fused GEMM/online-LSE), the caller's
-sum + .item() sync, and the backward with the uniform upstream gradient
-1/N into an fp32 dW accumulator.  Inputs are seeded synthetic tensors of the
-named configuration, resident in HBM before timing starts.
+it: forward, the caller's sum + .item() sync, and the backward with the
+uniform upstream gradient 1/N into an fp32 dW accumulator.  train.py knows
+that scale before the forward, so the step passes it as grad_scale and bf16
+runs the fused path (each logits tile computed once; dX and dW formed during
+the forward, the backward checks the gradient it receives); the general path
+(forward keeps lse only, backward recomputes the logits) is timed beside it.
+Inputs are seeded synthetic tensors of the named configuration, resident in
+HBM before timing starts.
 
 Prints ONE JSON line (driver contract) with, in addition:
-  roofline      the dominant kernel (fwd4_kernel: 2*H*V*N MFMA flops per
-                launch) timed with HIP events through the C ABI on the
-                stream it is launched on, against the bf16 dense peak;
+  roofline      the logits GEMM (fwd4_kernel: 2*H*V*N MFMA flops per
+                launch, one launch over all valid rows through
+                mt_flce_forward) timed with HIP events through the C ABI on
+                the stream it is launched on, against the bf16 dense peak;
                 traffic = HBM bytes per launch from the committed rocprofv3
                 FETCH_SIZE / WRITE_SIZE summary (profiles/)
   cpu_baseline  the reference torch path (oracle/torch_path.py) on the host
@@ -144,15 +149,34 @@ def main():
     N_total = sum(n_valid)
     T_total = T * len(data)
 
-    def step():
-        # one optimizer step's worth of minibatches (config 5: 4 grad-accum minibatches)
-        for X, y in data:
-            Xl = X.detach().requires_grad_(True)
-            loss = fused_linear_cross_entropy(Xl, Wl, y, dw_accumulator=dW)
-            s = loss.float().sum()
-            s.item()  # the caller's sync (train.py:99)
-            torch.autograd.grad(s * (1.0 / N_total), (Xl,))
+    scale = 1.0 / N_total  # train.py:102 with world_size 1: known before the forward
 
+    def make_step(fused: bool):
+        def step():
+            # one optimizer step's worth of minibatches (config 5: 4 grad-accum minibatches)
+            for X, y in data:
+                Xl = X.detach().requires_grad_(True)
+                loss = fused_linear_cross_entropy(Xl, Wl, y, dw_accumulator=dW,
+                                                  grad_scale=scale if fused else None)
+                s = loss.float().sum()
+                s.item()  # the caller's sync (train.py:99)
+                torch.autograd.grad(s * scale, (Xl,))
+        return step
+
+    def timed(step):
+        for _ in range(args.warmup):
+            step()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(args.steps):
+            step()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / args.steps
+
+    fused = cfg.dtype == torch.bfloat16
+    step = make_step(fused)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -168,15 +192,11 @@ def main():
     extra = peak - base - outputs
     budget = 0.05 * T * V * es
 
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record()
-    for _ in range(args.steps):
-        step()
-    ev1.record()
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms = timed(step)
     t_step = ms / 1e3
+    # the general path (gradient not known at the forward: recompute in the backward)
+    ms_general = timed(make_step(False)) if fused else ms
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     # dominant kernel: fwd_kernel via mt_flce_forward on the current stream
     X, y = data[0]
@@ -244,6 +264,10 @@ def main():
             "achieved_TFLOPs": alg_flops / t_step / 1e12,
             "frac_of_peak": alg_flops / t_step / peak_flops,
             "dense_convention_frac": 6.0 * H * V * T_total / t_step / peak_flops,
+            "path": ("fused: grad_scale = 1/N passed at the forward (mt_flce_fused, 6HVN)"
+                     if fused else "general (mt_flce_forward + mt_flce_backward, 8HVN)"),
+            "general_path_ms_per_step": ms_general,
+            "general_path_frac_of_peak": alg_flops / (ms_general / 1e3) / peak_flops,
             "extra_hbm_GB": extra / 1e9,
             "extra_hbm_budget_GB": budget / 1e9,
             "peak_memory_GB": peak / 1e9,

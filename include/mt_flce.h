@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MT_FLCE_ABI_VERSION 1
+#define MT_FLCE_ABI_VERSION 2
 
 typedef struct ihipStream_t* mt_stream_t; /* == hipStream_t */
 
@@ -135,6 +135,39 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H,
                      int64_t lddw, int accumulate_dW, int64_t chunk_rows,
                      int64_t chunk_vocab, void* workspace,
                      size_t workspace_bytes, mt_stream_t stream);
+
+/*
+ * Fused forward + backward plan (bf16 only): the largest chunk of valid rows
+ * (multiple of 256) whose workspace -- the chunk's bf16 logits [chunk,
+ * round_up(V, 256)], the (max, sum) partials, the label logits and the chunk's
+ * X^T -- fits budget_bytes (0 = default: 5% of T*V*2), then evened out over
+ * the chunks.  Writes the chunk size and workspace size.
+ */
+int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
+                       int dtype, size_t budget_bytes, int64_t* chunk_rows,
+                       size_t* workspace_bytes);
+
+/*
+ * Fused forward + backward for a caller that knows the upstream gradient of
+ * every token before the forward -- as train.py:97-104 does: it scales the
+ * summed loss by world_size / batch_num_loss_counted_tokens, a number fixed
+ * by the batch.  Produces loss and lse as mt_flce_forward, dX and dW as
+ * mt_flce_backward would for that gradient, with 6*H*V*n_valid flops (each
+ * logits tile is computed once and kept in bf16 for its chunk, the structure
+ * of LIGER:ops/fused_linear_cross_entropy.py::fused_linear_cross_entropy_forward
+ * reached from none_reduction_losses.py:16-23, which computes the gradients
+ * in its forward and rescales them in its backward).
+ *   grad_loss / grad_stride  as in mt_flce_backward
+ *   chunk_rows / workspace   from mt_flce_fused_plan
+ * bf16 only (MT_ERR_UNSUPPORTED otherwise).
+ */
+int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
+                  int64_t ldx, int64_t ldw, int dtype, float softcap,
+                  const int32_t* row_index, const int32_t* row_label,
+                  int64_t n_valid, const float* grad_loss, int64_t grad_stride,
+                  float* loss, float* lse, void* dX, int64_t lddx, float* dW,
+                  int64_t lddw, int accumulate_dW, int64_t chunk_rows,
+                  void* workspace, size_t workspace_bytes, mt_stream_t stream);
 
 /*
  * Per-sample sums over a packed batch (no counterpart in the reference, which

@@ -240,14 +240,18 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
   a.vt_per_split = (int32_t)p.per;
   a.part = reinterpret_cast<float*>(ws);
   a.xy = reinterpret_cast<float*>(ws + align_up((size_t)p.splits * n_valid * 2 * sizeof(float)));
-  if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL(softcap > 0.f ? fwd4_kernel<true> : fwd4_kernel<false>,
-                       dim3(persistent_grid(p.tiles_m * p.vt_total)), dim3(kThreads4), 0, stream, a);
-  else
+  a.S = nullptr;
+  a.lds_b = 0;
+  if constexpr (sizeof(T) == 2) {
+    void (*kern)(FwdArgs) = softcap > 0.f ? fwd4_kernel<true, false> : fwd4_kernel<false, false>;
+    hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * p.vt_total)), dim3(kThreads4), 0,
+                       stream, a);
+  } else {
     hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
                        stream, a);
+  }
   MT_TRY(check_launch("fwd_kernel"));
-  hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(n_valid, 256)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(n_valid, 4)), dim3(256), 0, stream,
                      a.part, a.xy, a.N, a.splits, row_index, loss, lse);
   return check_launch("fwd_finalize_kernel");
 }
@@ -356,6 +360,136 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
                            stream, w);
       MT_TRY(check_launch("dw_kernel"));
     }
+  }
+  return MT_OK;
+}
+
+// ------------------------------------------------------------------ fused
+// Fused forward + backward (bf16): per chunk of C valid rows, the logits
+// S [C, Vpad] are written once (bf16), turned into G in place once the rows'
+// lse is known, and consumed by dX = G W (complete, K = V) and
+// dW (+)= G^T X_chunk.  6 H V N flops, no recompute.
+struct FusedPlan {
+  int64_t C = 0;
+  size_t ws = 0;
+};
+
+inline int64_t vocab_pad(int64_t V) { return round_up(V, 256); }
+
+size_t fused_ws(int64_t C, int64_t H, int64_t V) {
+  if (C == 0) return 0;
+  const int64_t vt = cdiv(V, 256);
+  return align_up((size_t)C * vocab_pad(V) * 2) + align_up((size_t)vt * C * 2 * sizeof(float)) +
+         align_up((size_t)C * sizeof(float)) + align_up((size_t)H * C * 2);
+}
+
+FusedPlan plan_fused(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) {
+  FusedPlan p;
+  if (N <= 0) return p;
+  if (budget == 0) budget = (size_t)((double)T * V * 2 * 0.05);
+  int64_t best = 256;
+  for (int64_t C = 256; C <= round_up(N, 256); C += 256) {
+    if (fused_ws(C, H, V) > budget) break;
+    if ((uint64_t)C * vocab_pad(V) * 2 > kMaxBufferBytes || (uint64_t)H * C * 2 > kMaxBufferBytes) break;
+    best = C;
+  }
+  // equal chunks: same number of chunks, the smallest 256-multiple that covers N
+  const int64_t nch = cdiv(N, best);
+  p.C = round_up(cdiv(N, nch), 256);
+  p.ws = fused_ws(p.C, H, V);
+  return p;
+}
+
+int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx, int64_t ldw,
+                 float softcap, const int32_t* row_index, const int32_t* row_label, int64_t N,
+                 const float* grad, int64_t gstride, float* loss, float* lse, void* dX,
+                 int64_t lddx, float* dW, int64_t lddw, int accumulate, int64_t C, char* ws,
+                 hipStream_t stream) {
+  const int64_t Vp = vocab_pad(V), vt = cdiv(V, 256);
+  char* S = ws;
+  float* part = reinterpret_cast<float*>(ws + align_up((size_t)C * Vp * 2));
+  float* xy = reinterpret_cast<float*>(reinterpret_cast<char*>(part) +
+                                       align_up((size_t)vt * C * 2 * sizeof(float)));
+  char* XcT = reinterpret_cast<char*>(xy) + align_up((size_t)C * sizeof(float));
+  const int64_t lds_b = Vp * 2, ldxt_b = C * 2;
+  for (int64_t c0 = 0; c0 < N; c0 += C) {
+    const int64_t cn = std::min(C, N - c0);
+    const int64_t tm = cdiv(cn, 256), cn_pad = tm * 256;
+    hipLaunchKernelGGL(gather_t_kernel<__bf16>, dim3((uint32_t)(cn_pad / 64), (uint32_t)cdiv(H, 64)),
+                       dim3(256), 0, stream, static_cast<const char*>(X), ldx * 2, row_index + c0,
+                       (int32_t)cn, (int32_t)H, XcT, ldxt_b);
+    MT_TRY(check_launch("gather_t_kernel"));
+
+    FwdArgs a;
+    a.X = static_cast<const char*>(X);
+    a.W = static_cast<const char*>(W);
+    a.ldx_b = ldx * 2;
+    a.ldw_b = ldw * 2;
+    a.H = (int32_t)H;
+    a.V = (int32_t)V;
+    a.N = (int32_t)cn;
+    a.row_index = row_index + c0;
+    a.row_label = row_label + c0;
+    a.softcap = softcap;
+    a.tiles_m = (int32_t)tm;
+    a.splits = (int32_t)vt;
+    a.vt_total = (int32_t)vt;
+    a.vt_per_split = 1;
+    a.part = part;
+    a.xy = xy;
+    a.S = S;
+    a.lds_b = lds_b;
+    void (*kern)(FwdArgs) = softcap > 0.f ? fwd4_kernel<true, true> : fwd4_kernel<false, true>;
+    hipLaunchKernelGGL(kern, dim3(persistent_grid(tm * vt)), dim3(kThreads4), 0, stream, a);
+    MT_TRY(check_launch("fwd4_kernel"));
+    hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(cn, 4)), dim3(256), 0, stream,
+                       part, xy, (int32_t)cn, (int32_t)vt, row_index + c0, loss, lse + c0);
+    MT_TRY(check_launch("fwd_finalize_kernel"));
+    hipLaunchKernelGGL(softmax_grad_kernel, dim3((uint32_t)cn_pad), dim3(256), 0, stream, S, lds_b,
+                       (int32_t)Vp, (int32_t)cn, (int32_t)V, lse + c0, grad, gstride,
+                       row_index + c0, row_label + c0, softcap);
+    MT_TRY(check_launch("softmax_grad_kernel"));
+
+    DxArgs x;
+    x.G = S;
+    x.ldg_b = lds_b;
+    x.W = static_cast<const char*>(W);
+    x.ldw_b = ldw * 2;
+    x.V = (int32_t)V;
+    x.v0 = 0;
+    x.kv = (int32_t)V;
+    x.H = (int32_t)H;
+    x.Cn = (int32_t)cn;
+    x.accbuf = nullptr;
+    x.ld_acc = 0;
+    x.mode = kDxEmit;
+    x.dX = static_cast<char*>(dX);
+    x.lddx_b = lddx * 2;
+    x.row_index = row_index + c0;
+    x.tiles_m = (int32_t)tm;
+    x.tiles_n = (int32_t)cdiv(H, 256);
+    DwArgs w;
+    w.G = S;
+    w.ldg_b = lds_b;
+    w.g_rows = (int32_t)cn_pad;
+    w.g_cols = (int32_t)Vp;
+    w.XcT = XcT;
+    w.ldxt_b = ldxt_b;
+    w.kt_rows = (int32_t)cn;
+    w.H = (int32_t)H;
+    w.cv = (int32_t)V;
+    w.v0 = 0;
+    w.dW = dW;
+    w.lddw = lddw;
+    w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
+    w.tiles_m = (int32_t)vt;
+    w.tiles_n = (int32_t)cdiv(H, 256);
+    hipLaunchKernelGGL(dx4_kernel, dim3(persistent_grid(x.tiles_m * x.tiles_n)), dim3(kThreads4), 0,
+                       stream, x);
+    MT_TRY(check_launch("dx4_kernel"));
+    hipLaunchKernelGGL(dw4_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)), dim3(kThreads4), 0,
+                       stream, w);
+    MT_TRY(check_launch("dw4_kernel"));
   }
   return MT_OK;
 }
@@ -488,6 +622,78 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
   return launch_backward<float>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                 grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, chunk_rows,
                                 chunk_vocab, static_cast<char*>(workspace), s);
+}
+
+int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
+                       size_t budget_bytes, int64_t* chunk_rows, size_t* workspace_bytes) {
+  if (dtype != MT_DTYPE_BF16)
+    return fail(MT_ERR_UNSUPPORTED, "the fused path is bf16 only (dtype %d)", dtype);
+  if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld n_valid=%lld H=%lld V=%lld", (long long)T,
+                (long long)n_valid, (long long)H, (long long)V);
+  if (!chunk_rows || !workspace_bytes) return fail(MT_ERR_INVALID_ARGUMENT, "null output pointer");
+  const FusedPlan p = plan_fused(T, n_valid, H, V, budget_bytes);
+  *chunk_rows = p.C;
+  *workspace_bytes = p.ws;
+  return MT_OK;
+}
+
+int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                  int64_t ldw, int dtype, float softcap, const int32_t* row_index,
+                  const int32_t* row_label, int64_t n_valid, const float* grad_loss,
+                  int64_t grad_stride, float* loss, float* lse, void* dX, int64_t lddx, float* dW,
+                  int64_t lddw, int accumulate_dW, int64_t chunk_rows, void* workspace,
+                  size_t workspace_bytes, mt_stream_t stream) {
+  if (dtype != MT_DTYPE_BF16)
+    return fail(MT_ERR_UNSUPPORTED, "the fused path is bf16 only (dtype %d)", dtype);
+  MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
+  if (n_valid < 0 || n_valid > T)
+    return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
+  if (lddx < H || lddw < H)
+    return fail(MT_ERR_INVALID_ARGUMENT, "lddx=%lld / lddw=%lld must be >= H", (long long)lddx, (long long)lddw);
+  if ((lddx * 2) % 16 != 0 || (lddw * 4) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dX / dW row pitches must be multiples of 16 bytes");
+  if (grad_stride < 0) return fail(MT_ERR_INVALID_ARGUMENT, "grad_stride must be >= 0");
+  if (!dW || (T > 0 && (!dX || !row_index || !loss)) ||
+      (n_valid > 0 && (!row_label || !lse || !grad_loss)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if ((reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(dW) |
+       reinterpret_cast<uintptr_t>(workspace)) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dX, dW and workspace must be 16-byte aligned");
+  if (n_valid > 0) {
+    if (chunk_rows <= 0 || chunk_rows % 256 != 0)
+      return fail(MT_ERR_INVALID_ARGUMENT, "chunk_rows=%lld must be a positive multiple of 256",
+                  (long long)chunk_rows);
+    if ((uint64_t)chunk_rows * vocab_pad(V) * 2 > kMaxBufferBytes ||
+        (uint64_t)H * chunk_rows * 2 > kMaxBufferBytes)
+      return fail(MT_ERR_UNSUPPORTED, "chunk_rows=%lld: logits chunk or X^T beyond 4 GiB",
+                  (long long)chunk_rows);
+    const size_t need = fused_ws(chunk_rows, H, V);
+    if (workspace_bytes < need || !workspace)
+      return fail(MT_ERR_WORKSPACE_TOO_SMALL, "fused workspace %zu bytes < required %zu",
+                  workspace_bytes, need);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (T - n_valid > 0) {
+    const int64_t n0 = T - n_valid;
+    hipLaunchKernelGGL(zero_scatter_f32_kernel, dim3((uint32_t)std::min<int64_t>(cdiv(n0, 256), 4096)),
+                       dim3(256), 0, s, loss, row_index + n_valid, n0);
+    MT_TRY(check_launch("zero_scatter_f32_kernel"));
+    hipLaunchKernelGGL(zero_rows_kernel, dim3((uint32_t)std::min<int64_t>(n0, 8192)), dim3(256), 0, s,
+                       static_cast<char*>(dX), lddx * 2, row_index + n_valid, n0, H * 2);
+    MT_TRY(check_launch("zero_rows_kernel"));
+  }
+  if (n_valid == 0) {
+    if (!accumulate_dW) {
+      hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
+                         s, dW, V, H, lddw);
+      MT_TRY(check_launch("zero_matrix_f32_kernel"));
+    }
+    return MT_OK;
+  }
+  return launch_fused(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, grad_loss,
+                      grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, chunk_rows,
+                      static_cast<char*>(workspace), s);
 }
 
 int mt_segment_sum(const float* loss, const int64_t* target, int64_t T, int64_t ignore_index,

@@ -63,8 +63,10 @@ struct FwdArgs {
   const int32_t* row_label;
   float softcap;
   int32_t tiles_m, splits, vt_total, vt_per_split;
-  float* part;  // [splits][N][2] = (max in log2 units, scaled sum)
+  float* part;  // [N][splits][2] = (max in log2 units, scaled sum)
   float* xy;    // [N] label logit
+  char* S;      // bf16 logits [>= tiles_m * 256][lds_b / 2] (fused path only)
+  int64_t lds_b;
 };
 
 // Columns at or beyond V are masked with a select (no separate tail variant:
@@ -167,7 +169,7 @@ __device__ __forceinline__ void fwd_final_merge(char* lds, float (&m2)[8], float
         lse_merge(m2[fm], d[fm], r[0], r[1]);
       }
       if (rglob[fm] < a.N) {
-        int64_t o = ((int64_t)ts * a.N + rglob[fm]) * 2;
+        int64_t o = ((int64_t)rglob[fm] * a.splits + ts) * 2;
         a.part[o + 0] = m2[fm];
         a.part[o + 1] = d[fm];
       }
@@ -222,18 +224,26 @@ MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
   fwd_final_merge(lds, m2, d, rglob, ts, ec, a);
 }
 
-__global__ void fwd_finalize_kernel(const float* part, const float* xy, int32_t N, int32_t splits,
-                                    const int32_t* row_index, float* loss, float* lse) {
-  int32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= N) return;
+// lse and loss of each valid row from its `splits` (max, sum) partials: one
+// wave per row, lanes merge strided partials, then a fixed shuffle tree
+// (deterministic order).
+__global__ __launch_bounds__(256) void fwd_finalize_kernel(const float* part, const float* xy,
+                                                           int32_t N, int32_t splits,
+                                                           const int32_t* row_index, float* loss,
+                                                           float* lse) {
+  const int32_t r = (int32_t)(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (r >= N) return;  // uniform per wave
+  const int lane = (int)(threadIdx.x & 63u);
+  const float* pr = part + (int64_t)r * splits * 2;
   float m = kNegBig, d = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    int64_t o = ((int64_t)s * N + r) * 2;
-    lse_merge(m, d, part[o], part[o + 1]);
+  for (int s = lane; s < splits; s += 64) lse_merge(m, d, pr[2 * s], pr[2 * s + 1]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lse_merge(m, d, __shfl_xor(m, off), __shfl_xor(d, off));
+  if (lane == 0) {
+    const float L = (m + fast_log2(d)) * kLn2;
+    lse[r] = L;
+    loss[row_index[r]] = L - xy[r];
   }
-  const float L = (m + fast_log2(d)) * kLn2;
-  lse[r] = L;
-  loss[row_index[r]] = L - xy[r];
 }
 
 // ===========================================================================

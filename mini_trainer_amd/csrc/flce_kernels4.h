@@ -39,9 +39,12 @@ struct TileSeq {
 // region beside the stage buffers -- and writes it to part[vocab tile][row];
 // the lane that holds a row's label logit writes it to xy[row].  Nothing is
 // carried in registers from one tile to the next.
+// With kStoreS the tile's bf16-rounded logits (before the softcap) are also
+// written to S, row = compacted row of the chunk, column = vocabulary index:
+// the fused path forms G from them in place once the row's lse is known.
 constexpr int kFwdRed4 = 3 * 256 * 2 * (int)sizeof(float);
 
-template <bool kCap>
+template <bool kCap, bool kStoreS>
 MT_GEMM4_KERNEL void fwd4_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLds4 + kFwdRed4];
   const TileSeq seq((uint32_t)(a.tiles_m * a.vt_total));
@@ -80,6 +83,17 @@ MT_GEMM4_KERNEL void fwd4_kernel(FwdArgs a) {
           d[fm] = 0.f;
         }
         fwd_tile_update<__bf16, kCap>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
+        if (kStoreS) {
+#pragma unroll
+          for (int fm = 0; fm < 8; ++fm) {
+            char* srow = a.S + (int64_t)rglob[fm] * a.lds_b;
+#pragma unroll
+            for (int fn = 0; fn < 4; ++fn) {
+              const float o[4] = {acc[fm][fn][0], acc[fm][fn][1], acc[fm][fn][2], acc[fm][fn][3]};
+              store4<__bf16>(srow + (int64_t)((int32_t)tv * 256 + ec.col(fn)) * 2, o);
+            }
+          }
+        }
         fwd_final_merge(lds + kLds4, m2, d, rglob, tv, ec, a);
       });
 }
@@ -175,6 +189,49 @@ MT_GEMM4_KERNEL void dw4_kernel(DwArgs a) {
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         dw_epilogue(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
       });
+}
+
+// Fused path: G = g_t (softmax(cap(S_t)) - onehot(y_t)) (1 - tanh^2), in place
+// over one chunk of the bf16 logits S written by fwd4_kernel<*, true>.  One
+// workgroup per row; rows >= cn and columns >= V become 0.  HBM-bound: one
+// 16-byte read and one 16-byte write per 8 elements.
+__global__ __launch_bounds__(256) void softmax_grad_kernel(char* S, int64_t lds_b, int32_t cols,
+                                                           int32_t cn, int32_t V,
+                                                           const float* lse, const float* grad,
+                                                           int64_t gstride,
+                                                           const int32_t* row_index,
+                                                           const int32_t* row_label,
+                                                           float softcap) {
+  const int32_t row = blockIdx.x;
+  const bool rv = row < cn;
+  const float lse2 = rv ? lse[row] * kLog2e : 0.f;
+  const float g = rv ? grad[(int64_t)row_index[row] * gstride] : 0.f;
+  const int32_t y = rv ? row_label[row] : -1;
+  const bool cap = softcap > 0.f;
+  const float inv_cap = cap ? 1.0f / softcap : 0.f;
+  u32x4_t* p = reinterpret_cast<u32x4_t*>(S + (int64_t)row * lds_b);
+  for (int32_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
+    u32x4_t v = p[c / 8];
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = v[j / 2];
+      float x = __builtin_bit_cast(float, (j & 1) ? (w & 0xffff0000u) : (w << 16));
+      float dcap = 1.f;
+      if (cap) {
+        const float t = tanh_approx(x * inv_cap);
+        x = softcap * t;
+        dcap = 1.f - t * t;
+      }
+      float q = fast_exp2(fmaf(x, kLog2e, -lse2));
+      q -= (c + j == y) ? 1.f : 0.f;
+      o[j] = (rv && c + j < V) ? q * g * dcap : 0.f;
+    }
+    u32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = pack_bf16x2(o[2 * j], o[2 * j + 1]);
+    p[c / 8] = r;
+  }
 }
 
 }  // namespace mtf

@@ -23,6 +23,7 @@ __all__ = [
     "prepare_targets",
     "per_sample_loss_sums",
     "backward_plan",
+    "fused_plan",
     "BACKWARD_BUDGET_ENV",
 ]
 
@@ -125,26 +126,31 @@ def _grad_vector(grad: torch.Tensor, T: int) -> Tuple[torch.Tensor, int]:
     return g, 1
 
 
+def _check_inputs(hidden, weight, target):
+    _require_device("hidden_states", hidden)
+    _require_device("lm_head_weight", weight)
+    if weight.dim() != 2:
+        raise ValueError(f"lm_head_weight must be [V, H], got {tuple(weight.shape)}")
+    if hidden.dtype != weight.dtype:
+        raise TypeError(f"hidden_states ({hidden.dtype}) and lm_head_weight ({weight.dtype}) "
+                        "must have the same dtype")
+    dt = _dtype_code(hidden.dtype)
+    V, H = weight.shape
+    if hidden.shape[-1] != H:
+        raise ValueError(f"hidden size mismatch: hidden_states {tuple(hidden.shape)}, "
+                         f"lm_head_weight {tuple(weight.shape)}")
+    X = _rows(hidden, "hidden_states")
+    W = _rows(weight, "lm_head_weight")
+    T = X.shape[0]
+    if target.numel() != T:
+        raise ValueError(f"target has {target.numel()} elements, expected {T}")
+    return X, W, T, H, V, dt
+
+
 class _FusedLinearCrossEntropyNone(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, target, ignore_index, softcap, shift, dw_accumulator):
-        _require_device("hidden_states", hidden)
-        _require_device("lm_head_weight", weight)
-        if weight.dim() != 2:
-            raise ValueError(f"lm_head_weight must be [V, H], got {tuple(weight.shape)}")
-        if hidden.dtype != weight.dtype:
-            raise TypeError(f"hidden_states ({hidden.dtype}) and lm_head_weight ({weight.dtype}) "
-                            "must have the same dtype")
-        dt = _dtype_code(hidden.dtype)
-        V, H = weight.shape
-        if hidden.shape[-1] != H:
-            raise ValueError(f"hidden size mismatch: hidden_states {tuple(hidden.shape)}, "
-                             f"lm_head_weight {tuple(weight.shape)}")
-        X = _rows(hidden, "hidden_states")
-        W = _rows(weight, "lm_head_weight")
-        T = X.shape[0]
-        if target.numel() != T:
-            raise ValueError(f"target has {target.numel()} elements, expected {T}")
+        X, W, T, H, V, dt = _check_inputs(hidden, weight, target)
         lib = load()
         dev = X.device
         row_index, row_label, n = prepare_targets(target, V, ignore_index, shift)
@@ -190,10 +196,90 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         return grad_x, grad_w, None, None, None, None, None
 
 
+def fused_plan(T: int, n_valid: int, H: int, V: int,
+               budget_bytes: Optional[int] = None) -> Tuple[int, int]:
+    """(chunk_rows, workspace_bytes) of the fused forward + backward (bf16)."""
+    lib = load()
+    if budget_bytes is None:
+        budget_bytes = int(os.environ.get(BACKWARD_BUDGET_ENV, "0"))
+    c, ws = ctypes.c_int64(), ctypes.c_size_t()
+    check(lib.mt_flce_fused_plan(T, n_valid, H, V, MT_DTYPE_BF16, budget_bytes, ctypes.byref(c),
+                                 ctypes.byref(ws)), "mt_flce_fused_plan")
+    return c.value, ws.value
+
+
+def _promised_grad(grad_scale, T: int, dev: torch.device) -> Tuple[torch.Tensor, int]:
+    if isinstance(grad_scale, torch.Tensor):
+        g = grad_scale.detach().reshape(-1).to(device=dev, dtype=torch.float32)
+        if g.numel() == 1:
+            return g.contiguous(), 0
+        if g.numel() != T:
+            raise ValueError(f"grad_scale has {g.numel()} elements, expected 1 or {T}")
+        return g.contiguous(), 1
+    return torch.full((1,), float(grad_scale), dtype=torch.float32, device=dev), 0
+
+
+class _FusedLinearCrossEntropyEager(torch.autograd.Function):
+    """Forward that also produces dX and dW for an upstream gradient promised
+    up front (mt_flce_fused); the backward checks the promise and hands the
+    stored gradients to autograd."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, target, ignore_index, softcap, shift, dw_accumulator,
+                grad_scale):
+        X, W, T, H, V, dt = _check_inputs(hidden, weight, target)
+        lib = load()
+        dev = X.device
+        row_index, row_label, n = prepare_targets(target, V, ignore_index, shift)
+        g, gstride = _promised_grad(grad_scale, T, dev)
+        loss = torch.empty(T, dtype=torch.float32, device=dev)
+        lse = torch.empty(n, dtype=torch.float32, device=dev)
+        dX = torch.empty((T, H), dtype=X.dtype, device=dev)
+        if dw_accumulator is not None:
+            dW, accumulate = dw_accumulator, 1
+        else:
+            dW, accumulate = torch.empty((V, H), dtype=torch.float32, device=dev), 0
+        C, ws_bytes = fused_plan(T, n, H, V)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        check(lib.mt_flce_fused(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt, float(softcap),
+                                _p(row_index), _p(row_label), n, _p(g), gstride, _p(loss), _p(lse),
+                                _p(dX), dX.stride(0), _p(dW), dW.stride(0), accumulate, C, _p(ws),
+                                ws_bytes, _stream(dev)), "mt_flce_fused")
+        del ws
+        ctx.save_for_backward(row_index, g)
+        ctx.meta = (n, gstride, hidden.shape)
+        ctx.dX = dX
+        ctx.dW = None if dw_accumulator is not None else dW
+        return loss.view(hidden.shape[:-1])
+
+    @staticmethod
+    def backward(ctx, grad_loss):
+        row_index, g = ctx.saved_tensors
+        n, gstride, hshape = ctx.meta
+        T = row_index.numel()
+        if n > 0:
+            gl = grad_loss.reshape(-1)
+            if gl.numel() == 1:
+                gl = gl.expand(T)
+            valid = row_index[:n].long()
+            want = g.expand(n) if gstride == 0 else g[valid]
+            if not bool(torch.equal(gl[valid].float(), want)):
+                raise RuntimeError(
+                    "the upstream gradient of the loss differs from the grad_scale promised to "
+                    "fused_linear_cross_entropy; the fused path has already formed dX and dW "
+                    "for the promised one (call without grad_scale for an arbitrary gradient)")
+        dX, dW = ctx.dX, ctx.dW
+        ctx.dX = ctx.dW = None
+        grad_x = dX.view(hshape) if ctx.needs_input_grad[0] else None
+        grad_w = dW if ctx.needs_input_grad[1] else None
+        return grad_x, grad_w, None, None, None, None, None, None
+
+
 def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torch.Tensor,
                                target: torch.Tensor, ignore_index: int = -100,
                                softcap: Optional[float] = None, shift_labels: bool = False,
-                               dw_accumulator: Optional[torch.Tensor] = None) -> torch.Tensor:
+                               dw_accumulator: Optional[torch.Tensor] = None,
+                               grad_scale=None) -> torch.Tensor:
     """Per-token loss of hidden_states @ lm_head_weight.T against target.
 
     loss[t] = logsumexp(logits[t]) - logits[t, target[t]], +0.0 where
@@ -203,6 +289,13 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     fp32.  With dw_accumulator (fp32 [V, H]) the weight gradient is added into
     that tensor instead of being returned to autograd.  shift_labels applies
     the causal shift (target[t] = labels[t + 1]) on the device.
+
+    grad_scale (a float, or a [T] tensor of per-token values) promises the
+    upstream gradient of the returned loss -- train.py:97-104 knows it before
+    the forward: world_size / batch_num_loss_counted_tokens for every token.
+    bf16 inputs then take the fused path (each logits tile computed once, dX
+    and dW formed during the forward); the backward checks that the gradient
+    it receives is the promised one and raises otherwise.
     """
     if dw_accumulator is not None:
         V, H = lm_head_weight.shape
@@ -213,6 +306,10 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     cap = 0.0 if softcap is None else float(softcap)
     if cap < 0:
         raise ValueError("softcap must be positive (or None)")
+    if grad_scale is not None and lm_head_weight.dtype == torch.bfloat16:
+        return _FusedLinearCrossEntropyEager.apply(hidden_states, lm_head_weight, target,
+                                                   int(ignore_index), cap, bool(shift_labels),
+                                                   dw_accumulator, grad_scale)
     return _FusedLinearCrossEntropyNone.apply(hidden_states, lm_head_weight, target,
                                               int(ignore_index), cap, bool(shift_labels),
                                               dw_accumulator)

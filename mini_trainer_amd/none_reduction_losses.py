@@ -29,10 +29,14 @@ def liger_fixed_fused_linear_cross_entropy_none_reduction(
     ignore_index and softcap=final_logit_softcapping to Liger's fused kernel
     and ignores num_items_in_batch and **kwargs (:9,12).  Returns fp32 [T]
     with +0.0 at ignored positions, differentiable in hidden_states and
-    lm_head_weight.
+    lm_head_weight.  Of **kwargs only `grad_scale` is read (absent from the
+    reference's callers, so they get the general path): a caller that knows
+    the upstream gradient of the loss before the forward passes it to select
+    the fused path (see flce.fused_linear_cross_entropy).
     """
     return fused_linear_cross_entropy(hidden_states, lm_head_weight, target,
-                                      ignore_index=ignore_index, softcap=final_logit_softcapping)
+                                      ignore_index=ignore_index, softcap=final_logit_softcapping,
+                                      grad_scale=kwargs.get("grad_scale"))
 
 
 def hf_fixed_cross_entropy_none_reduction(

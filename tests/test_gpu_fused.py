@@ -1,0 +1,108 @@
+"""Parity of the fused forward + backward (mt_flce_fused: the upstream
+gradient promised at the forward, each logits tile computed once) against the
+reference's torch path, with the north-star tolerances: per-token loss 2e-3
+relative (bf16), dX and dW 1e-2 relative Frobenius error, ignored positions
+exactly +0.0 / 0.  Also: its results agree with the general path's, the
+backward rejects a gradient other than the promised one, and the chunking
+(several chunks, uneven last chunk) does not change the result.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from mini_trainer_amd import fused_linear_cross_entropy
+from mini_trainer_amd.flce import BACKWARD_BUDGET_ENV, fused_plan
+from mini_trainer_amd.none_reduction_losses import (
+    liger_fixed_fused_linear_cross_entropy_none_reduction)
+from oracle.torch_path import rel_fro
+
+from test_gpu_parity import GRAD_RFRO, check_parity, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+def run_fused(dev, X, W, y, grad_scale, softcap=None, acc=None, backward_grad=None):
+    Xd = X.to(dev).requires_grad_(True)
+    Wd = W.to(dev).requires_grad_(True)
+    if acc is None:
+        acc = torch.zeros(W.shape, dtype=torch.float32, device=dev)
+    gs = grad_scale.to(dev) if isinstance(grad_scale, torch.Tensor) else grad_scale
+    loss = fused_linear_cross_entropy(Xd, Wd, y.to(dev), softcap=softcap, dw_accumulator=acc,
+                                      grad_scale=gs)
+    if backward_grad is None:
+        if isinstance(grad_scale, torch.Tensor):
+            loss.backward(grad_scale.to(dev))
+        else:
+            (loss.float().sum() * grad_scale).backward()
+    else:
+        loss.backward(backward_grad.to(dev))
+    torch.cuda.synchronize()
+    return loss.detach().cpu(), Xd.grad.detach().cpu(), acc.cpu()
+
+
+@pytest.mark.parametrize("T,H,V", [(300, 128, 1000), (513, 192, 2065), (64, 896, 4096)])
+def test_fused_uniform_grad(gpu, T, H, V):
+    print(f"case fused T={T} H={H} V={V}", flush=True)
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=T + V)
+    n = int((y != -100).sum())
+    loss, dX, dW = run_fused(gpu, X, W, y, 1.0 / n)
+    check_parity(X, W, y, loss, dX, dW, grad=torch.full((T,), 1.0 / n))
+
+
+def test_fused_per_token_grad_and_softcap(gpu):
+    X, W, y = make_case(400, 128, 3000, torch.bfloat16, seed=11, w_std=0.2)
+    grad = torch.rand(400, generator=torch.Generator().manual_seed(3)) * 2 - 0.5
+    loss, dX, dW = run_fused(gpu, X, W, y, grad, softcap=3.0)
+    check_parity(X, W, y, loss, dX, dW, grad=grad, softcap=3.0)
+
+
+def test_fused_many_chunks_matches_general_path(gpu, monkeypatch):
+    # tiny budget -> 256-row chunks: several chunks, an uneven last one, dW
+    # accumulated across chunks
+    monkeypatch.setenv(BACKWARD_BUDGET_ENV, "1")
+    X, W, y = make_case(1100, 128, 1300, torch.bfloat16, seed=7, mask_frac=0.2)
+    n = int((y != -100).sum())
+    C, ws = fused_plan(1100, n, 128, 1300)
+    assert C == 256 and ws > 0
+    loss, dX, dW = run_fused(gpu, X, W, y, 0.5)
+    check_parity(X, W, y, loss, dX, dW, grad=torch.full((1100,), 0.5))
+    # the general path on the same inputs: same loss bits, gradients within rounding
+    Xd, Wd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True)
+    acc = torch.zeros(W.shape, dtype=torch.float32, device=gpu)
+    l2 = fused_linear_cross_entropy(Xd, Wd, y.to(gpu), dw_accumulator=acc)
+    (l2.float().sum() * 0.5).backward()
+    assert torch.equal(l2.detach().cpu(), loss)
+    assert rel_fro(Xd.grad.cpu().float(), dX.float()) <= 1e-2
+    assert rel_fro(acc.cpu(), dW) <= 1e-3
+
+
+def test_fused_accumulates_and_all_masked(gpu):
+    X, W, y = make_case(300, 128, 700, torch.bfloat16, seed=9)
+    X2, _, y2 = make_case(200, 128, 700, torch.bfloat16, seed=10)
+    y3 = torch.full((50,), -100)
+    X3 = torch.randn(50, 128).to(torch.bfloat16)
+    acc = torch.zeros(W.shape, dtype=torch.float32, device=gpu)
+    for Xi, yi in ((X, y), (X2, y2), (X3, y3)):
+        loss, dX, _ = run_fused(gpu, Xi, W, yi, 1.0, acc=acc)
+    assert torch.equal(loss, torch.zeros(50)) and torch.count_nonzero(dX) == 0
+    from oracle.torch_path import torch_path
+    _, _, r1 = torch_path(X, W, y)
+    _, _, r2 = torch_path(X2, W, y2)
+    assert rel_fro(acc.cpu(), r1 + r2) <= GRAD_RFRO
+
+
+def test_fused_rejects_a_different_gradient(gpu):
+    X, W, y = make_case(256, 64, 512, torch.bfloat16, seed=21)
+    with pytest.raises(RuntimeError, match="promised"):
+        run_fused(gpu, X, W, y, 1.0, backward_grad=torch.full((256,), 2.0))
+
+
+def test_drop_in_reads_grad_scale_kwarg(gpu):
+    X, W, y = make_case(256, 64, 512, torch.bfloat16, seed=22)
+    Xd, Wd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True)
+    loss = liger_fixed_fused_linear_cross_entropy_none_reduction(
+        Xd, Wd, y.to(gpu), None, -100, None, grad_scale=0.25)
+    (loss.sum() * 0.25).backward()
+    check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), Wd.grad.cpu(),
+                 grad=torch.full((256,), 0.25))
