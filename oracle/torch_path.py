@@ -30,12 +30,16 @@ import torch.nn.functional as F
 def torch_path(X: torch.Tensor, W: torch.Tensor, target: torch.Tensor,
                grad: Optional[torch.Tensor] = None, ignore_index: int = -100,
                softcap: Optional[float] = None, chunk_rows: int = 1024,
-               rows: Optional[int] = None, need_grads: bool = True
+               rows: Optional[int] = None, need_grads: bool = True, upcast: bool = False
                ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor]]:
     """Returns (loss fp32 [T], dX [T, H] in X.dtype, dW fp32 [V, H]).
 
     grad: per-token upstream gradient ([T] or scalar); default 1.
     rows: only process the first `rows` rows (bounded CPU samples).
+    upcast: form the logits as an fp32 product rounded to X.dtype (what
+      F.linear in bf16 computes, up to the fp32 summation order) and dX as
+      an fp32 product of the rounded G -- the same arithmetic as the default,
+      only faster on CPUs without a fast bf16 GEMM.
     """
     T, H = X.shape
     V = W.shape[0]
@@ -53,7 +57,8 @@ def torch_path(X: torch.Tensor, W: torch.Tensor, target: torch.Tensor,
     for a in range(0, n, chunk_rows):
         b = min(a + chunk_rows, n)
         Xc, y = X[a:b], y_all[a:b]
-        logits = F.linear(Xc, W)
+        logits = (F.linear(Xc.float(), W.float()).to(X.dtype) if upcast and X.dtype != torch.float32
+                  else F.linear(Xc, W))
         z0 = logits.float().requires_grad_(need_grads)
         z = softcap * torch.tanh(z0 / softcap) if softcap else z0
         lc = F.cross_entropy(z, y, ignore_index=ignore_index, reduction="none")
@@ -61,7 +66,7 @@ def torch_path(X: torch.Tensor, W: torch.Tensor, target: torch.Tensor,
         if need_grads:
             (G,) = torch.autograd.grad(lc, z0, g_all[a:b])
             Gd = G.to(X.dtype)
-            dX[a:b] = Gd @ W
+            dX[a:b] = (Gd.float() @ W.float()).to(X.dtype) if upcast else Gd @ W
             dW += Gd.float().t() @ Xc.float()
     return loss, dX, dW
 
