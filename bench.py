@@ -37,7 +37,7 @@ sys.path.insert(0, ROOT)
 
 from mini_trainer_amd import _lib, synth  # noqa: E402
 from mini_trainer_amd.flce import (_dtype_code, _p, _stream, backward_plan,  # noqa: E402
-                                   fused_linear_cross_entropy, prepare_targets)
+                                   fused_linear_cross_entropy, fused_plan, prepare_targets)
 
 PEAK_BF16 = 2.5166e15  # MI355X dense bf16 MFMA, 256 CU x 2.4 GHz x 4096 flop/clk
 PEAK_FP32 = 157.3e12
@@ -227,6 +227,7 @@ def main():
     C, Cv, bws = backward_plan(T, n, H, V, cfg.dtype)
 
     fwd_kernel_name = "fwd4_kernel" if cfg.dtype == torch.bfloat16 else "fwd_kernel"
+    fused_taken = fused and fused_plan(T, n_valid[0], H, V)[2]
     traffic = measured_traffic(cfg.key, fwd_kernel_name)
 
     alg_flops = 6.0 * H * V * N_total
@@ -265,7 +266,9 @@ def main():
             "frac_of_peak": alg_flops / t_step / peak_flops,
             "dense_convention_frac": 6.0 * H * V * T_total / t_step / peak_flops,
             "path": ("fused: grad_scale = 1/N passed at the forward (mt_flce_fused, 6HVN)"
-                     if fused else "general (mt_flce_forward + mt_flce_backward, 8HVN)"),
+                     if fused_taken else
+                     "general (mt_flce_forward + mt_flce_backward, 8HVN)"
+                     + ("; the planner declined the fused path for this budget" if fused else "")),
             "general_path_ms_per_step": ms_general,
             "general_path_frac_of_peak": alg_flops / (ms_general / 1e3) / peak_flops,
             "extra_hbm_GB": extra / 1e9,

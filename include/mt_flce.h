@@ -141,11 +141,16 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H,
  * (multiple of 256) whose workspace -- the chunk's bf16 logits [chunk,
  * round_up(V, 256)], the (max, sum) partials, the label logits and the chunk's
  * X^T -- fits budget_bytes (0 = default: 5% of T*V*2), then evened out over
- * the chunks.  Writes the chunk size and workspace size.
+ * the chunks.  Writes the chunk size, the workspace size and *pays = 1 if
+ * a cost model expects the fused path to beat the general one
+ * (mt_flce_forward + mt_flce_backward) under the same budget, else 0: small
+ * budgets force small chunks, with few long dX tiles and one dW
+ * read-modify-write per chunk, which the general path's two-dimensional
+ * blocking avoids.
  */
 int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
                        int dtype, size_t budget_bytes, int64_t* chunk_rows,
-                       size_t* workspace_bytes);
+                       size_t* workspace_bytes, int* pays);
 
 /*
  * Fused forward + backward for a caller that knows the upstream gradient of

@@ -40,7 +40,7 @@ SIGNATURES = {
                                  c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64,
                                  c_int64, c_void_p, c_size_t, c_void_p]),
     "mt_flce_fused_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t,
-                                   POINTER(c_int64), POINTER(c_size_t)]),
+                                   POINTER(c_int64), POINTER(c_size_t), POINTER(c_int)]),
     "mt_flce_fused": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                               c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
                               c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int,

@@ -153,31 +153,55 @@ size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es) {
   return g + acc + xt;
 }
 
+// ----------------------------------------------------------------- costs
+// Modelled seconds of `tiles` output tiles (256 x 256) of depth k on the
+// persistent grid.  Whole rounds run at the busy per-CU rate; the CUs a
+// partial round leaves idle are charged 30% of a busy one: under the chip's
+// power limit the others clock up while they idle.
+constexpr double kCuRate = 4.5e12;  // sustained bf16 flop/s of one busy CU
+constexpr double kLaunch = 8e-6, kBw = 5e12;
+
+double gemm_time(int64_t tiles, int64_t k) {
+  if (tiles <= 0) return 0.0;
+  const double tile_time = 2.0 * 256 * 256 * (double)round_up(k, 64) / kCuRate;
+  const double full = (double)tiles / kCUs, rounds = std::ceil(full);
+  return (full + 0.3 * (rounds - full)) * tile_time + kLaunch;
+}
+
 // Modelled seconds for one backward with blocks of C x Cv.
 double backward_cost(int64_t N, int64_t H, int64_t V, int64_t C, int64_t Cv, int es) {
-  const Geometry geo = geometry(es);
-  const double tile_rate = 2.5e15 * 0.7 / geo.slots;  // flop/s of one resident tile
-  const double launch = 8e-6, bw = 5e12;
-  const double tmn = 2.0 * geo.tile_m * geo.tile_n;
+  (void)es;
   double t = 0, bytes = 0;
   for (int64_t c0 = 0; c0 < N; c0 += C) {
     const int64_t cn = std::min(C, N - c0);
-    const int64_t nv = cdiv(V, Cv);
+    const int64_t nv = cdiv(V, Cv), tm = cdiv(cn, 256), th = cdiv(H, 256);
     for (int64_t v0 = 0; v0 < V; v0 += Cv) {
-      const int64_t cv = std::min(Cv, V - v0);
-      const double tile_flops_re = tmn * H;
-      const double tile_flops_dx = tmn * round_up(cv, 64);
-      const double tile_flops_dw = tmn * round_up(cn, 64);
-      t += cdiv(cdiv(cn, geo.tile_m) * cdiv(cv, geo.tile_n), geo.slots) * tile_flops_re / tile_rate;
-      t += cdiv(cdiv(cn, geo.tile_m) * cdiv(H, geo.tile_n), geo.slots) * tile_flops_dx / tile_rate;
-      t += cdiv(cdiv(cv, geo.tile_m) * cdiv(H, geo.tile_n), geo.slots) * tile_flops_dw / tile_rate;
-      t += 3 * launch;
+      const int64_t cv = std::min(Cv, V - v0), tv = cdiv(cv, 256);
+      t += gemm_time(tm * tv, H) + gemm_time(tm * th, cv) + gemm_time(tv * th, cn);
     }
-    bytes += (double)V * H * 8;                        // dW read-modify-write
+    bytes += (double)V * H * 8;                              // dW read-modify-write
     if (nv > 1) bytes += (double)(2 * nv - 2) * cn * H * 4;  // dX accumulator
-    t += launch;
+    t += kLaunch;
   }
-  return t + 0.5 * bytes / bw;
+  return t + 0.5 * bytes / kBw;
+}
+
+// Modelled seconds of the general forward (one launch over all valid rows).
+double forward_cost(int64_t N, int64_t H, int64_t V) {
+  return gemm_time(cdiv(N, 256) * cdiv(V, 256), H);
+}
+
+// Modelled seconds of the fused forward + backward with row chunks of C.
+double fused_cost(int64_t N, int64_t H, int64_t V, int64_t C) {
+  const int64_t vt = cdiv(V, 256), th = cdiv(H, 256), Vp = round_up(V, 256);
+  double t = 0, bytes = 0;
+  for (int64_t c0 = 0; c0 < N; c0 += C) {
+    const int64_t cn = std::min(C, N - c0), tm = cdiv(cn, 256);
+    t += gemm_time(tm * vt, H) + gemm_time(tm * th, V) + gemm_time(vt * th, cn);
+    t += (double)cn * Vp * 2 * 2 / kBw + 4 * kLaunch;  // G formed in place: read + write
+    bytes += (double)V * H * 8 + (double)cn * Vp * 2;  // dW read-modify-write, S stores
+  }
+  return t + 0.5 * bytes / kBw;
 }
 
 struct BwdPlan {
@@ -398,6 +422,17 @@ FusedPlan plan_fused(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) 
   p.C = round_up(cdiv(N, nch), 256);
   p.ws = fused_ws(p.C, H, V);
   return p;
+}
+
+// Is the fused path expected to beat the general one (forward + recompute
+// backward) under the same budget?  Small budgets force small chunks: few
+// dX tiles with a long K and one dW read-modify-write per chunk, which the
+// general path's two-dimensional blocking avoids.
+bool fused_pays(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) {
+  const FusedPlan f = plan_fused(T, N, H, V, budget);
+  const BwdPlan b = plan_backward(T, N, H, V, 2, budget);
+  if (!f.C || !b.C) return false;
+  return fused_cost(N, H, V, f.C) < 0.97 * (forward_cost(N, H, V) + backward_cost(N, H, V, b.C, b.Cv, 2));
 }
 
 int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx, int64_t ldw,
@@ -625,16 +660,19 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
 }
 
 int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
-                       size_t budget_bytes, int64_t* chunk_rows, size_t* workspace_bytes) {
+                       size_t budget_bytes, int64_t* chunk_rows, size_t* workspace_bytes,
+                       int* pays) {
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "the fused path is bf16 only (dtype %d)", dtype);
   if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld n_valid=%lld H=%lld V=%lld", (long long)T,
                 (long long)n_valid, (long long)H, (long long)V);
-  if (!chunk_rows || !workspace_bytes) return fail(MT_ERR_INVALID_ARGUMENT, "null output pointer");
+  if (!chunk_rows || !workspace_bytes || !pays)
+    return fail(MT_ERR_INVALID_ARGUMENT, "null output pointer");
   const FusedPlan p = plan_fused(T, n_valid, H, V, budget_bytes);
   *chunk_rows = p.C;
   *workspace_bytes = p.ws;
+  *pays = fused_pays(T, n_valid, H, V, budget_bytes) ? 1 : 0;
   return MT_OK;
 }
 

@@ -25,11 +25,15 @@ __all__ = [
     "backward_plan",
     "fused_plan",
     "BACKWARD_BUDGET_ENV",
+    "FUSED_ENV",
 ]
 
 # Optional override of the backward workspace budget in bytes (default: 5% of
 # the materialised-logits size T * V * sizeof(dtype)).
 BACKWARD_BUDGET_ENV = "MT_FLCE_BWD_BUDGET_BYTES"
+# With grad_scale given (bf16): "auto" (default) takes the fused path when the
+# planner expects it to pay, "1" always, "0" never.
+FUSED_ENV = "MT_FLCE_FUSED"
 
 
 def _dtype_code(dt: torch.dtype) -> int:
@@ -148,14 +152,50 @@ def _check_inputs(hidden, weight, target):
 
 
 class _FusedLinearCrossEntropyNone(torch.autograd.Function):
+    """Per-token loss; two paths over the same arithmetic.
+
+    general  forward keeps lse (mt_flce_forward); the backward recomputes the
+             logits for whatever upstream gradient arrives (mt_flce_backward).
+    fused    grad_scale promised the upstream gradient at the forward and the
+             planner expects the fused path to pay (bf16, mt_flce_fused_plan):
+             the forward also forms dX and dW (mt_flce_fused); the backward
+             checks the gradient it receives against the promise and hands the
+             stored gradients to autograd.
+    """
+
     @staticmethod
-    def forward(ctx, hidden, weight, target, ignore_index, softcap, shift, dw_accumulator):
+    def forward(ctx, hidden, weight, target, ignore_index, softcap, shift, dw_accumulator,
+                grad_scale):
         X, W, T, H, V, dt = _check_inputs(hidden, weight, target)
         lib = load()
         dev = X.device
         row_index, row_label, n = prepare_targets(target, V, ignore_index, shift)
         loss = torch.empty(T, dtype=torch.float32, device=dev)
         lse = torch.empty(n, dtype=torch.float32, device=dev)
+        ctx.fused = False
+        if grad_scale is not None and dt == MT_DTYPE_BF16 and n > 0:
+            C, ws_bytes, pays = fused_plan(T, n, H, V)
+            ctx.fused = _use_fused(pays)
+        ctx.dw_accumulator = dw_accumulator
+        if ctx.fused:
+            g, gstride = _promised_grad(grad_scale, T, dev)
+            dX = torch.empty((T, H), dtype=X.dtype, device=dev)
+            if dw_accumulator is not None:
+                dW, accumulate = dw_accumulator, 1
+            else:
+                dW, accumulate = torch.empty((V, H), dtype=torch.float32, device=dev), 0
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            check(lib.mt_flce_fused(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
+                                    float(softcap), _p(row_index), _p(row_label), n, _p(g),
+                                    gstride, _p(loss), _p(lse), _p(dX), dX.stride(0), _p(dW),
+                                    dW.stride(0), accumulate, C, _p(ws), ws_bytes, _stream(dev)),
+                  "mt_flce_fused")
+            del ws
+            ctx.save_for_backward(row_index, g)
+            ctx.meta = (n, gstride, hidden.shape)
+            ctx.dX = dX
+            ctx.dW = None if dw_accumulator is not None else dW
+            return loss.view(hidden.shape[:-1])
         ws_bytes = lib.mt_flce_forward_workspace_bytes(T, n, H, V, dt)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
@@ -164,17 +204,19 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         del ws
         ctx.save_for_backward(X, W, row_index, row_label, lse)
         ctx.meta = (n, float(softcap), hidden.shape, dt)
-        ctx.dw_accumulator = dw_accumulator
         return loss.view(hidden.shape[:-1])
 
     @staticmethod
     def backward(ctx, grad_loss):
+        if ctx.fused:
+            return _FusedLinearCrossEntropyNone._backward_fused(ctx, grad_loss)
         X, W, row_index, row_label, lse = ctx.saved_tensors
         n, softcap, hshape, dt = ctx.meta
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         acc = ctx.dw_accumulator
+        none = (None,) * 6
         if not need_x and not need_w and acc is None:
-            return None, None, None, None, None, None, None
+            return (None, None) + none
         lib = load()
         T, H = X.shape
         V = W.shape[0]
@@ -193,67 +235,10 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
                                    _p(ws), ws_bytes, _stream(dev)), "mt_flce_backward")
         grad_x = dX.view(hshape) if need_x else None
         grad_w = dW if (need_w and acc is None) else None
-        return grad_x, grad_w, None, None, None, None, None
-
-
-def fused_plan(T: int, n_valid: int, H: int, V: int,
-               budget_bytes: Optional[int] = None) -> Tuple[int, int]:
-    """(chunk_rows, workspace_bytes) of the fused forward + backward (bf16)."""
-    lib = load()
-    if budget_bytes is None:
-        budget_bytes = int(os.environ.get(BACKWARD_BUDGET_ENV, "0"))
-    c, ws = ctypes.c_int64(), ctypes.c_size_t()
-    check(lib.mt_flce_fused_plan(T, n_valid, H, V, MT_DTYPE_BF16, budget_bytes, ctypes.byref(c),
-                                 ctypes.byref(ws)), "mt_flce_fused_plan")
-    return c.value, ws.value
-
-
-def _promised_grad(grad_scale, T: int, dev: torch.device) -> Tuple[torch.Tensor, int]:
-    if isinstance(grad_scale, torch.Tensor):
-        g = grad_scale.detach().reshape(-1).to(device=dev, dtype=torch.float32)
-        if g.numel() == 1:
-            return g.contiguous(), 0
-        if g.numel() != T:
-            raise ValueError(f"grad_scale has {g.numel()} elements, expected 1 or {T}")
-        return g.contiguous(), 1
-    return torch.full((1,), float(grad_scale), dtype=torch.float32, device=dev), 0
-
-
-class _FusedLinearCrossEntropyEager(torch.autograd.Function):
-    """Forward that also produces dX and dW for an upstream gradient promised
-    up front (mt_flce_fused); the backward checks the promise and hands the
-    stored gradients to autograd."""
+        return (grad_x, grad_w) + none
 
     @staticmethod
-    def forward(ctx, hidden, weight, target, ignore_index, softcap, shift, dw_accumulator,
-                grad_scale):
-        X, W, T, H, V, dt = _check_inputs(hidden, weight, target)
-        lib = load()
-        dev = X.device
-        row_index, row_label, n = prepare_targets(target, V, ignore_index, shift)
-        g, gstride = _promised_grad(grad_scale, T, dev)
-        loss = torch.empty(T, dtype=torch.float32, device=dev)
-        lse = torch.empty(n, dtype=torch.float32, device=dev)
-        dX = torch.empty((T, H), dtype=X.dtype, device=dev)
-        if dw_accumulator is not None:
-            dW, accumulate = dw_accumulator, 1
-        else:
-            dW, accumulate = torch.empty((V, H), dtype=torch.float32, device=dev), 0
-        C, ws_bytes = fused_plan(T, n, H, V)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        check(lib.mt_flce_fused(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt, float(softcap),
-                                _p(row_index), _p(row_label), n, _p(g), gstride, _p(loss), _p(lse),
-                                _p(dX), dX.stride(0), _p(dW), dW.stride(0), accumulate, C, _p(ws),
-                                ws_bytes, _stream(dev)), "mt_flce_fused")
-        del ws
-        ctx.save_for_backward(row_index, g)
-        ctx.meta = (n, gstride, hidden.shape)
-        ctx.dX = dX
-        ctx.dW = None if dw_accumulator is not None else dW
-        return loss.view(hidden.shape[:-1])
-
-    @staticmethod
-    def backward(ctx, grad_loss):
+    def _backward_fused(ctx, grad_loss):
         row_index, g = ctx.saved_tensors
         n, gstride, hshape = ctx.meta
         T = row_index.numel()
@@ -272,7 +257,40 @@ class _FusedLinearCrossEntropyEager(torch.autograd.Function):
         ctx.dX = ctx.dW = None
         grad_x = dX.view(hshape) if ctx.needs_input_grad[0] else None
         grad_w = dW if ctx.needs_input_grad[1] else None
-        return grad_x, grad_w, None, None, None, None, None, None
+        return (grad_x, grad_w) + (None,) * 6
+
+
+def fused_plan(T: int, n_valid: int, H: int, V: int,
+               budget_bytes: Optional[int] = None) -> Tuple[int, int, bool]:
+    """(chunk_rows, workspace_bytes, pays) of the fused forward + backward
+    (bf16); pays: the planner expects it to beat the general path."""
+    lib = load()
+    if budget_bytes is None:
+        budget_bytes = int(os.environ.get(BACKWARD_BUDGET_ENV, "0"))
+    c, ws, pays = ctypes.c_int64(), ctypes.c_size_t(), ctypes.c_int()
+    check(lib.mt_flce_fused_plan(T, n_valid, H, V, MT_DTYPE_BF16, budget_bytes, ctypes.byref(c),
+                                 ctypes.byref(ws), ctypes.byref(pays)), "mt_flce_fused_plan")
+    return c.value, ws.value, bool(pays.value)
+
+
+def _use_fused(pays: bool) -> bool:
+    mode = os.environ.get(FUSED_ENV, "auto").strip().lower()
+    if mode in ("1", "on", "always"):
+        return True
+    if mode in ("0", "off", "never"):
+        return False
+    return pays
+
+
+def _promised_grad(grad_scale, T: int, dev: torch.device) -> Tuple[torch.Tensor, int]:
+    if isinstance(grad_scale, torch.Tensor):
+        g = grad_scale.detach().reshape(-1).to(device=dev, dtype=torch.float32)
+        if g.numel() == 1:
+            return g.contiguous(), 0
+        if g.numel() != T:
+            raise ValueError(f"grad_scale has {g.numel()} elements, expected 1 or {T}")
+        return g.contiguous(), 1
+    return torch.full((1,), float(grad_scale), dtype=torch.float32, device=dev), 0
 
 
 def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torch.Tensor,
@@ -294,8 +312,10 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     upstream gradient of the returned loss -- train.py:97-104 knows it before
     the forward: world_size / batch_num_loss_counted_tokens for every token.
     bf16 inputs then take the fused path (each logits tile computed once, dX
-    and dW formed during the forward); the backward checks that the gradient
-    it receives is the promised one and raises otherwise.
+    and dW formed during the forward) when the planner expects it to beat the
+    general one under the workspace budget (mt_flce_fused_plan); the backward
+    of the fused path checks that the gradient it receives is the promised one
+    and raises otherwise.
     """
     if dw_accumulator is not None:
         V, H = lm_head_weight.shape
@@ -306,13 +326,9 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     cap = 0.0 if softcap is None else float(softcap)
     if cap < 0:
         raise ValueError("softcap must be positive (or None)")
-    if grad_scale is not None and lm_head_weight.dtype == torch.bfloat16:
-        return _FusedLinearCrossEntropyEager.apply(hidden_states, lm_head_weight, target,
-                                                   int(ignore_index), cap, bool(shift_labels),
-                                                   dw_accumulator, grad_scale)
     return _FusedLinearCrossEntropyNone.apply(hidden_states, lm_head_weight, target,
                                               int(ignore_index), cap, bool(shift_labels),
-                                              dw_accumulator)
+                                              dw_accumulator, grad_scale)
 
 
 class _CrossEntropyNone(torch.autograd.Function):

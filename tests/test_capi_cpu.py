@@ -120,3 +120,22 @@ def test_forward_workspace_is_small():
         assert 0 < ws <= cfg.T * per_row + 512
         assert ws < 0.02 * cfg.T * cfg.V * 2
     assert lib.mt_flce_forward_workspace_bytes(10, 0, 64, 100, 1) == 0
+
+
+def test_fused_planner_prefers_the_faster_path():
+    """The fused path pays where the 5% budget allows large row chunks
+    (configs 3, 4: measured 141 vs 165 ms and 264 vs 277 ms per step) and not
+    where it forces small ones (configs 2, 5: 62 vs 30 ms and 349 vs 223 ms)."""
+    lib = _lib.load()
+    want = {2: 0, 3: 1, 4: 1, 5: 0}
+    for key, pays_expected in want.items():
+        cfg = synth.CONFIGS[key]
+        n = int((synth.make_batch(cfg, 0, with_tensors=False)["target"] != -100).sum())
+        c, ws, pays = ctypes.c_int64(), ctypes.c_size_t(), ctypes.c_int()
+        assert lib.mt_flce_fused_plan(cfg.T, n, cfg.H, cfg.V, 1, 0, ctypes.byref(c),
+                                      ctypes.byref(ws), ctypes.byref(pays)) == 0
+        assert pays.value == pays_expected, key
+        assert c.value % 256 == 0 and 0 < ws.value <= 0.05 * cfg.T * cfg.V * 2
+    c, ws, pays = ctypes.c_int64(), ctypes.c_size_t(), ctypes.c_int()
+    assert lib.mt_flce_fused_plan(100, 50, 64, 100, 0, 0, ctypes.byref(c), ctypes.byref(ws),
+                                  ctypes.byref(pays)) == 3  # fp32: unsupported

@@ -20,12 +20,13 @@ import pytest
 import torch
 
 from mini_trainer_amd import fused_linear_cross_entropy, per_sample_loss_sums, synth
+from mini_trainer_amd.flce import FUSED_ENV
 from oracle.torch_path import rel_fro, torch_path
 
 pytestmark = pytest.mark.gpu
 
 
-def test_config3_full_size(gpu):
+def test_config3_full_size(gpu, monkeypatch):
     cfg = synth.CONFIGS[3]
     b = synth.make_batch(cfg, 0, with_tensors=False)
     T, H, V = cfg.T, cfg.H, cfg.V
@@ -40,6 +41,7 @@ def test_config3_full_size(gpu):
     scale = 1.0 / n
 
     def run(fused: bool):
+        monkeypatch.setenv(FUSED_ENV, "1" if fused else "0")
         Xd = X.detach().requires_grad_(True)
         dW = torch.zeros(V, H, dtype=torch.float32, device=gpu)
         loss = fused_linear_cross_entropy(Xd, W, y, dw_accumulator=dW,

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from mini_trainer_amd import fused_linear_cross_entropy
-from mini_trainer_amd.flce import BACKWARD_BUDGET_ENV, fused_plan
+from mini_trainer_amd.flce import BACKWARD_BUDGET_ENV, FUSED_ENV, fused_plan
 from mini_trainer_amd.none_reduction_losses import (
     liger_fixed_fused_linear_cross_entropy_none_reduction)
 from oracle.torch_path import rel_fro
@@ -20,6 +20,12 @@ from oracle.torch_path import rel_fro
 from test_gpu_parity import GRAD_RFRO, check_parity, make_case
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _always_fused(monkeypatch):
+    # these tests exercise the fused path itself, whatever the planner prefers
+    monkeypatch.setenv(FUSED_ENV, "1")
 
 
 def run_fused(dev, X, W, y, grad_scale, softcap=None, acc=None, backward_grad=None):
@@ -63,11 +69,12 @@ def test_fused_many_chunks_matches_general_path(gpu, monkeypatch):
     monkeypatch.setenv(BACKWARD_BUDGET_ENV, "1")
     X, W, y = make_case(1100, 128, 1300, torch.bfloat16, seed=7, mask_frac=0.2)
     n = int((y != -100).sum())
-    C, ws = fused_plan(1100, n, 128, 1300)
+    C, ws, _ = fused_plan(1100, n, 128, 1300)
     assert C == 256 and ws > 0
     loss, dX, dW = run_fused(gpu, X, W, y, 0.5)
     check_parity(X, W, y, loss, dX, dW, grad=torch.full((1100,), 0.5))
     # the general path on the same inputs: same loss bits, gradients within rounding
+    monkeypatch.setenv(FUSED_ENV, "0")
     Xd, Wd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True)
     acc = torch.zeros(W.shape, dtype=torch.float32, device=gpu)
     l2 = fused_linear_cross_entropy(Xd, Wd, y.to(gpu), dw_accumulator=acc)
