@@ -4,6 +4,12 @@ cross-entropy for mini_trainer-style padding-free training.
 The compute lives in libmt_flce.so (hand-written HIP, C ABI in
 include/mt_flce.h); this package is the PyTorch-facing host side.
 """
+from .causal_lm import (
+    causal_lm_loss,
+    cu_seqlens_from_lengths,
+    cu_seqlens_from_position_ids,
+    patch_causal_lm,
+)
 from .flce import (
     backward_plan,
     cross_entropy_none,
@@ -18,6 +24,10 @@ from .none_reduction_losses import (
 from .utils import patch_target_module
 
 __all__ = [
+    "causal_lm_loss",
+    "cu_seqlens_from_lengths",
+    "cu_seqlens_from_position_ids",
+    "patch_causal_lm",
     "backward_plan",
     "cross_entropy_none",
     "fused_linear_cross_entropy",
