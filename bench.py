@@ -11,7 +11,7 @@ Inputs are seeded synthetic tensors of the named configuration, resident in
 HBM before timing starts.
 
 Prints ONE JSON line (driver contract) with, in addition:
-  roofline      the logits GEMM (fwd4_kernel: 2*H*V*N MFMA flops per
+  roofline      the logits GEMM (fwd_bf16_kernel: 2*H*V*N MFMA flops per
                 launch, one launch over all valid rows through
                 mt_flce_forward) timed with HIP events through the C ABI on
                 the stream it is launched on, against the bf16 dense peak;
@@ -226,7 +226,7 @@ def main():
     peak_flops = PEAK_BF16 if cfg.dtype == torch.bfloat16 else PEAK_FP32
     C, Cv, bws = backward_plan(T, n, H, V, cfg.dtype)
 
-    fwd_kernel_name = "fwd4_kernel" if cfg.dtype == torch.bfloat16 else "fwd_kernel"
+    fwd_kernel_name = "fwd_bf16_kernel" if cfg.dtype == torch.bfloat16 else "fwd_kernel"
     fused_taken = fused and fused_plan(T, n_valid[0], H, V)[2]
     traffic = measured_traffic(cfg.key, fwd_kernel_name)
 

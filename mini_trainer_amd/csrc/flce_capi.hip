@@ -6,11 +6,12 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/mt_flce.h"
 #include "flce_kernels.h"
-#include "flce_kernels4.h"
+#include "flce_kernels_bf16.h"
 
 using namespace mtf;
 
@@ -63,6 +64,40 @@ int64_t device_cus() {
   return n;
 }
 
+// A second stream and two events per device, created once and kept for the
+// life of the process (default priority, non-blocking): the fused path runs
+// its dW GEMM beside its dX GEMM, which fills only tiles_m x tiles_n <= 192
+// of the CUs at config 3.  Streams and events are runtime handles, not
+// device memory; nothing here allocates buffers.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+int side_stream(SideStream** out) {
+  static SideStream cache[64];
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(MT_ERR_HIP, "hipGetDevice failed or device id out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  SideStream& c = cache[dev];
+  if (!c.stream) {
+    hipStream_t st = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess)
+      return fail(MT_ERR_HIP, "side stream / event creation failed: %s",
+                  hipGetErrorString(hipGetLastError()));
+    c.fork = f;
+    c.join = j;
+    c.stream = st;
+  }
+  *out = &c;
+  return MT_OK;
+}
+
 // Grid of a persistent kernel over `tiles` output tiles.
 inline uint32_t persistent_grid(int64_t tiles) { return (uint32_t)std::min(tiles, device_cus()); }
 inline int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
@@ -97,14 +132,22 @@ int check_common(const void* X, const void* W, int64_t T, int64_t H, int64_t V, 
   return MT_OK;
 }
 
-// Output tiles are 256 x 256 with one workgroup per CU (eight waves for the
-// bf16 kernels, four for fp32); threads = workgroup size.
+// Output tiles are 256 x 256 with one workgroup per CU of four waves (bf16
+// and fp32 kernels alike); threads = workgroup size.
 struct Geometry {
   int64_t tile_m, tile_n, slots;
   int threads;
 };
 inline Geometry geometry(int es) {
-  return es == 2 ? Geometry{256, 256, kCUs, kThreads4} : Geometry{256, 256, kCUs, kThreads};
+  return es == 2 ? Geometry{256, 256, kCUs, kThreadsBf} : Geometry{256, 256, kCUs, kThreads};
+}
+
+// One dX kernel instantiation per accumulation mode (uniform per launch).
+inline void launch_dx_bf16(const DxArgs& x, hipStream_t stream) {
+  static void (*const kern[4])(DxArgs) = {dx_bf16_kernel<kDxStore>, dx_bf16_kernel<kDxAdd>,
+                                          dx_bf16_kernel<kDxAddEmit>, dx_bf16_kernel<kDxEmit>};
+  hipLaunchKernelGGL(kern[x.mode & 3], dim3(persistent_grid(x.tiles_m * x.tiles_n)),
+                     dim3(kThreadsBf), 0, stream, x);
 }
 
 // ---------------------------------------------------------------- forward
@@ -267,8 +310,8 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
   a.S = nullptr;
   a.lds_b = 0;
   if constexpr (sizeof(T) == 2) {
-    void (*kern)(FwdArgs) = softcap > 0.f ? fwd4_kernel<true, false> : fwd4_kernel<false, false>;
-    hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * p.vt_total)), dim3(kThreads4), 0,
+    void (*kern)(FwdArgs) = softcap > 0.f ? fwd_bf16_kernel<true, false> : fwd_bf16_kernel<false, false>;
+    hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * p.vt_total)), dim3(kThreadsBf), 0,
                        stream, a);
   } else {
     hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
@@ -326,9 +369,9 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(softcap > 0.f ? recompute4_kernel<true> : recompute4_kernel<false>,
+        hipLaunchKernelGGL(softcap > 0.f ? recompute_bf16_kernel<true> : recompute_bf16_kernel<false>,
                            dim3(persistent_grid(r.tiles_m * r.tiles_n)),
-                           dim3(kThreads4), 0, stream, r);
+                           dim3(kThreadsBf), 0, stream, r);
       else
         hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
                            dim3(kThreads), 0, stream, r);
@@ -353,8 +396,7 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       x.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       x.tiles_n = (int32_t)cdiv(H, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(dx4_kernel, dim3(persistent_grid(x.tiles_m * x.tiles_n)), dim3(kThreads4), 0,
-                           stream, x);
+        launch_dx_bf16(x, stream);
       else
         hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
                            stream, x);
@@ -377,7 +419,7 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
       w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
       if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(dw4_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)), dim3(kThreads4), 0,
+        hipLaunchKernelGGL(dw_bf16_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)), dim3(kThreadsBf), 0,
                            stream, w);
       else
         hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
@@ -447,6 +489,8 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
                                        align_up((size_t)vt * C * 2 * sizeof(float)));
   char* XcT = reinterpret_cast<char*>(xy) + align_up((size_t)C * sizeof(float));
   const int64_t lds_b = Vp * 2, ldxt_b = C * 2;
+  SideStream* side = nullptr;
+  MT_TRY(side_stream(&side));
   for (int64_t c0 = 0; c0 < N; c0 += C) {
     const int64_t cn = std::min(C, N - c0);
     const int64_t tm = cdiv(cn, 256), cn_pad = tm * 256;
@@ -474,9 +518,9 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     a.xy = xy;
     a.S = S;
     a.lds_b = lds_b;
-    void (*kern)(FwdArgs) = softcap > 0.f ? fwd4_kernel<true, true> : fwd4_kernel<false, true>;
-    hipLaunchKernelGGL(kern, dim3(persistent_grid(tm * vt)), dim3(kThreads4), 0, stream, a);
-    MT_TRY(check_launch("fwd4_kernel"));
+    void (*kern)(FwdArgs) = softcap > 0.f ? fwd_bf16_kernel<true, true> : fwd_bf16_kernel<false, true>;
+    hipLaunchKernelGGL(kern, dim3(persistent_grid(tm * vt)), dim3(kThreadsBf), 0, stream, a);
+    MT_TRY(check_launch("fwd_bf16_kernel"));
     hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(cn, 4)), dim3(256), 0, stream,
                        part, xy, (int32_t)cn, (int32_t)vt, row_index + c0, loss, lse + c0);
     MT_TRY(check_launch("fwd_finalize_kernel"));
@@ -519,12 +563,26 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
     w.tiles_m = (int32_t)vt;
     w.tiles_n = (int32_t)cdiv(H, 256);
-    hipLaunchKernelGGL(dx4_kernel, dim3(persistent_grid(x.tiles_m * x.tiles_n)), dim3(kThreads4), 0,
-                       stream, x);
-    MT_TRY(check_launch("dx4_kernel"));
-    hipLaunchKernelGGL(dw4_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)), dim3(kThreads4), 0,
-                       stream, w);
-    MT_TRY(check_launch("dw4_kernel"));
+    // dX (tiles_m x tiles_n workgroups, fewer than the CUs) and dW (one
+    // workgroup per tile) run side by side: dW's workgroups take the CUs dX
+    // leaves free, then the rest.  Both read S and XcT, which the next chunk
+    // rewrites only after the join.
+    MT_TRY(hipEventRecord(side->fork, stream) == hipSuccess ? MT_OK
+                                                             : fail(MT_ERR_HIP, "hipEventRecord"));
+    MT_TRY(hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess
+               ? MT_OK
+               : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
+    launch_dx_bf16(x, stream);
+    MT_TRY(check_launch("dx_bf16_kernel"));
+    hipLaunchKernelGGL(dw_bf16_kernel, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreadsBf), 0,
+                       side->stream, w);
+    MT_TRY(check_launch("dw_bf16_kernel"));
+    MT_TRY(hipEventRecord(side->join, side->stream) == hipSuccess
+               ? MT_OK
+               : fail(MT_ERR_HIP, "hipEventRecord"));
+    MT_TRY(hipStreamWaitEvent(stream, side->join, 0) == hipSuccess
+               ? MT_OK
+               : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
   }
   return MT_OK;
 }

@@ -1,0 +1,388 @@
+// bf16 MFMA main loop shared by the GEMM-shaped kernels of the bf16 path
+// (gfx950).
+//
+// Workgroup = 4 waves (256 threads), one per CU, output tile 256 (A rows) x
+// 256 (B rows).  Wave w = (wm, wn) = (w >> 1, w & 1) owns a 128 x 128 block =
+// 8 x 8 fragments of v_mfma_f32_16x16x32_bf16: 256 accumulator registers
+// (the AGPR file), one wave per SIMD.  Per bf16 of K a wave reads 256
+// operand values from LDS for 16384 MACs, a third fewer LDS bytes per flop
+// than a 128 x 64 wave tile.
+//
+// K advances in stages of 64 bf16 (128 bytes per operand row, whole cache
+// lines); each stage is two halves kk of 32.  A stage's operands sit in one
+// of two 64 KiB LDS buffers (A 32 KiB + B 32 KiB), filled by LDS DMA
+// (buffer_load_dwordx4 ... lds: no VGPR staging, 32-bit lane offsets, the K
+// advance is the scalar offset).  With one wave per SIMD nothing else hides a
+// stall, so the loop is software pipelined inside the wave.  With F0 / F1 =
+// the kk = 0 / kk = 1 fragments of stage g:
+//
+//   phase 1   64 MFMAs on F0(g)        | 16 LDS reads of F1(g)
+//   sync      own LDS reads retired, own DMA of stage g + 1 landed, s_barrier
+//   phase 2   64 MFMAs on F1(g)        | 16 DMA instructions of stage g + 2
+//                                      |   into stage g's buffer,
+//                                      | 16 LDS reads of F0(g + 1)
+//
+// The barrier sits between two MFMA blocks whose operands are already in
+// registers; it publishes every wave's DMA of stage g + 1 and retires every
+// read of stage g, whose buffer is then refilled.  Inside a phase the order
+// is fixed with scheduling fences: groups of kMpg MFMAs, each followed by one
+// LDS read (and in phase 2 one DMA instruction).  Measured on gfx950 with
+// s_memtime around each part of the loop: a DS or VMEM instruction issued
+// within a couple of MFMAs of the previous one stalls the wave's MFMA issue
+// (a burst of 16 LDS reads costs more than the 64 MFMAs it sits beside), so
+// the memory instructions are spread thinly; LDS layouts are conflict-free.
+//
+// LDS tile formats (per operand per stage, 32 KiB):
+//   KC  operand rows contiguous along K (X rows, W rows in the logits GEMM,
+//       G rows in dX, X^T rows in dW): tile_off(row, chunk) of
+//       flce_device.h; a fragment is one ds_read_b128.
+//   TR  operand stored K-major (W in dX, G in dW): 64 K rows x 512 bytes,
+//       16-byte chunk j (8 columns) of K row k at k * 512 + (j ^ tr_swz(k)) *
+//       16.  A fragment is two ds_read_b64_tr_b16: within each 16-lane group
+//       the instruction hands lane i element (i & 3) of the 8-byte read of
+//       lane 4 e + (i >> 2), e = 0..3, so lanes reading (K row k0 + e,
+//       columns c0 + 4 q .. + 3) deliver to lane i column c0 + i at K rows
+//       k0 .. k0 + 3, which is the MFMA operand layout.  The reads are issued
+//       from inline asm (the compiler would otherwise wait for every
+//       in-flight LDS DMA before each one); their registers are tied to the
+//       explicit lgkmcnt wait that ends the phase.
+// Accumulator layout (B fragment issued as the MFMA's first operand): lane l
+// holds for fragment (fm, fn) four consecutive columns of one row:
+//   row = wm * 128 + fm * 16 + (l & 15),  col = wn * 128 + fn * 16 + 4 (l >> 4) + r.
+#pragma once
+
+#include "flce_gemm.h"
+
+namespace mtf {
+
+constexpr int kThreadsBf = 256;
+constexpr int kBKBf = 64;                   // bf16 K elements per stage
+constexpr int kTileBf = 256 * 128;          // one operand, one stage: 32 KiB
+constexpr int kStageBf = 2 * kTileBf;       // A + B
+constexpr int kLdsBf = 2 * kStageBf;        // two stages: 128 KiB
+constexpr int kNIBf = 8;                    // DMA instructions of 1 KiB per wave per operand tile
+// MFMAs per memory-instruction group inside a phase (see the header comment;
+// 2 and 3 measure the same on the logits GEMM, 1 and bursts are slower).
+constexpr int kMpg = 3;
+
+// XOR applied to the 16-byte chunk index of K row k in a TR tile.  The eight
+// K rows {0..3, 8..11} (+16, +32 ...) read by one half-wave of a transposing
+// fragment read get eight distinct even values, i.e. distinct 32-byte bank
+// groups; bit 3 also differs between rows 16 apart so that the halves
+// (lanes 0-15, 32-47) and (16-31, 48-63) are spread as well.
+__device__ __forceinline__ uint32_t tr_swz(uint32_t k) {
+  return ((k & 3u) << 1) | ((((k >> 3) ^ (k >> 4)) & 1u) << 3);
+}
+
+// Byte offset of an LDS location (address space 3) from a generic pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// ds_read_b64_tr_b16 outside the compiler's view of LDS accesses.
+__device__ __forceinline__ u32x2_t ds_read_tr(uint32_t addr) {
+  u32x2_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+// s_waitcnt vmcnt(0) only (expcnt and lgkmcnt left at their maximum).
+__device__ __forceinline__ void wait_vm0() {
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+}
+
+// s_waitcnt lgkmcnt(0) (memory operations do not move across it).
+__device__ __forceinline__ void lgkm_wait0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Nothing is scheduled across this point.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Raw buffer resource over `bytes` bytes from `base` (stride 0, dword 3 =
+// the gfx9 raw-buffer format word).  Operand loads go through buffer
+// instructions so that a lane's address is a 32-bit offset (one VGPR instead
+// of two) and the K advance of a stage is a scalar offset; every access is
+// kept in range by the callers, the resource bound only backs that up.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+constexpr uint32_t kWholeRange = 0xffffffffu;
+
+// 16-byte LDS DMA of one lane: LDS[dst + 16 lane] = mem[rsrc + voff + soff].
+__device__ __forceinline__ void dma16(rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)dst, 16, voff, soff, 0, 0);
+}
+
+// Operand whose rows are contiguous along K.  The 32 KiB tile is filled by
+// 32 DMA instructions of 1 KiB (8 per wave); lane l of instruction q lands at
+// q * 1024 + 16 l, so the lane -> (row, chunk) assignment is the inverse of
+// tile_off().
+struct KcOp {
+  static constexpr bool kTr = false;
+  rsrc_t rsrc;
+  uint32_t off[kNIBf];
+  uint32_t frag[2];  // LDS offset of this lane's fragment 0 for K halves 0, 1
+
+  __device__ __forceinline__ static uint32_t row_of(uint32_t i) {
+    const uint32_t l = lane_id(), q = wave_id() * kNIBf + i;
+    return (q >> 1) * 16 + ((l >> 3) & 1u) * 8 + (q & 1u) * 4 + (l >> 4);
+  }
+  __device__ __forceinline__ static uint32_t chunk_of(uint32_t i) {
+    const uint32_t l = lane_id(), q = wave_id() * kNIBf + i;
+    return (l & 7u) ^ ((q & 1u) * 4 + (l >> 4));
+  }
+  // row_off(r) = byte offset from the resource base of K element 0 of tile row r.
+  template <class RowOff>
+  __device__ __forceinline__ void set_rows(rsrc_t r, RowOff row_off) {
+    rsrc = r;
+#pragma unroll
+    for (uint32_t i = 0; i < kNIBf; ++i) off[i] = row_off(row_of(i)) + chunk_of(i) * 16u;
+  }
+  // wave_row0: first tile row of this wave's fragments.
+  __device__ __forceinline__ void init_frag(uint32_t wave_row0) {
+    const uint32_t l = lane_id();
+#pragma unroll
+    for (uint32_t kk = 0; kk < 2; ++kk) frag[kk] = tile_off(wave_row0 + (l & 15u), kk * 4 + (l >> 4));
+  }
+  // DMA instruction i (0..7) of this wave for stage kt.
+  __device__ __forceinline__ void issue_one(char* tile, int kt, int i) const {
+    dma16(rsrc, tile + (wave_id() * kNIBf + (uint32_t)i) * 1024u, off[i], (uint32_t)kt * 128u);
+  }
+  __device__ __forceinline__ void issue(char* tile, int kt) const {
+#pragma unroll
+    for (int i = 0; i < kNIBf; ++i) issue_one(tile, kt, i);
+  }
+  __device__ __forceinline__ u32x4_t read(const char* tile, int kk, int f) const {
+    return lds_read16(tile, frag[kk] + (uint32_t)f * 2048u);
+  }
+};
+
+// Operand stored K-major: row-major [K, 256-column tile].  Instruction q of
+// the tile covers K rows 2 q and 2 q + 1; lane l writes LDS chunk l & 31 of
+// K row 2 q + (l >> 5) and so loads global chunk (l & 31) ^ tr_swz(k).
+struct TrOp {
+  static constexpr bool kTr = true;
+  rsrc_t rsrc;
+  uint32_t base, ld_b;
+  int32_t k_limit;
+  uint32_t moff[kNIBf];
+  uint32_t krow[kNIBf];
+  uint32_t fbase[2][2], fxor[2][2];  // [kk][h]
+
+  // r, base: resource and byte offset of (K row 0, column 0) of the tile;
+  // k_limit: K rows that exist (rows at or beyond it read row k_limit - 1,
+  // whose products the caller discards or multiplies by zero); m_valid: tile
+  // columns that exist (the others read column 0 and are discarded later);
+  // wave_col0: first tile column of this wave's fragments, a multiple of 128
+  // (fragments f = 0..7 then stay inside one group of 16 chunks, so the XOR
+  // of tr_swz never leaves it).
+  __device__ __forceinline__ void init(rsrc_t r, uint32_t base_, uint32_t ld_b_, int32_t k_limit_,
+                                       int32_t m_valid, uint32_t wave_col0) {
+    rsrc = r;
+    base = base_;
+    ld_b = ld_b_;
+    k_limit = k_limit_;
+    const uint32_t l = lane_id(), w = wave_id();
+#pragma unroll
+    for (uint32_t i = 0; i < kNIBf; ++i) {
+      const uint32_t q = w * kNIBf + i;
+      const uint32_t k = 2 * q + (l >> 5);
+      const uint32_t j = (l & 31u) ^ tr_swz(k);
+      krow[i] = k;
+      const int32_t m0 = (int32_t)j * 8;
+      moff[i] = m0 < m_valid ? (uint32_t)m0 * 2u : 0u;
+    }
+    const uint32_t g = l >> 4, L = l & 15u, c0 = wave_col0 / 8u;
+#pragma unroll
+    for (uint32_t kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        const uint32_t k = 32 * kk + 8 * g + 4 * h + (L >> 2);
+        // fragment f sits at chunk c0 + 2 f + ((L & 3) >> 1); c0's low four
+        // bits and that lane bit join the XOR mask, so f enters as 32 f ^ mask
+        fbase[kk][h] = k * 512u + (c0 & ~15u) * 16u + (L & 1u) * 8u;
+        fxor[kk][h] = ((c0 & 15u) ^ tr_swz(k) ^ ((L & 3u) >> 1)) * 16u;
+      }
+  }
+  __device__ __forceinline__ void issue_one(char* tile, int kt, int i) const {
+    int32_t k = kt * kBKBf + (int32_t)krow[i];
+    k = k < k_limit ? k : k_limit - 1;
+    dma16(rsrc, tile + (wave_id() * kNIBf + (uint32_t)i) * 1024u,
+          base + (uint32_t)k * ld_b + moff[i], 0u);
+  }
+  __device__ __forceinline__ void issue(char* tile, int kt) const {
+#pragma unroll
+    for (int i = 0; i < kNIBf; ++i) issue_one(tile, kt, i);
+  }
+  // Two transposing reads into one 128-bit register tuple (inline asm; the
+  // phase ends with lgkm_wait0 and tie_frags before any use).
+  __device__ __forceinline__ u32x4_t read(const char* tile, int kk, int f) const {
+    const uint32_t t = lds_addr(tile);
+    const u32x2_t lo = ds_read_tr(t + fbase[kk][0] + ((32u * (uint32_t)f) ^ fxor[kk][0]));
+    const u32x2_t hi = ds_read_tr(t + fbase[kk][1] + ((32u * (uint32_t)f) ^ fxor[kk][1]));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
+  }
+};
+
+// Make fragments read by inline asm depend on the preceding explicit wait
+// (the compiler does not know that those reads complete only then).
+template <class Op>
+__device__ __forceinline__ void tie_frags(u32x4_t (&fr)[8]) {
+  if constexpr (Op::kTr) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(fr[i]));
+  }
+}
+
+// MFMA i (0..63) of a phase: fragment row fm = i / 8, column fn = i % 8.
+__device__ __forceinline__ void mfma_one(f32x4_t (&acc)[8][8], const u32x4_t (&fa)[8],
+                                         const u32x4_t (&fb)[8], int i) {
+  acc[i >> 3][i & 7] = mma_chunk<__bf16>(fb[i & 7], fa[i >> 3], acc[i >> 3][i & 7]);
+}
+
+// Stream of ntiles output tiles of KT stages each (see the header comment);
+// retarget(tile) re-points the operands before the first DMA of a tile,
+// init(tile, acc, second) sets a work item's accumulators before its first
+// MFMA (zero, or values loaded from memory that the item adds to), and
+// epilogue(tile, acc, second) runs after a work item's last MFMA and may use
+// LDS only beyond the two stage buffers (the next item's first two stages
+// are in flight or resident).
+//
+// k_split > 0 splits this workgroup's first tile: stages [k_split, KT) are
+// its first work item and stages [0, k_split) its last (second = true), so a
+// kernel whose epilogue accumulates into memory can stagger k_split over the
+// grid and spread its epilogues over time instead of having every workgroup
+// run one at the same moment.  Both parts of a tile belong to the same
+// workgroup and run one after the other.
+//
+// Each phase is one basic block: the retarget branch sits before phase 1,
+// and phase 2 always issues its DMA -- the two stages past the end reload
+// the last item's final stage into a buffer that is never read again.
+// Accumulators start at zero (the init hook of every kernel but dW).
+struct ZeroInit {
+  __device__ __forceinline__ void operator()(int, f32x4_t (&acc)[8][8], bool) const {
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn) acc[fm][fn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+};
+
+template <class A, class B, class Retarget, class Epi, class Init = ZeroInit>
+__device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int ntiles,
+                                              Retarget retarget, Epi epilogue, int k_split = 0,
+                                              Init init = Init()) {
+  if (KT <= 0 || ntiles <= 0) return;
+  const bool split = k_split > 0 && k_split < KT;
+  const int n_items = ntiles + (split ? 1 : 0);
+  // work item -> (tile, first stage, end stage)
+  auto item_tile = [&](int it) __attribute__((always_inline)) { return it < ntiles ? it : 0; };
+  auto item_kb = [&](int it) __attribute__((always_inline)) {
+    return !split ? 0 : (it == 0 ? k_split : 0);
+  };
+  auto item_ke = [&](int it) __attribute__((always_inline)) {
+    return split && it == ntiles ? k_split : KT;
+  };
+  // (item2, kt2) = coordinates of the next stage to be loaded; they stop at
+  // the last stage of the last item
+  int item2 = 0, kt2 = item_kb(0), ke2 = item_ke(0);
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (kt2 + 1 < ke2) {
+      ++kt2;
+    } else if (item2 + 1 < n_items) {
+      ++item2;
+      kt2 = item_kb(item2);
+      ke2 = item_ke(item2);
+      if (item_tile(item2) != item_tile(item2 - 1)) retarget(item_tile(item2));
+    }
+  };
+  retarget(0);
+  a.issue(lds, kt2);
+  b.issue(lds + kTileBf, kt2);
+  advance();
+  a.issue(lds + kStageBf, kt2);
+  b.issue(lds + kStageBf + kTileBf, kt2);
+  wait_vm0();
+  __builtin_amdgcn_s_barrier();
+  u32x4_t fa0[8], fb0[8], fa1[8], fb1[8];
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    fa0[f] = a.read(lds, 0, f);
+    fb0[f] = b.read(lds + kTileBf, 0, f);
+  }
+  lgkm_wait0();
+  tie_frags<A>(fa0);
+  tie_frags<B>(fb0);
+  int g = 0;
+  for (int it = 0; it < n_items; ++it) {
+    f32x4_t acc[8][8];
+    init(item_tile(it), acc, split && it == ntiles);
+    const int kb = item_kb(it), ke = item_ke(it);
+    for (int kt = kb; kt < ke; ++kt, ++g) {
+      advance();
+      sched_fence();
+      const char* st = lds + (g & 1) * kStageBf;
+      // phase 1: MFMAs on F0(g), LDS reads of F1(g)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+#pragma unroll
+        for (int j = 0; j < kMpg; ++j) mfma_one(acc, fa0, fb0, kMpg * i + j);
+        if (i & 1) fb1[i >> 1] = b.read(st + kTileBf, 1, i >> 1);
+        else fa1[i >> 1] = a.read(st, 1, i >> 1);
+        sched_fence();
+      }
+#pragma unroll
+      for (int i = 16 * kMpg; i < 64; ++i) mfma_one(acc, fa0, fb0, i);
+      sched_fence();
+      // every wave: reads of stage g retired, own DMA of stage g + 1 landed
+      lgkm_wait0();
+      tie_frags<A>(fa1);
+      tie_frags<B>(fb1);
+      wait_vm0();
+      __builtin_amdgcn_s_barrier();
+      sched_fence();
+      // phase 2: MFMAs on F1(g), DMA of stage g + 2 into stage g's buffer,
+      // LDS reads of F0(g + 1) (stale after the last stage, never used)
+      char* st2 = lds + (g & 1) * kStageBf;
+      const char* st1 = lds + ((g + 1) & 1) * kStageBf;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+#pragma unroll
+        for (int j = 0; j < kMpg; ++j) mfma_one(acc, fa1, fb1, kMpg * i + j);
+        if (i < kNIBf) a.issue_one(st2, kt2, i);
+        else b.issue_one(st2 + kTileBf, kt2, i - kNIBf);
+        if (i & 1) fb0[i >> 1] = b.read(st1 + kTileBf, 0, i >> 1);
+        else fa0[i >> 1] = a.read(st1, 0, i >> 1);
+        sched_fence();
+      }
+#pragma unroll
+      for (int i = 16 * kMpg; i < 64; ++i) mfma_one(acc, fa1, fb1, i);
+      sched_fence();
+      lgkm_wait0();
+      tie_frags<A>(fa0);
+      tie_frags<B>(fb0);
+    }
+    epilogue(item_tile(it), acc, split && it == ntiles);
+    // The next item's first fragments were read in the last phase; reading
+    // them again here (stage g is resident until phase 2 of stage g refills
+    // the other buffer) keeps their 64 registers free during the epilogue.
+    if (it + 1 < n_items) {
+      // (the memory clobber keeps these reads from being hoisted into the
+      // epilogue, where their registers would be live again)
+      lgkm_wait0();
+      const char* st = lds + (g & 1) * kStageBf;
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        fa0[f] = a.read(st, 0, f);
+        fb0[f] = b.read(st + kTileBf, 0, f);
+      }
+      lgkm_wait0();
+      tie_frags<A>(fa0);
+      tie_frags<B>(fb0);
+    }
+  }
+  wait_vm0();
+}
+
+}  // namespace mtf

@@ -1,0 +1,422 @@
+// bf16 kernels on the four-wave main loop (flce_gemm_bf16.h): output tiles
+// of 256 x 256, wave tiles 128 x 128.  Arguments, accumulation order and
+// epilogues are those of the generic kernels in flce_kernels.h (the fp32
+// path).
+#pragma once
+
+#include "flce_gemm_bf16.h"
+#include "flce_kernels.h"
+
+namespace mtf {
+
+#define MT_GEMM_BF16_KERNEL \
+  __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+
+// Wave (wm, wn) of the 2 x 2 wave grid, 8 x 8 fragments each.
+typedef EpiCoordsT<8, 2> EpiCoordsBf;
+
+// A copy of the wave coordinates that the compiler cannot treat as invariant
+// across the persistent tile loop: an epilogue's per-lane address arithmetic
+// is then formed inside the epilogue instead of being hoisted out of the
+// loop and spilled across the main loop.
+__device__ __forceinline__ EpiCoordsBf fresh(const EpiCoordsBf& ec) {
+  EpiCoordsBf e = ec;
+  asm volatile("" : "+v"(e.lane));
+  return e;
+}
+
+// Persistent schedule of the single-pass GEMM kernels: the grid holds
+// P <= #tiles workgroups (one per CU) and workgroup b takes the logical tiles
+// k * P + xcd_remap(b, P), k = 0, 1, ...  In every round the workgroups of one
+// XCD therefore hold a contiguous logical range (neighbouring tiles share
+// operand panels in that XCD's L2), and a tile's epilogue overlaps the first
+// operand loads of the workgroup's next tile.
+struct TileSeq {
+  uint32_t first, stride, total;
+  __device__ __forceinline__ explicit TileSeq(uint32_t total_) : total(total_) {
+    stride = gridDim.x;
+    first = xcd_remap(blockIdx.x, gridDim.x);
+  }
+  __device__ __forceinline__ int count() const {
+    return first < total ? (int)((total - first + stride - 1) / stride) : 0;
+  }
+  __device__ __forceinline__ uint32_t logical(int k) const { return first + (uint32_t)k * stride; }
+};
+
+// Forward: one 256 x 256 logits tile per work unit (A = gathered X rows, B =
+// W rows), persistent over the (row tile, vocabulary tile) grid.  The
+// epilogue reduces the tile to a (max, sum) partial per row -- lanes that
+// share a row through shuffles, the two wave columns through a 2 KiB LDS
+// region beside the stage buffers -- and writes it to part[vocab tile][row];
+// the lane that holds a row's label logit writes it to xy[row].  Nothing is
+// carried in registers from one tile to the next.
+// With kStoreS the tile's bf16-rounded logits (before the softcap) are also
+// written to S, row = compacted row of the chunk, column = vocabulary index:
+// the fused path forms G from them in place once the row's lse is known.
+constexpr int kFwdRedBf = 1 * 256 * 2 * (int)sizeof(float);
+// Row tiles per group of the forward's tile walk: W (the larger operand) is
+// streamed once per group, so wider groups cut its re-reads (8: 2% faster
+// than 4 at config 3; 16 is no better and costs L2 hits).
+constexpr uint32_t kFwdGroupBf = 8;
+
+// Forward tile epilogue of the bf16 kernels, one fragment row fm at a time
+// (a scheduling fence after each keeps a single row group's values in
+// registers; the unrolled whole-tile form spilled): the lane's 32 logits of
+// the row are rounded to bf16 once, stored to S (kStoreS, before the
+// softcap), soft-capped, masked past V, merged into the row's running
+// (max, sum) and scanned for the label (same arithmetic as
+// fwd_tile_epilogue).
+template <bool kCap, bool kStoreS>
+__device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], float (&m2)[8],
+                                                  float (&d)[8], const int32_t (&lbl)[8],
+                                                  const int32_t (&rglob)[8], int32_t vrow0,
+                                                  const EpiCoordsBf& ec, const FwdArgs& a) {
+  const int32_t ncol0 = vrow0 + ec.col(0);
+  int32_t rel[8];
+  bool hit = false;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    rel[fm] = lbl[fm] - ncol0;
+    hit |= lane_holds<8>(rel[fm]);
+  }
+  const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
+  const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    float v[8][4];
+    char* srow = kStoreS ? a.S + (int64_t)rglob[fm] * a.lds_b : nullptr;
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+      const uint32_t lo = pack_bf16x2(acc[fm][fn][0], acc[fm][fn][1]);
+      const uint32_t hi = pack_bf16x2(acc[fm][fn][2], acc[fm][fn][3]);
+      if (kStoreS) {
+        u32x2_t o;
+        o[0] = lo;
+        o[1] = hi;
+        *reinterpret_cast<u32x2_t*>(srow + (int64_t)(vrow0 + ec.col(fn)) * 2) = o;
+      }
+      v[fn][0] = __builtin_bit_cast(float, lo << 16);
+      v[fn][1] = __builtin_bit_cast(float, lo & 0xffff0000u);
+      v[fn][2] = __builtin_bit_cast(float, hi << 16);
+      v[fn][3] = __builtin_bit_cast(float, hi & 0xffff0000u);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = v[fn][r];
+        if (kCap) x = cap * tanh_approx(x * inv_cap);
+        x = ncol0 + fn * 16 + r < a.V ? x : -INFINITY;
+        v[fn][r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    }
+    const float mn = fmaxf(m2[fm], tmax * kLog2e);
+    float sum = 0.f;
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sum += fast_exp2(fmaf(v[fn][r], kLog2e, -mn));
+    d[fm] = fmaf(d[fm], fast_exp2(m2[fm] - mn), sum);
+    m2[fm] = mn;
+    if (any_hit) {
+      const int rl = rel[fm];
+      if (lane_holds<8>(rl) && rglob[fm] < a.N) {
+        float hitv = 0.f;
+#pragma unroll
+        for (int fn = 0; fn < 8; ++fn)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) hitv = (rl == fn * 16 + r) ? v[fn][r] : hitv;
+        a.xy[rglob[fm]] = hitv;
+      }
+    }
+    sched_fence();
+  }
+}
+
+template <bool kCap, bool kStoreS>
+MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf + kFwdRedBf];
+  const TileSeq seq((uint32_t)(a.tiles_m * a.vt_total));
+  const EpiCoordsBf ec0;
+  KcOp A, B;
+  A.init_frag(ec0.wm * 128);
+  B.init_frag(ec0.wn * 128);
+  mainloop_bf16(
+      lds, A, B, a.H / kBKBf, seq.count(),
+      [&](int k) __attribute__((always_inline)) {
+        uint32_t tm, tv;
+        grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, kFwdGroupBf, tm, tv);
+        const int32_t row0 = (int32_t)tm * 256, vrow0 = (int32_t)tv * 256;
+        A.set_rows(make_rsrc(a.X, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+          int32_t rr = row0 + (int32_t)r;
+          rr = rr < a.N ? rr : a.N - 1;
+          return (uint32_t)a.row_index[rr] * (uint32_t)a.ldx_b;
+        });
+        B.set_rows(make_rsrc(a.W, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+          int32_t v = vrow0 + (int32_t)r;
+          v = v < a.V ? v : a.V - 1;
+          return (uint32_t)v * (uint32_t)a.ldw_b;
+        });
+      },
+      [&](int k, f32x4_t(&acc)[8][8], bool second) __attribute__((always_inline)) {
+        const EpiCoordsBf ec = fresh(ec0);
+        uint32_t tm, tv;
+        grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, kFwdGroupBf, tm, tv);
+        const int32_t row0 = (int32_t)tm * 256;
+        int32_t rglob[8], lbl[8];
+        float m2[8], d[8];
+#pragma unroll
+        for (int fm = 0; fm < 8; ++fm) {
+          rglob[fm] = row0 + ec.row(fm);
+          lbl[fm] = rglob[fm] < a.N ? a.row_label[rglob[fm]] : -1;
+          m2[fm] = kNegBig;
+          d[fm] = 0.f;
+        }
+        fwd_epilogue_bf16<kCap, kStoreS>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
+        fwd_final_merge(lds + kLdsBf, m2, d, rglob, tv, ec, a);
+      });
+}
+
+// Backward step 1: A = X rows of the block (256 tokens), B = W rows (256
+// vocabulary entries); the epilogue writes G.
+template <bool kCap>
+MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
+  const EpiCoordsBf ec0;
+  KcOp A, B;
+  A.init_frag(ec0.wm * 128);
+  B.init_frag(ec0.wn * 128);
+  mainloop_bf16(
+      lds, A, B, a.H / kBKBf, seq.count(),
+      [&](int k) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        const int32_t row0 = (int32_t)tm * 256, vrow0 = a.v0 + (int32_t)tn * 256;
+        A.set_rows(make_rsrc(a.X, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+          int32_t rr = row0 + (int32_t)r;
+          rr = rr < a.Cn ? rr : a.Cn - 1;
+          return (uint32_t)a.row_index[rr] * (uint32_t)a.ldx_b;
+        });
+        B.set_rows(make_rsrc(a.W, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+          int32_t v = vrow0 + (int32_t)r;
+          v = v < a.V ? v : a.V - 1;
+          return (uint32_t)v * (uint32_t)a.ldw_b;
+        });
+      },
+      [&](int k, f32x4_t(&acc)[8][8], bool second) __attribute__((always_inline)) {
+        const EpiCoordsBf ec = fresh(ec0);
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        const int32_t row0 = (int32_t)tm * 256, col0 = (int32_t)tn * 256;
+        recompute_epilogue<__bf16, 8, kCap>(acc, a, ec, row0, col0);
+      });
+}
+
+// dX tile epilogue of the bf16 kernels (one mode of dx_epilogue per
+// instantiation: a kernel holding all four spilled accumulators), half a
+// fragment row at a time: bounds checks guard single stores, and a scheduling
+// fence after each half row -- in uniform control flow -- keeps one group's
+// values in registers.
+template <int kMode>
+__device__ __forceinline__ void dx_epilogue_bf16(const f32x4_t (&acc)[8][8], const DxArgs& a,
+                                                 const EpiCoordsBf& ec, int32_t row0, int32_t h0) {
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const int32_t rowl = row0 + ec.row(fm);
+    const bool rv = rowl < a.Cn;
+    float* arow = a.accbuf + (int64_t)(rv ? rowl : 0) * a.ld_acc;
+    char* xrow = kMode >= kDxAddEmit ? a.dX + (int64_t)a.row_index[rv ? rowl : 0] * a.lddx_b
+                                     : nullptr;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int fn = 4 * half + q;
+        const int32_t h = h0 + ec.col(fn);
+        f32x4_t v = acc[fm][fn];
+        if (rv && h < a.H) {
+          if (kMode == kDxAdd || kMode == kDxAddEmit)
+            v += *reinterpret_cast<const f32x4_t*>(arow + h);
+          if (kMode <= kDxAdd) {
+            *reinterpret_cast<f32x4_t*>(arow + h) = v;
+          } else {
+            u32x2_t o;
+            o[0] = pack_bf16x2(v[0], v[1]);
+            o[1] = pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<u32x2_t*>(xrow + (int64_t)h * 2) = o;
+          }
+        }
+      }
+      sched_fence();
+    }
+  }
+}
+
+// Backward step 2: A = G rows (256 tokens, K = vocabulary), B = W read
+// K-major (256 hidden columns).
+template <int kMode>
+MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
+  const EpiCoordsBf ec0;
+  KcOp A;
+  TrOp B;
+  A.init_frag(ec0.wm * 128);
+  mainloop_bf16(
+      lds, A, B, (a.kv + kBKBf - 1) / kBKBf, seq.count(),
+      [&](int k) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        const int32_t row0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
+        A.set_rows(make_rsrc(a.G, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+          return (uint32_t)(row0 + (int32_t)r) * (uint32_t)a.ldg_b;
+        });
+        B.init(make_rsrc(a.W, kWholeRange), (uint32_t)a.v0 * (uint32_t)a.ldw_b + (uint32_t)h0 * 2u,
+               (uint32_t)a.ldw_b, a.V - a.v0, a.H - h0, ec0.wn * 128);
+      },
+      [&](int k, f32x4_t(&acc)[8][8], bool second) __attribute__((always_inline)) {
+        const EpiCoordsBf ec = fresh(ec0);
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        dx_epilogue_bf16<kMode>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
+      });
+}
+
+// dW tiles accumulate in place: a tile's accumulators start from the fp32
+// values already in dW (when the kernel accumulates, or for the second part
+// of a split tile) -- 64 loads per lane in flight together, straight into
+// the accumulator registers -- and the epilogue only stores.  Rows past cv
+// and columns past H start at zero and are not stored.
+__device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& a,
+                                            const EpiCoordsBf& ec, int32_t m0, int32_t h0,
+                                            bool load) {
+  const float* base = a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0;
+  if (load && m0 + 256 <= a.cv && h0 + 256 <= a.H) {
+    // whole tile inside dW (all but the edge tiles): unconditional loads
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn)
+        acc[fm][fn] = *reinterpret_cast<const f32x4_t*>(base + (int64_t)ec.row(fm) * a.lddw +
+                                                        ec.col(fn));
+    return;
+  }
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const int32_t vl = m0 + ec.row(fm);
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+      const int32_t h = h0 + ec.col(fn);
+      f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (load && vl < a.cv && h < a.H)
+        v = *reinterpret_cast<const f32x4_t*>(base + (int64_t)ec.row(fm) * a.lddw + ec.col(fn));
+      acc[fm][fn] = v;
+    }
+  }
+}
+
+__device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const DwArgs& a,
+                                             const EpiCoordsBf& ec, int32_t m0, int32_t h0) {
+  float* base = a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const int32_t vl = m0 + ec.row(fm);
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+      const int32_t h = h0 + ec.col(fn);
+      if (vl < a.cv && h < a.H)
+        *reinterpret_cast<f32x4_t*>(base + (int64_t)ec.row(fm) * a.lddw + ec.col(fn)) = acc[fm][fn];
+    }
+    sched_fence();
+  }
+}
+
+// Backward step 3: A = G read K-major (256 vocabulary columns, K = tokens),
+// B = X^T rows of the block (256 hidden rows).
+MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
+  const EpiCoordsBf ec0;
+  TrOp A;
+  KcOp B;
+  B.init_frag(ec0.wn * 128);
+  mainloop_bf16(
+      lds, A, B, (a.kt_rows + kBKBf - 1) / kBKBf, seq.count(),
+      [&](int k) __attribute__((always_inline)) {
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        const int32_t m0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
+        A.init(make_rsrc(a.G, kWholeRange), (uint32_t)m0 * 2u, (uint32_t)a.ldg_b, a.g_rows,
+               a.g_cols - m0, ec0.wm * 128);
+        B.set_rows(make_rsrc(a.XcT, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+          int32_t h = h0 + (int32_t)r;
+          h = h < a.H ? h : a.H - 1;
+          return (uint32_t)h * (uint32_t)a.ldxt_b;
+        });
+      },
+      [&](int k, f32x4_t(&acc)[8][8], bool) __attribute__((always_inline)) {
+        const EpiCoordsBf ec = fresh(ec0);
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        dw_store_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
+      },
+      // persistent grid: stagger the split point over the workgroups, so
+      // that the tiles' dW loads and stores (256 KiB each) spread over the
+      // kernel instead of every workgroup issuing them at once (a grid of one
+      // workgroup per tile staggers by itself)
+      gridDim.x < (uint32_t)(a.tiles_m * a.tiles_n)
+          ? (int)(((int64_t)blockIdx.x * ((a.kt_rows + kBKBf - 1) / kBKBf)) / (int64_t)gridDim.x)
+          : 0,
+      [&](int k, f32x4_t(&acc)[8][8], bool second) __attribute__((always_inline)) {
+        const EpiCoordsBf ec = fresh(ec0);
+        uint32_t tm, tn;
+        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        // the second part of the split first tile adds to its first part
+        dw_load_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0 || second);
+      });
+}
+
+// Fused path: G = g_t (softmax(cap(S_t)) - onehot(y_t)) (1 - tanh^2), in place
+// over one chunk of the bf16 logits S written by fwd_bf16_kernel<*, true>.  One
+// workgroup per row; rows >= cn and columns >= V become 0.  HBM-bound: one
+// 16-byte read and one 16-byte write per 8 elements.
+__global__ __launch_bounds__(256) void softmax_grad_kernel(char* S, int64_t lds_b, int32_t cols,
+                                                           int32_t cn, int32_t V,
+                                                           const float* lse, const float* grad,
+                                                           int64_t gstride,
+                                                           const int32_t* row_index,
+                                                           const int32_t* row_label,
+                                                           float softcap) {
+  const int32_t row = blockIdx.x;
+  const bool rv = row < cn;
+  const float lse2 = rv ? lse[row] * kLog2e : 0.f;
+  const float g = rv ? grad[(int64_t)row_index[row] * gstride] : 0.f;
+  const int32_t y = rv ? row_label[row] : -1;
+  const bool cap = softcap > 0.f;
+  const float inv_cap = cap ? 1.0f / softcap : 0.f;
+  u32x4_t* p = reinterpret_cast<u32x4_t*>(S + (int64_t)row * lds_b);
+  for (int32_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
+    u32x4_t v = p[c / 8];
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = v[j / 2];
+      float x = __builtin_bit_cast(float, (j & 1) ? (w & 0xffff0000u) : (w << 16));
+      float dcap = 1.f;
+      if (cap) {
+        const float t = tanh_approx(x * inv_cap);
+        x = softcap * t;
+        dcap = 1.f - t * t;
+      }
+      float q = fast_exp2(fmaf(x, kLog2e, -lse2));
+      q -= (c + j == y) ? 1.f : 0.f;
+      o[j] = (rv && c + j < V) ? q * g * dcap : 0.f;
+    }
+    u32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = pack_bf16x2(o[2 * j], o[2 * j + 1]);
+    p[c / 8] = r;
+  }
+}
+
+}  // namespace mtf
