@@ -28,6 +28,13 @@
  *     ldx and ldw must be multiples of 8 and the base pointers 16-byte aligned.
  *     H must be a multiple of 64.  dtype selects bf16 (MFMA path) or fp32
  *     inputs; loss / lse / dW are always fp32, dX has the dtype of X.
+ *   - mt_flce_fused runs its dW GEMM on a second stream of the library's own
+ *     (one per device, created on first use, default priority), forked from
+ *     and joined back to the caller's stream with events inside the call; to
+ *     the caller the call stays ordered on its stream.
+ *   - Test hook: the environment variable MT_FLCE_GRID_CAP=n (> 0) caps the
+ *     bf16 GEMM grids at n workgroups, so small problems exercise the
+ *     multi-tile persistent schedules.  Unset in production.
  */
 #ifndef MT_FLCE_H
 #define MT_FLCE_H

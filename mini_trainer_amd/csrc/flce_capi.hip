@@ -6,6 +6,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -98,8 +99,21 @@ int side_stream(SideStream** out) {
   return MT_OK;
 }
 
+// Test hook: MT_FLCE_GRID_CAP=n (> 0) caps every bf16 GEMM grid at n
+// workgroups, so that small problems run the multi-tile persistent paths
+// (tile-to-tile pipelining, split first tiles) that otherwise only large
+// problems reach.  Read at each launch; unset or 0 = no cap.
+int64_t grid_cap() {
+  const char* e = std::getenv("MT_FLCE_GRID_CAP");
+  const long v = e ? std::strtol(e, nullptr, 10) : 0;
+  return v > 0 ? (int64_t)v : 0;
+}
+
 // Grid of a persistent kernel over `tiles` output tiles.
-inline uint32_t persistent_grid(int64_t tiles) { return (uint32_t)std::min(tiles, device_cus()); }
+inline uint32_t persistent_grid(int64_t tiles) {
+  const int64_t cap = grid_cap();
+  return (uint32_t)std::min(tiles, cap > 0 ? std::min(cap, device_cus()) : device_cus());
+}
 inline int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 inline size_t align_up(size_t a) { return (a + kAlign - 1) / kAlign * kAlign; }
 
@@ -574,8 +588,9 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
                : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
     launch_dx_bf16(x, stream);
     MT_TRY(check_launch("dx_bf16_kernel"));
-    hipLaunchKernelGGL(dw_bf16_kernel, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreadsBf), 0,
-                       side->stream, w);
+    const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
+    hipLaunchKernelGGL(dw_bf16_kernel, dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
+                       dim3(kThreadsBf), 0, side->stream, w);
     MT_TRY(check_launch("dw_bf16_kernel"));
     MT_TRY(hipEventRecord(side->join, side->stream) == hipSuccess
                ? MT_OK

@@ -236,3 +236,32 @@ def test_real_vocab_tail_qwen(gpu):
     X, W, y = make_case(384, 1536, 151936, torch.bfloat16, seed=21, mask_frac=0.5)
     loss, dX, dW = run_ours(gpu, X, W, y)
     check_parity(X, W, y, loss, dX, dW)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_persistent_multi_tile(gpu, monkeypatch, fused):
+    # A grid of 3 workgroups makes every bf16 GEMM walk several tiles per
+    # workgroup: tile-to-tile pipelining, the split first tile of dW (its two
+    # parts accumulate), and dW's fp32 tile preload are all exercised at small
+    # sizes.  The multi-block backward budget adds dX accumulation modes.
+    monkeypatch.setenv("MT_FLCE_GRID_CAP", "3")
+    if fused:
+        monkeypatch.setenv("MT_FLCE_FUSED", "1")
+    else:
+        monkeypatch.setenv(BACKWARD_BUDGET_ENV, "1")
+    X, W, y = make_case(700, 384, 2300, torch.bfloat16, seed=21, w_std=0.05)
+    grad = torch.rand(700, generator=torch.Generator().manual_seed(4)) + 0.5
+    Xd = X.to(gpu).requires_grad_(True)
+    Wd = W.to(gpu).requires_grad_(True)
+    acc = torch.zeros(W.shape, dtype=torch.float32, device=gpu)
+    n = int((y != -100).sum())
+    if fused:
+        g = torch.full((700,), 1.0 / n)
+        loss = fused_linear_cross_entropy(Xd, Wd, y.to(gpu), dw_accumulator=acc, grad_scale=1.0 / n)
+        (loss.float().sum() * (1.0 / n)).backward()
+    else:
+        g = grad
+        loss = fused_linear_cross_entropy(Xd, Wd, y.to(gpu), dw_accumulator=acc)
+        loss.backward(grad.to(gpu))
+    torch.cuda.synchronize()
+    check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), acc.cpu(), grad=g)
