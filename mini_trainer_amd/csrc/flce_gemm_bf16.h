@@ -9,28 +9,33 @@
 // than a 128 x 64 wave tile.
 //
 // K advances in stages of 64 bf16 (128 bytes per operand row, whole cache
-// lines); each stage is two halves kk of 32.  A stage's operands sit in one
-// of two 64 KiB LDS buffers (A 32 KiB + B 32 KiB), filled by LDS DMA
+// lines); each stage is two halves kk of 32.  A stage's operands sit in
+// 32 KiB LDS slots (A 256 rows x 128 bytes, B the same) of a 160 KiB ring --
+// two slots for one operand, three for the other -- filled by LDS DMA
 // (buffer_load_dwordx4 ... lds: no VGPR staging, 32-bit lane offsets, the K
 // advance is the scalar offset).  With one wave per SIMD nothing else hides a
 // stall, so the loop is software pipelined inside the wave.  With F0 / F1 =
 // the kk = 0 / kk = 1 fragments of stage g:
 //
 //   phase 1   64 MFMAs on F0(g)        | 16 LDS reads of F1(g)
+//                                      | 8 DMA instructions: three-slot
+//                                      |   operand, stage g + 2
 //   sync      own LDS reads retired, own DMA of stage g + 1 landed, s_barrier
-//   phase 2   64 MFMAs on F1(g)        | 16 DMA instructions of stage g + 2
-//                                      |   into stage g's buffer,
+//   phase 2   64 MFMAs on F1(g)        | 8 DMA instructions: two-slot
+//                                      |   operand, stage g + 2 (into the
+//                                      |   slot of its stage g)
 //                                      | 16 LDS reads of F0(g + 1)
 //
 // The barrier sits between two MFMA blocks whose operands are already in
 // registers; it publishes every wave's DMA of stage g + 1 and retires every
-// read of stage g, whose buffer is then refilled.  Inside a phase the order
+// read of stage g, whose slots are then refilled.  Inside a phase the order
 // is fixed with scheduling fences: groups of kMpg MFMAs, each followed by one
-// LDS read (and in phase 2 one DMA instruction).  Measured on gfx950 with
-// s_memtime around each part of the loop: a DS or VMEM instruction issued
-// within a couple of MFMAs of the previous one stalls the wave's MFMA issue
-// (a burst of 16 LDS reads costs more than the 64 MFMAs it sits beside), so
-// the memory instructions are spread thinly; LDS layouts are conflict-free.
+// LDS read (and every other group by one DMA instruction).  Measured on
+// gfx950 with s_memtime around each part of the loop: a DS or VMEM
+// instruction issued within a couple of MFMAs of the previous one stalls the
+// wave's MFMA issue (a burst of 16 LDS reads costs more than the 64 MFMAs it
+// sits beside), so the memory instructions are spread thinly, and the third
+// slot halves the DMA instructions per phase; LDS layouts are conflict-free.
 //
 // LDS tile formats (per operand per stage, 32 KiB):
 //   KC  operand rows contiguous along K (X rows, W rows in the logits GEMM,
@@ -58,8 +63,7 @@ namespace mtf {
 constexpr int kThreadsBf = 256;
 constexpr int kBKBf = 64;                   // bf16 K elements per stage
 constexpr int kTileBf = 256 * 128;          // one operand, one stage: 32 KiB
-constexpr int kStageBf = 2 * kTileBf;       // A + B
-constexpr int kLdsBf = 2 * kStageBf;        // two stages: 128 KiB
+constexpr int kLdsBf = 5 * kTileBf;         // ring of 2 + 3 operand slots: 160 KiB
 constexpr int kNIBf = 8;                    // DMA instructions of 1 KiB per wave per operand tile
 // MFMAs per memory-instruction group inside a phase (see the header comment;
 // 2 and 3 measure the same on the logits GEMM, 1 and bursts are slower).
@@ -241,24 +245,6 @@ __device__ __forceinline__ void mfma_one(f32x4_t (&acc)[8][8], const u32x4_t (&f
   acc[i >> 3][i & 7] = mma_chunk<__bf16>(fb[i & 7], fa[i >> 3], acc[i >> 3][i & 7]);
 }
 
-// Stream of ntiles output tiles of KT stages each (see the header comment);
-// retarget(tile) re-points the operands before the first DMA of a tile,
-// init(tile, acc, second) sets a work item's accumulators before its first
-// MFMA (zero, or values loaded from memory that the item adds to), and
-// epilogue(tile, acc, second) runs after a work item's last MFMA and may use
-// LDS only beyond the two stage buffers (the next item's first two stages
-// are in flight or resident).
-//
-// k_split > 0 splits this workgroup's first tile: stages [k_split, KT) are
-// its first work item and stages [0, k_split) its last (second = true), so a
-// kernel whose epilogue accumulates into memory can stagger k_split over the
-// grid and spread its epilogues over time instead of having every workgroup
-// run one at the same moment.  Both parts of a tile belong to the same
-// workgroup and run one after the other.
-//
-// Each phase is one basic block: the retarget branch sits before phase 1,
-// and phase 2 always issues its DMA -- the two stages past the end reload
-// the last item's final stage into a buffer that is never read again.
 // Accumulators start at zero (the init hook of every kernel but dW).
 struct ZeroInit {
   __device__ __forceinline__ void operator()(int, f32x4_t (&acc)[8][8], bool) const {
@@ -269,7 +255,39 @@ struct ZeroInit {
   }
 };
 
-template <class A, class B, class Retarget, class Epi, class Init = ZeroInit>
+// s_waitcnt vmcnt(8): every DMA but the last eight issued has landed.
+__device__ __forceinline__ void wait_vm8() {
+  __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));
+}
+
+// Stream of ntiles output tiles of KT stages each (see the header comment);
+// retarget(tile) re-points the operands before the first DMA of a tile,
+// init(tile, acc, second) sets a work item's accumulators before its first
+// MFMA (zero, or values loaded from memory that the item adds to), and
+// epilogue(tile, acc, second, scratch) runs after a work item's last MFMA;
+// `scratch` is a 32 KiB LDS buffer that is free until the next phase 1 (the
+// epilogue ends with a barrier if it uses it).
+//
+// LDS ring (160 KiB): the operand named by kThreeA (A if true, else B) has
+// three 32 KiB slots, the other two.  The three-slot operand's DMA of stage
+// g + 2 goes into the slot of its stage g - 1 during phase 1 (free since the
+// barrier that closed phase 1 of g - 1), the two-slot operand's into the
+// slot of its stage g during phase 2: eight DMA instructions per wave per
+// phase instead of sixteen in phase 2 alone, and one and a half stages of
+// lead for the three-slot operand, which is the one streamed from HBM (W;
+// G in dW).  The sync between the phases waits for all but the newest eight
+// DMAs (the three-slot operand's stage g + 2).
+//
+// k_split > 0 splits this workgroup's first tile: stages [k_split, KT) are
+// its first work item and stages [0, k_split) its last (second = true), so a
+// kernel whose tiles load and store memory around their MFMAs can stagger
+// k_split over the grid and spread that traffic over time.  Both parts of a
+// tile belong to the same workgroup and run one after the other.
+//
+// Each phase is one basic block: the retarget branch sits before phase 1,
+// and every phase issues its DMA -- the two stages past the end reload the
+// last item's final stage into slots that are never read again.
+template <bool kThreeA, class A, class B, class Retarget, class Epi, class Init = ZeroInit>
 __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int ntiles,
                                               Retarget retarget, Epi epilogue, int k_split = 0,
                                               Init init = Init()) {
@@ -284,8 +302,8 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
   auto item_ke = [&](int it) __attribute__((always_inline)) {
     return split && it == ntiles ? k_split : KT;
   };
-  // (item2, kt2) = coordinates of the next stage to be loaded; they stop at
-  // the last stage of the last item
+  // (item2, kt2) = coordinates of stage g + 2, the next stage to be loaded;
+  // they stop at the last stage of the last item
   int item2 = 0, kt2 = item_kb(0), ke2 = item_ke(0);
   auto advance = [&]() __attribute__((always_inline)) {
     if (kt2 + 1 < ke2) {
@@ -297,63 +315,86 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
       if (item_tile(item2) != item_tile(item2 - 1)) retarget(item_tile(item2));
     }
   };
+  // slots: the two-slot operand at [0, 64 KiB), the three-slot one above
+  char* const two0 = lds;
+  char* const three0 = lds + 2 * kTileBf;
+  auto slot_a = [&](int s2, int s3) __attribute__((always_inline)) {
+    return kThreeA ? three0 + s3 * kTileBf : two0 + s2 * kTileBf;
+  };
+  auto slot_b = [&](int s2, int s3) __attribute__((always_inline)) {
+    return kThreeA ? two0 + s2 * kTileBf : three0 + s3 * kTileBf;
+  };
   retarget(0);
-  a.issue(lds, kt2);
-  b.issue(lds + kTileBf, kt2);
+  a.issue(slot_a(0, 0), kt2);
+  b.issue(slot_b(0, 0), kt2);
   advance();
-  a.issue(lds + kStageBf, kt2);
-  b.issue(lds + kStageBf + kTileBf, kt2);
+  a.issue(slot_a(1, 1), kt2);
+  b.issue(slot_b(1, 1), kt2);
   wait_vm0();
   __builtin_amdgcn_s_barrier();
   u32x4_t fa0[8], fb0[8], fa1[8], fb1[8];
 #pragma unroll
   for (int f = 0; f < 8; ++f) {
-    fa0[f] = a.read(lds, 0, f);
-    fb0[f] = b.read(lds + kTileBf, 0, f);
+    fa0[f] = a.read(slot_a(0, 0), 0, f);
+    fb0[f] = b.read(slot_b(0, 0), 0, f);
   }
   lgkm_wait0();
   tie_frags<A>(fa0);
   tie_frags<B>(fb0);
-  int g = 0;
+  int g = 0, g3 = 0;  // stage being multiplied, g % 3
   for (int it = 0; it < n_items; ++it) {
     f32x4_t acc[8][8];
     init(item_tile(it), acc, split && it == ntiles);
     const int kb = item_kb(it), ke = item_ke(it);
-    for (int kt = kb; kt < ke; ++kt, ++g) {
+    for (int kt = kb; kt < ke; ++kt, ++g, g3 = (g3 == 2 ? 0 : g3 + 1)) {
       advance();
       sched_fence();
-      const char* st = lds + (g & 1) * kStageBf;
-      // phase 1: MFMAs on F0(g), LDS reads of F1(g)
+      const int g2 = g & 1, g2n = g2 ^ 1;
+      const int g3n = g3 == 2 ? 0 : g3 + 1, g3p = g3 == 0 ? 2 : g3 - 1;  // (g+1)%3, (g+2)%3
+      const char* ra = slot_a(g2, g3);
+      const char* rb = slot_b(g2, g3);
+      // phase 1: MFMAs on F0(g), LDS reads of F1(g), DMA of the three-slot
+      // operand's stage g + 2 (into the slot of its stage g - 1)
+      char* w3 = three0 + g3p * kTileBf;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
 #pragma unroll
         for (int j = 0; j < kMpg; ++j) mfma_one(acc, fa0, fb0, kMpg * i + j);
-        if (i & 1) fb1[i >> 1] = b.read(st + kTileBf, 1, i >> 1);
-        else fa1[i >> 1] = a.read(st, 1, i >> 1);
+        if (i & 1) fb1[i >> 1] = b.read(rb, 1, i >> 1);
+        else fa1[i >> 1] = a.read(ra, 1, i >> 1);
+        if (i & 1) {
+          if (kThreeA) a.issue_one(w3, kt2, i >> 1);
+          else b.issue_one(w3, kt2, i >> 1);
+        }
         sched_fence();
       }
 #pragma unroll
       for (int i = 16 * kMpg; i < 64; ++i) mfma_one(acc, fa0, fb0, i);
       sched_fence();
       // every wave: reads of stage g retired, own DMA of stage g + 1 landed
+      // (the three-slot operand's stage g + 2 may still be in flight)
       lgkm_wait0();
       tie_frags<A>(fa1);
       tie_frags<B>(fb1);
-      wait_vm0();
+      wait_vm8();
       __builtin_amdgcn_s_barrier();
       sched_fence();
-      // phase 2: MFMAs on F1(g), DMA of stage g + 2 into stage g's buffer,
-      // LDS reads of F0(g + 1) (stale after the last stage, never used)
-      char* st2 = lds + (g & 1) * kStageBf;
-      const char* st1 = lds + ((g + 1) & 1) * kStageBf;
+      // phase 2: MFMAs on F1(g), DMA of the two-slot operand's stage g + 2
+      // into the slot of its stage g, LDS reads of F0(g + 1) (stale after the
+      // last stage, never used)
+      char* w2 = two0 + g2 * kTileBf;
+      const char* ra1 = slot_a(g2n, g3n);
+      const char* rb1 = slot_b(g2n, g3n);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
 #pragma unroll
         for (int j = 0; j < kMpg; ++j) mfma_one(acc, fa1, fb1, kMpg * i + j);
-        if (i < kNIBf) a.issue_one(st2, kt2, i);
-        else b.issue_one(st2 + kTileBf, kt2, i - kNIBf);
-        if (i & 1) fb0[i >> 1] = b.read(st1 + kTileBf, 0, i >> 1);
-        else fa0[i >> 1] = a.read(st1, 0, i >> 1);
+        if (i & 1) {
+          if (kThreeA) b.issue_one(w2, kt2, i >> 1);
+          else a.issue_one(w2, kt2, i >> 1);
+        }
+        if (i & 1) fb0[i >> 1] = b.read(rb1, 0, i >> 1);
+        else fa0[i >> 1] = a.read(ra1, 0, i >> 1);
         sched_fence();
       }
 #pragma unroll
@@ -363,19 +404,24 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
       tie_frags<A>(fa0);
       tie_frags<B>(fb0);
     }
-    epilogue(item_tile(it), acc, split && it == ntiles);
+    // the three-slot operand's slot of the last stage (g - 1) is free until
+    // phase 1 of stage g refills it
+    epilogue(item_tile(it), acc, split && it == ntiles,
+             three0 + (g3 == 0 ? 2 : g3 - 1) * kTileBf);
     // The next item's first fragments were read in the last phase; reading
     // them again here (stage g is resident until phase 2 of stage g refills
-    // the other buffer) keeps their 64 registers free during the epilogue.
+    // the two-slot operand's other buffer) keeps their 64 registers free
+    // during the epilogue.
     if (it + 1 < n_items) {
       // (the memory clobber keeps these reads from being hoisted into the
       // epilogue, where their registers would be live again)
       lgkm_wait0();
-      const char* st = lds + (g & 1) * kStageBf;
+      const char* ra = slot_a(g & 1, g3);
+      const char* rb = slot_b(g & 1, g3);
 #pragma unroll
       for (int f = 0; f < 8; ++f) {
-        fa0[f] = a.read(st, 0, f);
-        fb0[f] = b.read(st + kTileBf, 0, f);
+        fa0[f] = a.read(ra, 0, f);
+        fb0[f] = b.read(rb, 0, f);
       }
       lgkm_wait0();
       tie_frags<A>(fa0);

@@ -46,14 +46,14 @@ struct TileSeq {
 // Forward: one 256 x 256 logits tile per work unit (A = gathered X rows, B =
 // W rows), persistent over the (row tile, vocabulary tile) grid.  The
 // epilogue reduces the tile to a (max, sum) partial per row -- lanes that
-// share a row through shuffles, the two wave columns through a 2 KiB LDS
-// region beside the stage buffers -- and writes it to part[vocab tile][row];
+// share a row through shuffles, the two wave columns through 2 KiB of the
+// ring slot the main loop hands to the epilogue -- and writes it to
+// part[vocab tile][row];
 // the lane that holds a row's label logit writes it to xy[row].  Nothing is
 // carried in registers from one tile to the next.
 // With kStoreS the tile's bf16-rounded logits (before the softcap) are also
 // written to S, row = compacted row of the chunk, column = vocabulary index:
 // the fused path forms G from them in place once the row's lse is known.
-constexpr int kFwdRedBf = 1 * 256 * 2 * (int)sizeof(float);
 // Row tiles per group of the forward's tile walk: W (the larger operand) is
 // streamed once per group, so wider groups cut its re-reads (8: 2% faster
 // than 4 at config 3; 16 is no better and costs L2 hits).
@@ -134,13 +134,13 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
 
 template <bool kCap, bool kStoreS>
 MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf + kFwdRedBf];
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
   const TileSeq seq((uint32_t)(a.tiles_m * a.vt_total));
   const EpiCoordsBf ec0;
   KcOp A, B;
   A.init_frag(ec0.wm * 128);
   B.init_frag(ec0.wn * 128);
-  mainloop_bf16(
+  mainloop_bf16<false>(
       lds, A, B, a.H / kBKBf, seq.count(),
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tv;
@@ -157,7 +157,7 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
           return (uint32_t)v * (uint32_t)a.ldw_b;
         });
       },
-      [&](int k, f32x4_t(&acc)[8][8], bool second) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], bool second, char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tv;
         grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, kFwdGroupBf, tm, tv);
@@ -172,7 +172,9 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
           d[fm] = 0.f;
         }
         fwd_epilogue_bf16<kCap, kStoreS>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
-        fwd_final_merge(lds + kLdsBf, m2, d, rglob, tv, ec, a);
+        fwd_final_merge(scratch, m2, d, rglob, tv, ec, a);
+        // the merge's LDS is the ring slot refilled in the next phase 1
+        __syncthreads();
       });
 }
 
@@ -186,7 +188,7 @@ MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
   KcOp A, B;
   A.init_frag(ec0.wm * 128);
   B.init_frag(ec0.wn * 128);
-  mainloop_bf16(
+  mainloop_bf16<false>(
       lds, A, B, a.H / kBKBf, seq.count(),
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tn;
@@ -203,7 +205,7 @@ MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
           return (uint32_t)v * (uint32_t)a.ldw_b;
         });
       },
-      [&](int k, f32x4_t(&acc)[8][8], bool second) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], bool second, char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
@@ -262,7 +264,7 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
   KcOp A;
   TrOp B;
   A.init_frag(ec0.wm * 128);
-  mainloop_bf16(
+  mainloop_bf16<false>(
       lds, A, B, (a.kv + kBKBf - 1) / kBKBf, seq.count(),
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tn;
@@ -274,7 +276,7 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
         B.init(make_rsrc(a.W, kWholeRange), (uint32_t)a.v0 * (uint32_t)a.ldw_b + (uint32_t)h0 * 2u,
                (uint32_t)a.ldw_b, a.V - a.v0, a.H - h0, ec0.wn * 128);
       },
-      [&](int k, f32x4_t(&acc)[8][8], bool second) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], bool second, char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
@@ -340,7 +342,7 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
   TrOp A;
   KcOp B;
   B.init_frag(ec0.wn * 128);
-  mainloop_bf16(
+  mainloop_bf16<true>(
       lds, A, B, (a.kt_rows + kBKBf - 1) / kBKBf, seq.count(),
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tn;
@@ -354,7 +356,7 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
           return (uint32_t)h * (uint32_t)a.ldxt_b;
         });
       },
-      [&](int k, f32x4_t(&acc)[8][8], bool) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], bool, char*) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
