@@ -165,14 +165,20 @@ struct KcOp {
 // Operand stored K-major: row-major [K, 256-column tile].  Instruction q of
 // the tile covers K rows 2 q and 2 q + 1; lane l writes LDS chunk l & 31 of
 // K row 2 q + (l >> 5) and so loads global chunk (l & 31) ^ tr_swz(k).
+// The per-lane state is small: the K row of instruction i is krow0 + 2 i,
+// and with k = 16 w + (l >> 5) + 2 i, tr_swz(k) depends on i only through
+// (i & 1, i >= 4), so the column offsets take four values; the fragment
+// reads' bases differ by constants and share one XOR mask (the lane's K row
+// inside a fragment read, 8 g + 4 h + (L >> 2), fixes tr_swz independently
+// of kk and h).
 struct TrOp {
   static constexpr bool kTr = true;
   rsrc_t rsrc;
   uint32_t base, ld_b;
   int32_t k_limit;
-  uint32_t moff[kNIBf];
-  uint32_t krow[kNIBf];
-  uint32_t fbase[2][2], fxor[2][2];  // [kk][h]
+  uint32_t krow0;
+  uint32_t moff[4];  // [(i >= 4) * 2 + (i & 1)]
+  uint32_t fbase, fxor;
 
   // r, base: resource and byte offset of (K row 0, column 0) of the tile;
   // k_limit: K rows that exist (rows at or beyond it read row k_limit - 1,
@@ -188,43 +194,38 @@ struct TrOp {
     ld_b = ld_b_;
     k_limit = k_limit_;
     const uint32_t l = lane_id(), w = wave_id();
+    krow0 = 16u * w + (l >> 5);
 #pragma unroll
-    for (uint32_t i = 0; i < kNIBf; ++i) {
-      const uint32_t q = w * kNIBf + i;
-      const uint32_t k = 2 * q + (l >> 5);
-      const uint32_t j = (l & 31u) ^ tr_swz(k);
-      krow[i] = k;
+    for (uint32_t p = 0; p < 4; ++p) {
+      const uint32_t i = (p >> 1) * 4 + (p & 1);  // representative i of the pattern
+      const uint32_t j = (l & 31u) ^ tr_swz(krow0 + 2 * i);
       const int32_t m0 = (int32_t)j * 8;
-      moff[i] = m0 < m_valid ? (uint32_t)m0 * 2u : 0u;
+      moff[p] = m0 < m_valid ? (uint32_t)m0 * 2u : 0u;
     }
     const uint32_t g = l >> 4, L = l & 15u, c0 = wave_col0 / 8u;
-#pragma unroll
-    for (uint32_t kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (uint32_t h = 0; h < 2; ++h) {
-        const uint32_t k = 32 * kk + 8 * g + 4 * h + (L >> 2);
-        // fragment f sits at chunk c0 + 2 f + ((L & 3) >> 1); c0's low four
-        // bits and that lane bit join the XOR mask, so f enters as 32 f ^ mask
-        fbase[kk][h] = k * 512u + (c0 & ~15u) * 16u + (L & 1u) * 8u;
-        fxor[kk][h] = ((c0 & 15u) ^ tr_swz(k) ^ ((L & 3u) >> 1)) * 16u;
-      }
+    const uint32_t k = 8 * g + (L >> 2);
+    // fragment f sits at chunk c0 + 2 f + ((L & 3) >> 1); c0's low four bits
+    // and that lane bit join the XOR mask, so f enters as 32 f ^ mask
+    fbase = k * 512u + (c0 & ~15u) * 16u + (L & 1u) * 8u;
+    fxor = ((c0 & 15u) ^ tr_swz(k) ^ ((L & 3u) >> 1)) * 16u;
   }
   __device__ __forceinline__ void issue_one(char* tile, int kt, int i) const {
-    int32_t k = kt * kBKBf + (int32_t)krow[i];
+    int32_t k = kt * kBKBf + (int32_t)(krow0 + 2u * (uint32_t)i);
     k = k < k_limit ? k : k_limit - 1;
     dma16(rsrc, tile + (wave_id() * kNIBf + (uint32_t)i) * 1024u,
-          base + (uint32_t)k * ld_b + moff[i], 0u);
+          base + (uint32_t)k * ld_b + moff[(i >= 4 ? 2 : 0) + (i & 1)], 0u);
   }
   __device__ __forceinline__ void issue(char* tile, int kt) const {
 #pragma unroll
     for (int i = 0; i < kNIBf; ++i) issue_one(tile, kt, i);
   }
   // Two transposing reads into one 128-bit register tuple (inline asm; the
-  // phase ends with lgkm_wait0 and tie_frags before any use).
+  // phase ends with lgkm_wait0 and tie_frags before any use).  K half kk and
+  // read h add (32 kk + 4 h) K rows of 512 bytes to the base.
   __device__ __forceinline__ u32x4_t read(const char* tile, int kk, int f) const {
-    const uint32_t t = lds_addr(tile);
-    const u32x2_t lo = ds_read_tr(t + fbase[kk][0] + ((32u * (uint32_t)f) ^ fxor[kk][0]));
-    const u32x2_t hi = ds_read_tr(t + fbase[kk][1] + ((32u * (uint32_t)f) ^ fxor[kk][1]));
+    const uint32_t t = lds_addr(tile) + fbase + ((32u * (uint32_t)f) ^ fxor);
+    const u32x2_t lo = ds_read_tr(t + (uint32_t)kk * 32u * 512u);
+    const u32x2_t hi = ds_read_tr(t + (uint32_t)kk * 32u * 512u + 4u * 512u);
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
   }
 };
@@ -247,7 +248,7 @@ __device__ __forceinline__ void mfma_one(f32x4_t (&acc)[8][8], const u32x4_t (&f
 
 // Accumulators start at zero (the init hook of every kernel but dW).
 struct ZeroInit {
-  __device__ __forceinline__ void operator()(int, f32x4_t (&acc)[8][8], bool) const {
+  __device__ __forceinline__ void operator()(int, f32x4_t (&acc)[8][8]) const {
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm)
 #pragma unroll
@@ -262,9 +263,9 @@ __device__ __forceinline__ void wait_vm8() {
 
 // Stream of ntiles output tiles of KT stages each (see the header comment);
 // retarget(tile) re-points the operands before the first DMA of a tile,
-// init(tile, acc, second) sets a work item's accumulators before its first
-// MFMA (zero, or values loaded from memory that the item adds to), and
-// epilogue(tile, acc, second, scratch) runs after a work item's last MFMA;
+// init(tile, acc) sets a tile's accumulators before its first MFMA (zero, or
+// values loaded from memory that the tile adds to), and
+// epilogue(tile, acc, scratch) runs after a tile's last MFMA;
 // `scratch` is a 32 KiB LDS buffer that is free until the next phase 1 (the
 // epilogue ends with a barrier if it uses it).
 //
@@ -278,41 +279,23 @@ __device__ __forceinline__ void wait_vm8() {
 // G in dW).  The sync between the phases waits for all but the newest eight
 // DMAs (the three-slot operand's stage g + 2).
 //
-// k_split > 0 splits this workgroup's first tile: stages [k_split, KT) are
-// its first work item and stages [0, k_split) its last (second = true), so a
-// kernel whose tiles load and store memory around their MFMAs can stagger
-// k_split over the grid and spread that traffic over time.  Both parts of a
-// tile belong to the same workgroup and run one after the other.
-//
 // Each phase is one basic block: the retarget branch sits before phase 1,
 // and every phase issues its DMA -- the two stages past the end reload the
-// last item's final stage into slots that are never read again.
+// last tile's final stage into slots that are never read again.
 template <bool kThreeA, class A, class B, class Retarget, class Epi, class Init = ZeroInit>
 __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int ntiles,
-                                              Retarget retarget, Epi epilogue, int k_split = 0,
-                                              Init init = Init()) {
+                                              Retarget retarget, Epi epilogue, Init init = Init()) {
   if (KT <= 0 || ntiles <= 0) return;
-  const bool split = k_split > 0 && k_split < KT;
-  const int n_items = ntiles + (split ? 1 : 0);
-  // work item -> (tile, first stage, end stage)
-  auto item_tile = [&](int it) __attribute__((always_inline)) { return it < ntiles ? it : 0; };
-  auto item_kb = [&](int it) __attribute__((always_inline)) {
-    return !split ? 0 : (it == 0 ? k_split : 0);
-  };
-  auto item_ke = [&](int it) __attribute__((always_inline)) {
-    return split && it == ntiles ? k_split : KT;
-  };
-  // (item2, kt2) = coordinates of stage g + 2, the next stage to be loaded;
-  // they stop at the last stage of the last item
-  int item2 = 0, kt2 = item_kb(0), ke2 = item_ke(0);
+  // (tile2, kt2) = coordinates of stage g + 2, the next stage to be loaded;
+  // they stop at the last stage of the last tile
+  int tile2 = 0, kt2 = 0;
   auto advance = [&]() __attribute__((always_inline)) {
-    if (kt2 + 1 < ke2) {
+    if (kt2 + 1 < KT) {
       ++kt2;
-    } else if (item2 + 1 < n_items) {
-      ++item2;
-      kt2 = item_kb(item2);
-      ke2 = item_ke(item2);
-      if (item_tile(item2) != item_tile(item2 - 1)) retarget(item_tile(item2));
+    } else if (tile2 + 1 < ntiles) {
+      kt2 = 0;
+      ++tile2;
+      retarget(tile2);
     }
   };
   // slots: the two-slot operand at [0, 64 KiB), the three-slot one above
@@ -342,11 +325,10 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
   tie_frags<A>(fa0);
   tie_frags<B>(fb0);
   int g = 0, g3 = 0;  // stage being multiplied, g % 3
-  for (int it = 0; it < n_items; ++it) {
+  for (int tile = 0; tile < ntiles; ++tile) {
     f32x4_t acc[8][8];
-    init(item_tile(it), acc, split && it == ntiles);
-    const int kb = item_kb(it), ke = item_ke(it);
-    for (int kt = kb; kt < ke; ++kt, ++g, g3 = (g3 == 2 ? 0 : g3 + 1)) {
+    init(tile, acc);
+    for (int kt = 0; kt < KT; ++kt, ++g, g3 = (g3 == 2 ? 0 : g3 + 1)) {
       advance();
       sched_fence();
       const int g2 = g & 1, g2n = g2 ^ 1;
@@ -406,13 +388,12 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
     }
     // the three-slot operand's slot of the last stage (g - 1) is free until
     // phase 1 of stage g refills it
-    epilogue(item_tile(it), acc, split && it == ntiles,
-             three0 + (g3 == 0 ? 2 : g3 - 1) * kTileBf);
-    // The next item's first fragments were read in the last phase; reading
+    epilogue(tile, acc, three0 + (g3 == 0 ? 2 : g3 - 1) * kTileBf);
+    // The next tile's first fragments were read in the last phase; reading
     // them again here (stage g is resident until phase 2 of stage g refills
     // the two-slot operand's other buffer) keeps their 64 registers free
     // during the epilogue.
-    if (it + 1 < n_items) {
+    if (tile + 1 < ntiles) {
       // (the memory clobber keeps these reads from being hoisted into the
       // epilogue, where their registers would be live again)
       lgkm_wait0();

@@ -157,7 +157,7 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
           return (uint32_t)v * (uint32_t)a.ldw_b;
         });
       },
-      [&](int k, f32x4_t(&acc)[8][8], bool second, char* scratch) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tv;
         grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, kFwdGroupBf, tm, tv);
@@ -205,7 +205,7 @@ MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
           return (uint32_t)v * (uint32_t)a.ldw_b;
         });
       },
-      [&](int k, f32x4_t(&acc)[8][8], bool second, char* scratch) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
@@ -276,7 +276,7 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
         B.init(make_rsrc(a.W, kWholeRange), (uint32_t)a.v0 * (uint32_t)a.ldw_b + (uint32_t)h0 * 2u,
                (uint32_t)a.ldw_b, a.V - a.v0, a.H - h0, ec0.wn * 128);
       },
-      [&](int k, f32x4_t(&acc)[8][8], bool second, char* scratch) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
@@ -285,22 +285,27 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
 }
 
 // dW tiles accumulate in place: a tile's accumulators start from the fp32
-// values already in dW (when the kernel accumulates, or for the second part
-// of a split tile) -- 64 loads per lane in flight together, straight into
-// the accumulator registers -- and the epilogue only stores.  Rows past cv
+// values already in dW (when the kernel accumulates) -- 64 loads per lane in
+// flight together, straight into the accumulator registers -- and the
+// epilogue only stores.  Rows past cv
 // and columns past H start at zero and are not stored.
 __device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& a,
                                             const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                             bool load) {
   const float* base = a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0;
   if (load && m0 + 256 <= a.cv && h0 + 256 <= a.H) {
-    // whole tile inside dW (all but the edge tiles): unconditional loads
+    // whole tile inside dW (all but the edge tiles): unconditional buffer
+    // loads off the tile's base, one lane offset for all 64 (fragment row fm
+    // adds a scalar offset, fragment column fn an immediate)
+    const rsrc_t r = make_rsrc(base, kWholeRange);
+    const uint32_t voff = ((uint32_t)ec.row(0) * (uint32_t)a.lddw + (uint32_t)ec.col(0)) * 4u;
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm)
 #pragma unroll
       for (int fn = 0; fn < 8; ++fn)
-        acc[fm][fn] = *reinterpret_cast<const f32x4_t*>(base + (int64_t)ec.row(fm) * a.lddw +
-                                                        ec.col(fn));
+        acc[fm][fn] = __builtin_bit_cast(
+            f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff + (uint32_t)fn * 64u,
+                                                           (uint32_t)(fm * 16) * (uint32_t)a.lddw * 4u, 0));
     return;
   }
 #pragma unroll
@@ -314,12 +319,29 @@ __device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& 
         v = *reinterpret_cast<const f32x4_t*>(base + (int64_t)ec.row(fm) * a.lddw + ec.col(fn));
       acc[fm][fn] = v;
     }
+    // one fragment row at a time (uniform point: the conditional loads above
+    // would otherwise all be hoisted and need 256 registers at once)
+    sched_fence();
   }
 }
 
 __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const DwArgs& a,
                                              const EpiCoordsBf& ec, int32_t m0, int32_t h0) {
   float* base = a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0;
+  if (m0 + 256 <= a.cv && h0 + 256 <= a.H) {
+    const rsrc_t r = make_rsrc(base, kWholeRange);
+    const uint32_t voff = ((uint32_t)ec.row(0) * (uint32_t)a.lddw + (uint32_t)ec.col(0)) * 4u;
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[fm][fn]), r,
+                                               voff + (uint32_t)fn * 64u,
+                                               (uint32_t)(fm * 16) * (uint32_t)a.lddw * 4u, 0);
+      sched_fence();
+    }
+    return;
+  }
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     const int32_t vl = m0 + ec.row(fm);
@@ -356,25 +378,17 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
           return (uint32_t)h * (uint32_t)a.ldxt_b;
         });
       },
-      [&](int k, f32x4_t(&acc)[8][8], bool, char*) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], char*) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         dw_store_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
       },
-      // persistent grid: stagger the split point over the workgroups, so
-      // that the tiles' dW loads and stores (256 KiB each) spread over the
-      // kernel instead of every workgroup issuing them at once (a grid of one
-      // workgroup per tile staggers by itself)
-      gridDim.x < (uint32_t)(a.tiles_m * a.tiles_n)
-          ? (int)(((int64_t)blockIdx.x * ((a.kt_rows + kBKBf - 1) / kBKBf)) / (int64_t)gridDim.x)
-          : 0,
-      [&](int k, f32x4_t(&acc)[8][8], bool second) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8]) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
-        // the second part of the split first tile adds to its first part
-        dw_load_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0 || second);
+        dw_load_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0);
       });
 }
 

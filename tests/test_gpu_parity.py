@@ -241,9 +241,10 @@ def test_real_vocab_tail_qwen(gpu):
 @pytest.mark.parametrize("fused", [False, True])
 def test_persistent_multi_tile(gpu, monkeypatch, fused):
     # A grid of 3 workgroups makes every bf16 GEMM walk several tiles per
-    # workgroup: tile-to-tile pipelining, the split first tile of dW (its two
-    # parts accumulate), and dW's fp32 tile preload are all exercised at small
-    # sizes.  The multi-block backward budget adds dX accumulation modes.
+    # workgroup: tile-to-tile pipelining through the LDS ring, the next
+    # tile's fragments re-read after each epilogue, and dW's fp32 tile
+    # preload (interior and edge tiles) are all exercised at small sizes.  The
+    # multi-block backward budget adds dX accumulation modes.
     monkeypatch.setenv("MT_FLCE_GRID_CAP", "3")
     if fused:
         monkeypatch.setenv("MT_FLCE_FUSED", "1")
