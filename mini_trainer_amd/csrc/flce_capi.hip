@@ -156,12 +156,14 @@ inline Geometry geometry(int es) {
   return es == 2 ? Geometry{256, 256, kCUs, kThreadsBf} : Geometry{256, 256, kCUs, kThreads};
 }
 
-// One dX kernel instantiation per accumulation mode (uniform per launch).
+// One dX kernel instantiation per accumulation mode (uniform per launch); one
+// workgroup per output tile (the kernel multiplies exactly one tile, so the
+// grid is never capped).
 inline void launch_dx_bf16(const DxArgs& x, hipStream_t stream) {
   static void (*const kern[4])(DxArgs) = {dx_bf16_kernel<kDxStore>, dx_bf16_kernel<kDxAdd>,
                                           dx_bf16_kernel<kDxAddEmit>, dx_bf16_kernel<kDxEmit>};
-  hipLaunchKernelGGL(kern[x.mode & 3], dim3(persistent_grid(x.tiles_m * x.tiles_n)),
-                     dim3(kThreadsBf), 0, stream, x);
+  hipLaunchKernelGGL(kern[x.mode & 3], dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreadsBf),
+                     0, stream, x);
 }
 
 // ---------------------------------------------------------------- forward

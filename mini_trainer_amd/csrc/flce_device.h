@@ -161,6 +161,12 @@ __device__ __forceinline__ void grouped_tile(uint32_t lid, uint32_t tiles_m, uin
   uint32_t in = lid - g * per_group;
   tm = first_m + in % gm;
   tn = in / gm;
+  // lid is uniform (a workgroup's tile index), but the divisions above run
+  // in vector registers and the compiler does not always prove the results
+  // uniform; a pointer or buffer resource built from them then becomes a
+  // per-lane waterfall loop around every memory instruction that uses it.
+  tm = __builtin_amdgcn_readfirstlane(tm);
+  tn = __builtin_amdgcn_readfirstlane(tn);
 }
 
 }  // namespace mtf

@@ -256,6 +256,12 @@ __device__ __forceinline__ void dx_epilogue_bf16(const f32x4_t (&acc)[8][8], con
 
 // Backward step 2: A = G rows (256 tokens, K = vocabulary), B = W read
 // K-major (256 hidden columns).
+// dX: one workgroup per output tile (grid = tiles_m x tiles_n, launched
+// that way by the host).  K = the block's vocabulary columns is long (hundreds
+// to thousands of stages), so a persistent tile loop gains nothing here, and
+// with one the compiler rotated accumulators through VGPRs and spilled inside
+// the K loop (the next tile's operand set-up lives in that loop); with a
+// single tile the loop compiles to the MFMAs, LDS reads and DMA only.
 template <int kMode>
 MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
@@ -265,7 +271,7 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
   TrOp B;
   A.init_frag(ec0.wm * 128);
   mainloop_bf16<false>(
-      lds, A, B, (a.kv + kBKBf - 1) / kBKBf, seq.count(),
+      lds, A, B, (a.kv + kBKBf - 1) / kBKBf, seq.count() > 0 ? 1 : 0,
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
