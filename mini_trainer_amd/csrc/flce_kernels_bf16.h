@@ -81,21 +81,28 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
   }
   const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
   const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
+  // S stores go through one buffer resource at the chunk base (the planner
+  // keeps the chunk below 4 GiB): a 32-bit row offset per fragment row and
+  // the fragment pair as a constant.  A lane holds 4 consecutive columns of
+  // each fragment (8 bytes); one v_permlane16_swap per dword pairs fragments
+  // fn = 2p, 2p + 1 so that lane group q (= lane / 16) holds 8 consecutive
+  // columns, 8 (2 (q & 1) + (q >> 1)) + 32 p, for one 16-byte store: half the
+  // store instructions, each writing 64 contiguous bytes per row instead of
+  // 32 (the store pipeline's cost goes with instructions x rows touched).
+  const rsrc_t srs = make_rsrc(kStoreS ? static_cast<const void*>(a.S) : a.xy, kWholeRange);
+  const uint32_t q = ec.lane >> 4;
+  const uint32_t scol = (uint32_t)vrow0 + ec.wn * 128u + 8u * (2u * (q & 1u) + (q >> 1));
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     float v[8][4];
-    char* srow = kStoreS ? a.S + (int64_t)rglob[fm] * a.lds_b : nullptr;
+    uint32_t slo[8], shi[8];
     float tmax = -INFINITY;
 #pragma unroll
     for (int fn = 0; fn < 8; ++fn) {
       const uint32_t lo = pack_bf16x2(acc[fm][fn][0], acc[fm][fn][1]);
       const uint32_t hi = pack_bf16x2(acc[fm][fn][2], acc[fm][fn][3]);
-      if (kStoreS) {
-        u32x2_t o;
-        o[0] = lo;
-        o[1] = hi;
-        *reinterpret_cast<u32x2_t*>(srow + (int64_t)(vrow0 + ec.col(fn)) * 2) = o;
-      }
+      slo[fn] = lo;
+      shi[fn] = hi;
       v[fn][0] = __builtin_bit_cast(float, lo << 16);
       v[fn][1] = __builtin_bit_cast(float, lo & 0xffff0000u);
       v[fn][2] = __builtin_bit_cast(float, hi << 16);
@@ -107,6 +114,20 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
         x = ncol0 + fn * 16 + r < a.V ? x : -INFINITY;
         v[fn][r] = x;
         tmax = fmaxf(tmax, x);
+      }
+    }
+    if (kStoreS) {
+      const uint32_t soff = (uint32_t)rglob[fm] * (uint32_t)a.lds_b + scol * 2u;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const auto l2 = __builtin_amdgcn_permlane16_swap(slo[2 * p], slo[2 * p + 1], false, false);
+        const auto h2 = __builtin_amdgcn_permlane16_swap(shi[2 * p], shi[2 * p + 1], false, false);
+        u32x4_t o;
+        o[0] = l2[0];
+        o[1] = h2[0];
+        o[2] = l2[1];
+        o[3] = h2[1];
+        __builtin_amdgcn_raw_buffer_store_b128(o, srs, soff + (uint32_t)p * 64u, 0, 0);
       }
     }
     const float mn = fmaxf(m2[fm], tmax * kLog2e);
