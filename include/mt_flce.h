@@ -33,8 +33,9 @@
  *     and joined back to the caller's stream with events inside the call; to
  *     the caller the call stays ordered on its stream.
  *   - Test hook: the environment variable MT_FLCE_GRID_CAP=n (> 0) caps the
- *     bf16 GEMM grids at n workgroups, so small problems exercise the
- *     multi-tile persistent schedules.  Unset in production.
+ *     persistent bf16 GEMM grids (logits, recompute, dW) at n workgroups, so
+ *     small problems exercise the multi-tile schedules; dX always runs one
+ *     workgroup per output tile.  Unset in production.
  */
 #ifndef MT_FLCE_H
 #define MT_FLCE_H

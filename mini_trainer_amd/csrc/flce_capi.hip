@@ -99,10 +99,11 @@ int side_stream(SideStream** out) {
   return MT_OK;
 }
 
-// Test hook: MT_FLCE_GRID_CAP=n (> 0) caps every bf16 GEMM grid at n
-// workgroups, so that small problems run the multi-tile persistent paths
-// (tile-to-tile pipelining, split first tiles) that otherwise only large
-// problems reach.  Read at each launch; unset or 0 = no cap.
+// Test hook: MT_FLCE_GRID_CAP=n (> 0) caps the persistent bf16 GEMM grids
+// (logits, recompute, dW) at n workgroups, so that small problems run the
+// multi-tile paths (tile-to-tile pipelining, the dW accumulator preload of a
+// workgroup's later tiles) that otherwise only large problems reach.  Read at
+// each launch; unset or 0 = no cap.
 int64_t grid_cap() {
   const char* e = std::getenv("MT_FLCE_GRID_CAP");
   const long v = e ? std::strtol(e, nullptr, 10) : 0;

@@ -240,10 +240,11 @@ def test_real_vocab_tail_qwen(gpu):
 
 @pytest.mark.parametrize("fused", [False, True])
 def test_persistent_multi_tile(gpu, monkeypatch, fused):
-    # A grid of 3 workgroups makes every bf16 GEMM walk several tiles per
-    # workgroup: tile-to-tile pipelining through the LDS ring, the next
-    # tile's fragments re-read after each epilogue, and dW's fp32 tile
-    # preload (interior and edge tiles) are all exercised at small sizes.  The
+    # A grid of 3 workgroups makes the persistent bf16 GEMMs (logits,
+    # recompute, dW) walk several tiles per workgroup: tile-to-tile
+    # pipelining through the LDS ring, the next tile's fragments re-read after
+    # each epilogue, and dW's fp32 tile preload (interior and edge tiles) are
+    # all exercised at small sizes (dX keeps one workgroup per tile).  The
     # multi-block backward budget adds dX accumulation modes.
     monkeypatch.setenv("MT_FLCE_GRID_CAP", "3")
     if fused:
