@@ -95,8 +95,17 @@ __device__ __forceinline__ void wait_vm0() {
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 }
 
-// s_waitcnt lgkmcnt(0) (memory operations do not move across it).
-__device__ __forceinline__ void lgkm_wait0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// s_waitcnt lgkmcnt(0) (memory operations do not move across it).  Issued
+// through the builtin so that the compiler's wait insertion sees it: after it
+// every LDS read counts as complete, and the next phase's MFMAs on fragments
+// read before it get no lgkmcnt waits of their own (as inline asm it was
+// invisible, and each first use of a fragment waited on the LDS reads the
+// phase itself had issued since).
+__device__ __forceinline__ void lgkm_wait0() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+  asm volatile("" ::: "memory");
+}
 
 // Nothing is scheduled across this point.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
