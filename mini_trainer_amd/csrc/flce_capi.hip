@@ -541,7 +541,8 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(cn, 4)), dim3(256), 0, stream,
                        part, xy, (int32_t)cn, (int32_t)vt, row_index + c0, loss, lse + c0);
     MT_TRY(check_launch("fwd_finalize_kernel"));
-    hipLaunchKernelGGL(softmax_grad_kernel, dim3((uint32_t)cn_pad), dim3(256), 0, stream, S, lds_b,
+    hipLaunchKernelGGL(softcap > 0.f ? softmax_grad_kernel<true> : softmax_grad_kernel<false>,
+                       dim3((uint32_t)cn_pad), dim3(256), 0, stream, S, lds_b,
                        (int32_t)Vp, (int32_t)cn, (int32_t)V, lse + c0, grad, gstride,
                        row_index + c0, row_label + c0, softcap);
     MT_TRY(check_launch("softmax_grad_kernel"));

@@ -423,6 +423,7 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
 // over one chunk of the bf16 logits S written by fwd_bf16_kernel<*, true>.  One
 // workgroup per row; rows >= cn and columns >= V become 0.  HBM-bound: one
 // 16-byte read and one 16-byte write per 8 elements.
+template <bool kCap>
 __global__ __launch_bounds__(256) void softmax_grad_kernel(char* S, int64_t lds_b, int32_t cols,
                                                            int32_t cn, int32_t V,
                                                            const float* lse, const float* grad,
@@ -435,18 +436,17 @@ __global__ __launch_bounds__(256) void softmax_grad_kernel(char* S, int64_t lds_
   const float lse2 = rv ? lse[row] * kLog2e : 0.f;
   const float g = rv ? grad[(int64_t)row_index[row] * gstride] : 0.f;
   const int32_t y = rv ? row_label[row] : -1;
-  const bool cap = softcap > 0.f;
-  const float inv_cap = cap ? 1.0f / softcap : 0.f;
+  const float inv_cap = kCap ? 1.0f / softcap : 0.f;
   u32x4_t* p = reinterpret_cast<u32x4_t*>(S + (int64_t)row * lds_b);
-  for (int32_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
-    u32x4_t v = p[c / 8];
+  // G of 8 consecutive columns starting at c
+  auto grad8 = [&](u32x4_t v, int32_t c) __attribute__((always_inline)) {
     float o[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t w = v[j / 2];
       float x = __builtin_bit_cast(float, (j & 1) ? (w & 0xffff0000u) : (w << 16));
       float dcap = 1.f;
-      if (cap) {
+      if (kCap) {
         const float t = tanh_approx(x * inv_cap);
         x = softcap * t;
         dcap = 1.f - t * t;
@@ -458,8 +458,20 @@ __global__ __launch_bounds__(256) void softmax_grad_kernel(char* S, int64_t lds_
     u32x4_t r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = pack_bf16x2(o[2 * j], o[2 * j + 1]);
-    p[c / 8] = r;
+    return r;
+  };
+  // four 16-byte loads in flight per thread before the first store (one at
+  // a time left the pass at 5.5 TB/s)
+  constexpr int32_t kStep = 256 * 8;
+  int32_t c = threadIdx.x * 8;
+  for (; c + 3 * kStep < cols; c += 4 * kStep) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = p[(c + k * kStep) / 8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) p[(c + k * kStep) / 8] = grad8(v[k], c + k * kStep);
   }
+  for (; c < cols; c += kStep) p[c / 8] = grad8(p[c / 8], c);
 }
 
 }  // namespace mtf
