@@ -28,12 +28,14 @@
  *     ldx and ldw must be multiples of 8 and the base pointers 16-byte aligned.
  *     H must be a multiple of 64.  dtype selects bf16 (MFMA path) or fp32
  *     inputs; loss / lse / dW are always fp32, dX has the dtype of X.
- *   - mt_flce_fused runs its dW GEMM on a second stream of the library's own
- *     (one per device, created on first use, default priority), forked from
- *     and joined back to the caller's stream with events inside the call; to
- *     the caller the call stays ordered on its stream.
+ *   - mt_flce_fused and the bf16 mt_flce_backward run their dW GEMMs on a
+ *     second stream of the library's own (one per device, created on first
+ *     use, default priority), beside dX, forked from and joined back to the
+ *     caller's stream with events inside the call; to the caller the call
+ *     stays ordered on its stream.
  *   - Test hook: the environment variable MT_FLCE_GRID_CAP=n (> 0) caps the
- *     persistent bf16 GEMM grids (logits, recompute, dW) at n workgroups, so
+ *     persistent bf16 GEMM grids (logits, recompute) and the dW grids at n
+ *     workgroups, so
  *     small problems exercise the multi-tile schedules; dX always runs one
  *     workgroup per output tile.  Unset in production.
  */

@@ -100,10 +100,10 @@ int side_stream(SideStream** out) {
 }
 
 // Test hook: MT_FLCE_GRID_CAP=n (> 0) caps the persistent bf16 GEMM grids
-// (logits, recompute, dW) at n workgroups, so that small problems run the
-// multi-tile paths (tile-to-tile pipelining, the dW accumulator preload of a
-// workgroup's later tiles) that otherwise only large problems reach.  Read at
-// each launch; unset or 0 = no cap.
+// (logits, recompute) and the dW grids at n workgroups, so that small
+// problems run the multi-tile paths (tile-to-tile pipelining, the dW
+// accumulator preload of a workgroup's later tiles) that otherwise only large
+// problems reach.  Read at each launch; unset or 0 = no cap.
 int64_t grid_cap() {
   const char* e = std::getenv("MT_FLCE_GRID_CAP");
   const long v = e ? std::strtol(e, nullptr, 10) : 0;
@@ -165,6 +165,35 @@ inline void launch_dx_bf16(const DxArgs& x, hipStream_t stream) {
                                           dx_bf16_kernel<kDxAddEmit>, dx_bf16_kernel<kDxEmit>};
   hipLaunchKernelGGL(kern[x.mode & 3], dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreadsBf),
                      0, stream, x);
+}
+
+// dX and dW of one block side by side: dX (tiles_m x tiles_n workgroups,
+// often fewer than the CUs or a partial last round) on the caller's stream,
+// dW (one workgroup per tile) on the library's side stream, forked from and
+// joined back to the caller's stream with events, so dW's workgroups take
+// the CUs dX leaves free and then the rest.  Both only read G and the X^T
+// block; whatever rewrites them is enqueued after the join.
+int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream) {
+  SideStream* side = nullptr;
+  MT_TRY(side_stream(&side));
+  MT_TRY(hipEventRecord(side->fork, stream) == hipSuccess ? MT_OK
+                                                           : fail(MT_ERR_HIP, "hipEventRecord"));
+  MT_TRY(hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess
+             ? MT_OK
+             : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
+  launch_dx_bf16(x, stream);
+  MT_TRY(check_launch("dx_bf16_kernel"));
+  const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
+  hipLaunchKernelGGL(dw_bf16_kernel, dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
+                     dim3(kThreadsBf), 0, side->stream, w);
+  MT_TRY(check_launch("dw_bf16_kernel"));
+  MT_TRY(hipEventRecord(side->join, side->stream) == hipSuccess
+             ? MT_OK
+             : fail(MT_ERR_HIP, "hipEventRecord"));
+  MT_TRY(hipStreamWaitEvent(stream, side->join, 0) == hipSuccess
+             ? MT_OK
+             : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
+  return MT_OK;
 }
 
 // ---------------------------------------------------------------- forward
@@ -412,12 +441,20 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       x.row_index = row_index + c0;
       x.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       x.tiles_n = (int32_t)cdiv(H, geo.tile_n);
-      if constexpr (sizeof(T) == 2)
-        launch_dx_bf16(x, stream);
-      else
-        hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
-                           stream, x);
-      MT_TRY(check_launch("dx_kernel"));
+      // dX with fewer tiles than CUs leaves CUs idle for its whole (long) K:
+      // dW then runs beside it on the side stream.  Otherwise dX and the
+      // persistent dW run one after the other on the caller's stream
+      // (measured: side by side costs config 3's general path 2%, gains
+      // config 5's 2%).
+      const bool beside = sizeof(T) == 2 && (int64_t)x.tiles_m * x.tiles_n < device_cus();
+      if (!beside) {
+        if constexpr (sizeof(T) == 2)
+          launch_dx_bf16(x, stream);
+        else
+          hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
+                             stream, x);
+        MT_TRY(check_launch("dx_kernel"));
+      }
 
       DwArgs w;
       w.G = G;
@@ -435,13 +472,18 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
       w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
       w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
-      if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(dw_bf16_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)), dim3(kThreadsBf), 0,
-                           stream, w);
-      else
-        hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
-                           stream, w);
-      MT_TRY(check_launch("dw_kernel"));
+      if (beside) {
+        // the next block's recompute (G) and gather (X^T) follow the join
+        MT_TRY(launch_dx_dw_bf16(x, w, stream));
+      } else {
+        if constexpr (sizeof(T) == 2)
+          hipLaunchKernelGGL(dw_bf16_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)),
+                             dim3(kThreadsBf), 0, stream, w);
+        else
+          hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
+                             stream, w);
+        MT_TRY(check_launch("dw_kernel"));
+      }
     }
   }
   return MT_OK;
@@ -506,8 +548,6 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
                                        align_up((size_t)vt * C * 2 * sizeof(float)));
   char* XcT = reinterpret_cast<char*>(xy) + align_up((size_t)C * sizeof(float));
   const int64_t lds_b = Vp * 2, ldxt_b = C * 2;
-  SideStream* side = nullptr;
-  MT_TRY(side_stream(&side));
   for (int64_t c0 = 0; c0 < N; c0 += C) {
     const int64_t cn = std::min(C, N - c0);
     const int64_t tm = cdiv(cn, 256), cn_pad = tm * 256;
@@ -581,27 +621,8 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
     w.tiles_m = (int32_t)vt;
     w.tiles_n = (int32_t)cdiv(H, 256);
-    // dX (tiles_m x tiles_n workgroups, fewer than the CUs) and dW (one
-    // workgroup per tile) run side by side: dW's workgroups take the CUs dX
-    // leaves free, then the rest.  Both read S and XcT, which the next chunk
-    // rewrites only after the join.
-    MT_TRY(hipEventRecord(side->fork, stream) == hipSuccess ? MT_OK
-                                                             : fail(MT_ERR_HIP, "hipEventRecord"));
-    MT_TRY(hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess
-               ? MT_OK
-               : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
-    launch_dx_bf16(x, stream);
-    MT_TRY(check_launch("dx_bf16_kernel"));
-    const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
-    hipLaunchKernelGGL(dw_bf16_kernel, dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
-                       dim3(kThreadsBf), 0, side->stream, w);
-    MT_TRY(check_launch("dw_bf16_kernel"));
-    MT_TRY(hipEventRecord(side->join, side->stream) == hipSuccess
-               ? MT_OK
-               : fail(MT_ERR_HIP, "hipEventRecord"));
-    MT_TRY(hipStreamWaitEvent(stream, side->join, 0) == hipSuccess
-               ? MT_OK
-               : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
+    // S and XcT are rewritten by the next chunk only after the join
+    MT_TRY(launch_dx_dw_bf16(x, w, stream));
   }
   return MT_OK;
 }
