@@ -314,8 +314,8 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
 // dW tiles accumulate in place: a tile's accumulators start from the fp32
 // values already in dW (when the kernel accumulates) -- 64 loads per lane in
 // flight together, straight into the accumulator registers -- and the
-// epilogue only stores.  Rows past cv
-// and columns past H start at zero and are not stored.
+// epilogue only stores.  Rows past cv and columns past H start at zero and
+// are not stored.
 __device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& a,
                                             const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                             bool load) {
