@@ -66,13 +66,16 @@ int64_t device_cus() {
 }
 
 // A second stream and two events per device, created once and kept for the
-// life of the process (default priority, non-blocking): the fused path runs
-// its dW GEMM beside its dX GEMM, which fills only tiles_m x tiles_n <= 192
-// of the CUs at config 3.  Streams and events are runtime handles, not
-// device memory; nothing here allocates buffers.
+// life of the process (default priority, non-blocking): dW GEMMs run beside
+// dX GEMMs that fill only part of the CUs (tiles_m x tiles_n = 192 at
+// config 3).  Streams and events are runtime handles, not device memory;
+// nothing here allocates buffers.  `use` serialises the fork / launch / join
+// sequences of calls from different host threads: the events are shared, and
+// a wait must capture the record its own call made.
 struct SideStream {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  std::mutex use;
 };
 
 int side_stream(SideStream** out) {
@@ -176,6 +179,7 @@ inline void launch_dx_bf16(const DxArgs& x, hipStream_t stream) {
 int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream) {
   SideStream* side = nullptr;
   MT_TRY(side_stream(&side));
+  std::lock_guard<std::mutex> lock(side->use);
   MT_TRY(hipEventRecord(side->fork, stream) == hipSuccess ? MT_OK
                                                            : fail(MT_ERR_HIP, "hipEventRecord"));
   MT_TRY(hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess

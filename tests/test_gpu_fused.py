@@ -8,6 +8,8 @@ backward rejects a gradient other than the promised one, and the chunking
 """
 from __future__ import annotations
 
+import threading
+
 import pytest
 import torch
 
@@ -113,3 +115,37 @@ def test_drop_in_reads_grad_scale_kwarg(gpu):
     (loss.sum() * 0.25).backward()
     check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), Wd.grad.cpu(),
                  grad=torch.full((256,), 0.25))
+
+
+def test_fused_concurrent_host_threads(gpu):
+    # Two host threads, each on its own stream, share the library's per-device
+    # side stream and fork / join events; every call must still order its dW
+    # after its own G and its caller's stream after its own dW.  Results are
+    # bit-identical to the same calls made one after the other.
+    cases = []
+    for seed in (31, 32):
+        X, W, y = make_case(600, 128, 1500, torch.bfloat16, seed=seed)
+        cases.append((X, W, y, 1.0 / int((y != -100).sum())))
+    ref = [run_fused(gpu, X, W, y, s) for X, W, y, s in cases]
+    streams = [torch.cuda.Stream(device=gpu) for _ in cases]
+    out = [None] * len(cases)
+    errors = []
+
+    def work(i):
+        try:
+            X, W, y, s = cases[i]
+            with torch.cuda.stream(streams[i]):
+                out[i] = run_fused(gpu, X, W, y, s)
+        except Exception as e:  # reported below, in the main thread
+            errors.append(e)
+
+    for _ in range(3):
+        threads = [threading.Thread(target=work, args=(i,)) for i in range(len(cases))]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert not errors, errors
+        for got, want in zip(out, ref):
+            for g, w in zip(got, want):
+                assert torch.equal(g, w)
