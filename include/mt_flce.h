@@ -35,7 +35,8 @@
  *     stays ordered on its stream.
  *   - Test hook: the environment variable MT_FLCE_GRID_CAP=n (> 0) caps the
  *     persistent bf16 GEMM grids (logits, recompute) and the dW grids at n
- *     workgroups, so
+ *     workgroups, and the general backward takes n as the CU count when it
+ *     decides whether dW runs beside dX, so
  *     small problems exercise the multi-tile schedules; dX always runs one
  *     workgroup per output tile.  Unset in production.
  */

@@ -245,7 +245,9 @@ def test_persistent_multi_tile(gpu, monkeypatch, fused):
     # pipelining through the LDS ring, the next tile's fragments re-read after
     # each epilogue, and dW's fp32 tile preload (interior and edge tiles) are
     # all exercised at small sizes (dX keeps one workgroup per tile).  The
-    # multi-block backward budget adds dX accumulation modes.
+    # multi-block backward budget adds dX accumulation modes, and with the
+    # cap standing in for a 3-CU GPU the general path runs dX and the
+    # persistent dW one after the other instead of side by side.
     monkeypatch.setenv("MT_FLCE_GRID_CAP", "3")
     if fused:
         monkeypatch.setenv("MT_FLCE_FUSED", "1")
