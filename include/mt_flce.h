@@ -36,9 +36,9 @@
  *   - Test hook: the environment variable MT_FLCE_GRID_CAP=n (> 0) caps the
  *     persistent bf16 GEMM grids (logits, recompute) and the dW grids at n
  *     workgroups, and the general backward takes n as the CU count when it
- *     decides whether dW runs beside dX, so
- *     small problems exercise the multi-tile schedules; dX always runs one
- *     workgroup per output tile.  Unset in production.
+ *     decides whether dW runs beside dX, so small problems exercise the
+ *     multi-tile schedules; dX always runs one workgroup per output tile.
+ *     Unset in production.
  */
 #ifndef MT_FLCE_H
 #define MT_FLCE_H
