@@ -69,6 +69,9 @@ def check_parity(X, W, y, loss, dX, dW, grad=None, softcap=None):
     (513, 192, 2065, torch.bfloat16),       # H not a multiple of 256
     (257, 64, 777, torch.float32),          # fp32 path
     (64, 896, 4096, torch.bfloat16),        # Qwen2.5-0.5B hidden size
+    (200, 1536, 2304, torch.bfloat16),      # config 2's hidden size (6 H tiles)
+    (160, 3584, 1100, torch.bfloat16),      # config 4's hidden size (14 H tiles), V tail
+    (96, 8192, 800, torch.bfloat16),        # config 5's hidden size: 128-stage logits K loop
 ])
 def test_parity_small(gpu, T, H, V, dtype):
     print(f"case T={T} H={H} V={V} {dtype}", flush=True)
