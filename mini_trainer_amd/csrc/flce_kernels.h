@@ -730,6 +730,19 @@ __device__ __forceinline__ float load_one(const char* p) {
   }
 }
 
+// 16 bytes of T from floats (bf16: rounded to nearest even).
+template <typename T>
+__device__ __forceinline__ void store_vec(char* p, const float (&x)[16 / sizeof(T)]) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<f32x4_t*>(p) = f32x4_t{x[0], x[1], x[2], x[3]};
+  } else {
+    u32x4_t v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    *reinterpret_cast<u32x4_t*>(p) = v;
+  }
+}
+
 // Block-wide merge of per-thread (m, d) states; result valid in all threads.
 __device__ __forceinline__ void block_lse_merge(float& m, float& d, float* sm) {
 #pragma unroll
@@ -776,9 +789,7 @@ __global__ __launch_bounds__(256) void ce_forward_kernel(const char* logits, int
   const int64_t head = mis ? min<int64_t>(VEC - mis, V) : 0;
   const int64_t nvec = (V - head) / VEC;
   const char* vrow = row + head * E;
-  for (int64_t i = threadIdx.x; i < nvec; i += 256) {
-    float x[VEC];
-    load_vec<T>(vrow + i * 16, x);
+  auto merge_vec = [&](const float (&x)[VEC]) __attribute__((always_inline)) {
     float mx = x[0];
 #pragma unroll
     for (int j = 1; j < VEC; ++j) mx = fmaxf(mx, x[j]);
@@ -788,6 +799,20 @@ __global__ __launch_bounds__(256) void ce_forward_kernel(const char* logits, int
     for (int j = 0; j < VEC; ++j) s += fast_exp2(fmaf(x[j], kLog2e, -mn));
     d = fmaf(d, fast_exp2(m - mn), s);
     m = mn;
+  };
+  // four 16-byte loads in flight per thread
+  int64_t i = threadIdx.x;
+  for (; i + 3 * 256 < nvec; i += 4 * 256) {
+    float x[4][VEC];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) load_vec<T>(vrow + (i + k * 256) * 16, x[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) merge_vec(x[k]);
+  }
+  for (; i < nvec; i += 256) {
+    float x[VEC];
+    load_vec<T>(vrow + i * 16, x);
+    merge_vec(x);
   }
   for (int64_t v = threadIdx.x; v < head; v += 256) lse_merge(m, d, load_one<T>(row + v * E) * kLog2e, 1.0f);
   for (int64_t v = head + nvec * VEC + threadIdx.x; v < V; v += 256)
@@ -814,7 +839,54 @@ __global__ __launch_bounds__(256) void ce_backward_kernel(const char* logits, in
   const float l2 = valid ? lse[t] * kLog2e : 0.f;
   const char* row = logits + t * ld_b;
   char* drow = dlogits + t * ldd_b;
-  // pairs of elements so bf16 rows are written 4 bytes at a time
+  constexpr int VEC = 16 / E;
+  if (((reinterpret_cast<uintptr_t>(row) | reinterpret_cast<uintptr_t>(drow)) & 15u) == 0) {
+    // 16-byte rows (the usual case): whole vectors, four loads in flight per
+    // thread, then the scalar tail of V mod VEC
+    const int64_t nvec = V / VEC;
+    auto grad_vec = [&](float (&x)[VEC], int64_t c0) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float p = fast_exp2(fmaf(x[j], kLog2e, -l2));
+        x[j] = valid ? g * (p - (c0 + j == y ? 1.f : 0.f)) : 0.f;
+      }
+    };
+    int64_t i = threadIdx.x;
+    for (; i + 3 * 256 < nvec; i += 4 * 256) {
+      float x[4][VEC];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (valid) load_vec<T>(row + (i + k * 256) * 16, x[k]);
+        else
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) x[k][j] = 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        grad_vec(x[k], (i + k * 256) * VEC);
+        store_vec<T>(drow + (i + k * 256) * 16, x[k]);
+      }
+    }
+    for (; i < nvec; i += 256) {
+      float x[VEC];
+      if (valid) load_vec<T>(row + i * 16, x);
+      else
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) x[j] = 0.f;
+      grad_vec(x, i * VEC);
+      store_vec<T>(drow + i * 16, x);
+    }
+    for (int64_t c = nvec * VEC + threadIdx.x; c < V; c += 256) {
+      float r = 0.f;
+      if (valid) r = g * (fast_exp2(fmaf(load_one<T>(row + c * E), kLog2e, -l2)) - (c == y ? 1.f : 0.f));
+      if constexpr (E == 4)
+        reinterpret_cast<float*>(drow)[c] = r;
+      else
+        *reinterpret_cast<uint16_t*>(drow + c * 2) = (uint16_t)(pack_bf16x2(r, 0.f) & 0xffffu);
+    }
+    return;
+  }
+  // any alignment: pairs of elements so bf16 rows are written 4 bytes at a time
   for (int64_t v = 2 * threadIdx.x; v < V; v += 512) {
     float o[2];
 #pragma unroll
