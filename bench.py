@@ -83,6 +83,52 @@ def cpu_baseline(cfg, budget_s: float):
     }
 
 
+def torch_gpu_path(data, W, scale: float, steps: int = 2):
+    """The reference's torch path on the GPU as a comparator: per minibatch
+    F.linear in the model dtype (TF/models/llama/modeling_llama.py:480), the
+    fp32 upcast (TF/loss/loss_utils.py:59), F.cross_entropy(reduction='none')
+    (none_reduction_losses.py:35), sum, .item(), backward with the uniform
+    scale (train.py:98-104).  It materialises T x V logits, their fp32 copy,
+    the saved log-softmax and its gradient (~16 bytes per logit), so it runs
+    only where that fits beside what is already allocated."""
+    dev = W.device
+    T, V = data[0][0].shape[0], W.shape[0]
+    need = 16 * T * V + (8 << 30)
+    free, total = torch.cuda.mem_get_info(dev)
+    if need > free:
+        return {"skipped": f"needs ~{need / 1e9:.0f} GB of device memory, {free / 1e9:.0f} GB free"}
+    Wr = W.detach().requires_grad_(True)
+
+    def step():
+        for X, y in data:
+            Xr = X.detach().requires_grad_(True)
+            logits = torch.nn.functional.linear(Xr, Wr).float()
+            loss = torch.nn.functional.cross_entropy(logits, y, ignore_index=-100, reduction="none")
+            s = loss.sum()
+            s.item()
+            (s * scale).backward()
+            del logits, loss, s, Xr
+        Wr.grad = None
+
+    try:
+        step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+    except torch.cuda.OutOfMemoryError as e:  # reported, not fatal: a comparator only
+        Wr.grad = None
+        torch.cuda.empty_cache()
+        return {"skipped": f"out of memory ({str(e).splitlines()[0][:80]})"}
+    ms = e0.elapsed_time(e1) / steps
+    torch.cuda.empty_cache()
+    return {"ms_per_step": ms, "tokens_per_s": T * len(data) / (ms / 1e3), "steps": steps,
+            "path": "F.linear -> .float() -> F.cross_entropy(reduction='none') -> backward (torch on the GPU)"}
+
+
 def measured_traffic(key: int, kernel: str):
     """HBM bytes per launch of the dominant kernel, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload (calibrated
@@ -119,6 +165,8 @@ def main():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-torch-gpu", action="store_true",
+                    help="skip the reference torch path on the GPU (a comparator, not the metric)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (the reference point that scales "
                          "FETCH_SIZE / WRITE_SIZE counter readings to bytes) and exit")
@@ -276,6 +324,13 @@ def main():
             "peak_memory_GB": peak / 1e9,
         },
     }
+    if not args.no_torch_gpu:
+        del ws
+        torch.cuda.empty_cache()
+        tg = torch_gpu_path(data, W, scale)
+        if "ms_per_step" in tg:
+            tg["speedup_of_value"] = out["value"] / tg["tokens_per_s"]
+        out["torch_gpu_path"] = tg
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget_s)
     print(json.dumps(out), flush=True)
