@@ -360,7 +360,10 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
   a.S = nullptr;
   a.lds_b = 0;
   if constexpr (sizeof(T) == 2) {
-    void (*kern)(FwdArgs) = softcap > 0.f ? fwd_bf16_kernel<true, false> : fwd_bf16_kernel<false, false>;
+    static void (*const kerns[2][2])(FwdArgs) = {
+        {fwd_bf16_kernel<false, false, false>, fwd_bf16_kernel<false, false, true>},
+        {fwd_bf16_kernel<true, false, false>, fwd_bf16_kernel<true, false, true>}};
+    void (*kern)(FwdArgs) = kerns[softcap > 0.f][V % 256 != 0];
     hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * p.vt_total)), dim3(kThreadsBf), 0,
                        stream, a);
   } else {
@@ -582,7 +585,10 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     a.xy = xy;
     a.S = S;
     a.lds_b = lds_b;
-    void (*kern)(FwdArgs) = softcap > 0.f ? fwd_bf16_kernel<true, true> : fwd_bf16_kernel<false, true>;
+    static void (*const kerns[2][2])(FwdArgs) = {
+        {fwd_bf16_kernel<false, true, false>, fwd_bf16_kernel<false, true, true>},
+        {fwd_bf16_kernel<true, true, false>, fwd_bf16_kernel<true, true, true>}};
+    void (*kern)(FwdArgs) = kerns[softcap > 0.f][V % 256 != 0];
     hipLaunchKernelGGL(kern, dim3(persistent_grid(tm * vt)), dim3(kThreadsBf), 0, stream, a);
     MT_TRY(check_launch("fwd_bf16_kernel"));
     hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(cn, 4)), dim3(256), 0, stream,

@@ -66,7 +66,7 @@ constexpr uint32_t kFwdGroupBf = 8;
 // softcap), soft-capped, masked past V, merged into the row's running
 // (max, sum) and scanned for the label (same arithmetic as
 // fwd_tile_epilogue).
-template <bool kCap, bool kStoreS>
+template <bool kCap, bool kStoreS, bool kTail>
 __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], float (&m2)[8],
                                                   float (&d)[8], const int32_t (&lbl)[8],
                                                   const int32_t (&rglob)[8], int32_t vrow0,
@@ -111,7 +111,7 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
       for (int r = 0; r < 4; ++r) {
         float x = v[fn][r];
         if (kCap) x = cap * tanh_approx(x * inv_cap);
-        x = ncol0 + fn * 16 + r < a.V ? x : -INFINITY;
+        if (kTail) x = ncol0 + fn * 16 + r < a.V ? x : -INFINITY;
         v[fn][r] = x;
         tmax = fmaxf(tmax, x);
       }
@@ -153,7 +153,9 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
   }
 }
 
-template <bool kCap, bool kStoreS>
+// kTail: V is not a multiple of 256, so the last vocabulary tile masks its
+// columns past V (without it the epilogue skips that select per logit).
+template <bool kCap, bool kStoreS, bool kTail>
 MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
   const TileSeq seq((uint32_t)(a.tiles_m * a.vt_total));
@@ -192,7 +194,7 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
           m2[fm] = kNegBig;
           d[fm] = 0.f;
         }
-        fwd_epilogue_bf16<kCap, kStoreS>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
+        fwd_epilogue_bf16<kCap, kStoreS, kTail>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
         fwd_final_merge(scratch, m2, d, rglob, tv, ec, a);
         // the merge's LDS is the ring slot refilled in the next phase 1
         __syncthreads();

@@ -58,8 +58,9 @@ def test_fused_uniform_grad(gpu, T, H, V):
     check_parity(X, W, y, loss, dX, dW, grad=torch.full((T,), 1.0 / n))
 
 
-def test_fused_per_token_grad_and_softcap(gpu):
-    X, W, y = make_case(400, 128, 3000, torch.bfloat16, seed=11, w_std=0.2)
+@pytest.mark.parametrize("V", [3000, 2560])  # vocabulary tail / whole 256-column tiles
+def test_fused_per_token_grad_and_softcap(gpu, V):
+    X, W, y = make_case(400, 128, V, torch.bfloat16, seed=11, w_std=0.2)
     grad = torch.rand(400, generator=torch.Generator().manual_seed(3)) * 2 - 0.5
     loss, dX, dW = run_fused(gpu, X, W, y, grad, softcap=3.0)
     check_parity(X, W, y, loss, dX, dW, grad=grad, softcap=3.0)

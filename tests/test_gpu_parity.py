@@ -92,8 +92,9 @@ def test_parity_fp32_tight(gpu):
     assert rel_fro(dW, torch.from_numpy(rdW)) <= 1e-5
 
 
-def test_per_token_grad_and_softcap(gpu):
-    X, W, y = make_case(400, 128, 3000, torch.bfloat16, seed=11, w_std=0.2)
+@pytest.mark.parametrize("V", [3000, 2560])  # vocabulary tail / whole 256-column tiles
+def test_per_token_grad_and_softcap(gpu, V):
+    X, W, y = make_case(400, 128, V, torch.bfloat16, seed=11, w_std=0.2)
     grad = torch.rand(400, generator=torch.Generator().manual_seed(3)) * 2 - 0.5
     loss, dX, dW = run_ours(gpu, X, W, y, grad=grad, softcap=3.0)
     check_parity(X, W, y, loss, dX, dW, grad=grad, softcap=3.0)
