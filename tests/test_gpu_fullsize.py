@@ -1,6 +1,7 @@
-"""Config 3 at its full size (T=65536, H=4096, V=128256, bf16, Zipf labels,
-30% masked, 128 packed samples): the HIP paths are checked where the oracle
-can follow them at this size and through size-independent properties.
+"""Configs 2-5 at their full sizes (bf16; seeded lengths, masks and labels of
+each configuration; X and W drawn on the GPU): the HIP paths are checked where
+the oracle can follow them at these sizes and through size-independent
+properties.
 
   * sampled rows: loss and dX of 24 valid and 8 ignored rows against the
     reference torch path on the CPU (loss 2e-3
@@ -12,6 +13,11 @@ can follow them at this size and through size-independent properties.
   * the fused path (gradient promised at the forward) and the general path
     agree: identical loss bits, dX / dW within rounding;
   * per-sample segment sums add up to the batch sum and count the valid rows.
+
+Config 2 exercises the general path with a vocabulary tail (V = 151936 =
+256 * 593 + 128), config 4 the fused path over 128k packed tokens, and config
+5 fp32 dW accumulation across its 4 minibatches (linearity: the accumulated
+dW equals the sum of the per-minibatch dW) with 5 fully masked samples.
 """
 from __future__ import annotations
 
@@ -26,78 +32,148 @@ from oracle.torch_path import rel_fro, torch_path
 pytestmark = pytest.mark.gpu
 
 
-def test_config3_full_size(gpu, monkeypatch):
-    cfg = synth.CONFIGS[3]
-    b = synth.make_batch(cfg, 0, with_tensors=False)
-    T, H, V = cfg.T, cfg.H, cfg.V
-    print(f"config 3 full size: T={T} H={H} V={V}", flush=True)
-    gen = torch.Generator(device=gpu).manual_seed(3)
-    X = torch.randn(T, H, device=gpu, generator=gen).to(torch.bfloat16)
-    W = (torch.randn(V, H, device=gpu, generator=gen) * cfg.w_std).to(torch.bfloat16)
-    y = b["target"].to(gpu)
-    cu = b["cu_seqlens"].to(gpu)
+def full_size_inputs(gpu, cfg):
+    """W and every minibatch's (X, target, cu_seqlens) of config cfg on the GPU."""
+    gen = torch.Generator(device=gpu).manual_seed(cfg.key)
+    mbs = []
+    for j in range(cfg.minibatches):
+        b = synth.make_batch(cfg, j, with_tensors=False)
+        X = torch.randn(cfg.T, cfg.H, device=gpu, generator=gen).to(torch.bfloat16)
+        if j == 0:
+            W = (torch.randn(cfg.V, cfg.H, device=gpu, generator=gen) * cfg.w_std).to(torch.bfloat16)
+        mbs.append((X, b["target"].to(gpu), b["cu_seqlens"].to(gpu)))
+    return W, mbs
+
+
+def run_path(monkeypatch, fused, X, W, y, scale, dW):
+    """One minibatch through the fused (fused=True) or the general path,
+    dW accumulated into the fp32 tensor dW; returns (loss, dX)."""
+    monkeypatch.setenv(FUSED_ENV, "1" if fused else "0")
+    Xd = X.detach().requires_grad_(True)
+    loss = fused_linear_cross_entropy(Xd, W, y, dw_accumulator=dW,
+                                      grad_scale=scale if fused else None)
+    (loss.sum() * scale).backward()
+    torch.cuda.synchronize()
+    return loss.detach(), Xd.grad
+
+
+def check_rows(X, W, y, loss, dX, scale, seed):
+    """Ignored rows exactly zero; sampled rows' loss and dX against the
+    reference torch path on the CPU."""
     valid = y != -100
-    n = int(valid.sum())
-    scale = 1.0 / n
-
-    def run(fused: bool):
-        monkeypatch.setenv(FUSED_ENV, "1" if fused else "0")
-        Xd = X.detach().requires_grad_(True)
-        dW = torch.zeros(V, H, dtype=torch.float32, device=gpu)
-        loss = fused_linear_cross_entropy(Xd, W, y, dw_accumulator=dW,
-                                          grad_scale=scale if fused else None)
-        (loss.sum() * scale).backward()
-        torch.cuda.synchronize()
-        return loss.detach(), Xd.grad, dW
-
-    loss_f, dX_f, dW_f = run(True)
-    loss_g, dX_g, dW_g = run(False)
-    print("paths done", flush=True)
-
-    # fused vs general: same forward arithmetic, gradients within rounding
-    assert torch.equal(loss_f, loss_g)
-    assert rel_fro(dX_f.float(), dX_g.float()) <= 1e-2
-    assert rel_fro(dW_f, dW_g) <= 1e-3
-
-    # ignored rows
-    assert torch.count_nonzero(loss_f[~valid]) == 0 and not torch.signbit(loss_f[~valid]).any()
-    assert torch.count_nonzero(dX_f[~valid]) == 0
-    assert bool((loss_f[valid] > 0).all())
-
-    # sampled rows against the reference torch path on the CPU
-    rng = np.random.default_rng(33)
+    assert torch.count_nonzero(loss[~valid]) == 0 and not torch.signbit(loss[~valid]).any()
+    assert torch.count_nonzero(dX[~valid]) == 0
+    assert bool((loss[valid] > 0).all())
+    rng = np.random.default_rng(seed)
     vidx = torch.nonzero(valid).flatten().cpu().numpy()
     iidx = torch.nonzero(~valid).flatten().cpu().numpy()
     rows = np.concatenate([rng.choice(vidx, 24, replace=False), rng.choice(iidx, 8, replace=False)])
-    rows_t = torch.from_numpy(rows).to(gpu)
-    Wc = W.cpu()
-    rl, rdX, _ = torch_path(X[rows_t].cpu(), Wc, y[rows_t].cpu(), grad=torch.tensor(scale),
+    rows_t = torch.from_numpy(rows).to(X.device)
+    rl, rdX, _ = torch_path(X[rows_t].cpu(), W.cpu(), y[rows_t].cpu(), grad=torch.tensor(scale),
                             upcast=True)
-    sl, sdX = loss_f[rows_t].cpu(), dX_f[rows_t].cpu()
+    sl, sdX = loss[rows_t].cpu(), dX[rows_t].cpu()
     v = y[rows_t].cpu() != -100
     err = ((sl[v] - rl[v]).abs() / rl[v].abs()).max().item()
     assert err <= 2e-3, f"sampled loss rel err {err:.3e}"
     assert torch.equal(sl[~v], torch.zeros(int((~v).sum())))
     assert rel_fro(sdX.float(), rdX.float()) <= 1e-2
 
-    # sampled dW rows on the CPU, from the returned loss: lse_t = loss_t + logit_{t, y_t}
-    vrows = torch.from_numpy(rng.choice(V, 6, replace=False))
+
+def dw_rows_ref(X, W, y, loss, scale, vrows):
+    """Rows vrows of G^T X on the CPU in float64, G = scale (softmax - onehot)
+    with lse_t = loss_t + logit_{t, y_t} taken from the returned loss."""
+    valid = y != -100
     Xv = X[valid].float().cpu()
     yv = y[valid].cpu()
-    Wf = Wc.float()
+    Wf = W.cpu().float()
     ly = (Xv * Wf[yv]).sum(1).to(torch.bfloat16).float()
-    lse_v = loss_f[valid].cpu() + ly
-    logits = (Xv @ Wf[vrows].t()).to(torch.bfloat16).float()  # [n, 6]
+    lse_v = loss[valid].cpu() + ly
+    logits = (Xv @ Wf[vrows].t()).to(torch.bfloat16).float()  # [n, len(vrows)]
     onehot = (yv[:, None] == vrows[None, :]).float()
     Gs = scale * (torch.exp(logits.double() - lse_v.double()[:, None]) - onehot.double())
-    ref_rows = Gs.t() @ Xv.double()
-    assert rel_fro(dW_f[vrows.to(gpu)].cpu().double(), ref_rows) <= 1e-2
+    return Gs.t() @ Xv.double()
 
+
+def check_vocab_sum(dW):
     # every softmax - onehot row sums to zero, hence so does dW over the vocabulary
-    col = dW_f.double().sum(0)
-    assert (col.norm() / dW_f.double().norm()).item() <= 1e-2
+    col = dW.double().sum(0)
+    assert (col.norm() / dW.double().norm()).item() <= 1e-2
+
+
+@pytest.mark.parametrize("key", [2, 3, 4])
+def test_full_size(gpu, monkeypatch, key):
+    cfg = synth.CONFIGS[key]
+    T, H, V = cfg.T, cfg.H, cfg.V
+    print(f"config {key} full size: T={T} H={H} V={V}", flush=True)
+    W, [(X, y, cu)] = full_size_inputs(gpu, cfg)
+    valid = y != -100
+    n = int(valid.sum())
+    scale = 1.0 / n
+
+    dW_f = torch.zeros(V, H, dtype=torch.float32, device=gpu)
+    loss_f, dX_f = run_path(monkeypatch, True, X, W, y, scale, dW_f)
+    dW_g = torch.zeros(V, H, dtype=torch.float32, device=gpu)
+    loss_g, dX_g = run_path(monkeypatch, False, X, W, y, scale, dW_g)
+    print("paths done", flush=True)
+
+    # fused vs general: same forward arithmetic, gradients within rounding
+    assert torch.equal(loss_f, loss_g)
+    assert rel_fro(dX_f.float(), dX_g.float()) <= 1e-2
+    assert rel_fro(dW_f, dW_g) <= 1e-3
+    del dX_g, dW_g
+
+    check_rows(X, W, y, loss_f, dX_f, scale, seed=30 + key)
+    rng = np.random.default_rng(40 + key)
+    # the last vocabulary row sits in the tail tile when V is not a multiple of 256
+    vrows = torch.from_numpy(np.append(rng.choice(V - 1, 5, replace=False), V - 1))
+    ref_rows = dw_rows_ref(X, W, y, loss_f, scale, vrows)
+    assert rel_fro(dW_f[vrows.to(gpu)].cpu().double(), ref_rows) <= 1e-2
+    check_vocab_sum(dW_f)
 
     # segment sums: a checksum of checksums
     seg_loss, seg_cnt = per_sample_loss_sums(loss_f, y, cu)
     np.testing.assert_allclose(seg_loss.double().sum().item(), loss_f.double().sum().item(), rtol=1e-5)
     assert int(seg_cnt.sum()) == n
+
+
+def test_config5_accumulation_full_size(gpu, monkeypatch):
+    cfg = synth.CONFIGS[5]
+    T, H, V = cfg.T, cfg.H, cfg.V
+    print(f"config 5 full size: {cfg.minibatches} x T={T} H={H} V={V}", flush=True)
+    W, mbs = full_size_inputs(gpu, cfg)
+    n_total = sum(int((y != -100).sum()) for _, y, _ in mbs)
+    scale = 1.0 / n_total  # one optimizer step's normalisation for every minibatch
+
+    acc_f = torch.zeros(V, H, dtype=torch.float32, device=gpu)
+    acc_g = torch.zeros(V, H, dtype=torch.float32, device=gpu)
+    sum_sep = torch.zeros(V, H, dtype=torch.float32, device=gpu)
+    rng = np.random.default_rng(50)
+    vrows = torch.from_numpy(np.append(rng.choice(V - 1, 3, replace=False), V - 1))
+    ref_rows = 0
+    for j, (X, y, cu) in enumerate(mbs):
+        loss_f, dX_f = run_path(monkeypatch, True, X, W, y, scale, acc_f)
+        loss_g, dX_g = run_path(monkeypatch, False, X, W, y, scale, acc_g)
+        sep = torch.zeros(V, H, dtype=torch.float32, device=gpu)
+        run_path(monkeypatch, False, X, W, y, scale, sep)
+        sum_sep += sep
+        del sep
+        print(f"minibatch {j} done", flush=True)
+        assert torch.equal(loss_f, loss_g)
+        assert rel_fro(dX_f.float(), dX_g.float()) <= 1e-2
+        check_rows(X, W, y, loss_f, dX_f, scale, seed=60 + j)
+        ref_rows = ref_rows + dw_rows_ref(X, W, y, loss_f, scale, vrows)
+
+        # fully masked samples: zero loss sum and zero count
+        seg_loss, seg_cnt = per_sample_loss_sums(loss_f, y, cu)
+        yc, bounds = y.cpu(), cu.cpu().tolist()
+        masked = torch.tensor([bool((yc[a:b] == -100).all()) for a, b in zip(bounds[:-1], bounds[1:])])
+        assert int(masked.sum()) >= 1 and bounds[-1] == T
+        m = masked.to(seg_loss.device)
+        assert torch.count_nonzero(seg_loss[m]) == 0 and torch.count_nonzero(seg_cnt[m]) == 0
+        assert int(seg_cnt.sum()) == int((y != -100).sum())
+
+    # accumulated in place across minibatches == sum of the separate minibatch dW
+    assert rel_fro(acc_g, sum_sep) <= 1e-5
+    assert rel_fro(acc_f, acc_g) <= 1e-3
+    assert rel_fro(acc_f[vrows.to(gpu)].cpu().double(), ref_rows) <= 1e-2
+    check_vocab_sum(acc_f)
