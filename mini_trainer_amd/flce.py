@@ -326,6 +326,11 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     cap = 0.0 if softcap is None else float(softcap)
     if cap < 0:
         raise ValueError("softcap must be positive (or None)")
+    if not (torch.is_grad_enabled()
+            and (hidden_states.requires_grad or lm_head_weight.requires_grad)):
+        # no backward will follow (no_grad / evaluation): the fused path would
+        # form dX and dW nobody asked for and add into dw_accumulator
+        grad_scale = None
     return _FusedLinearCrossEntropyNone.apply(hidden_states, lm_head_weight, target,
                                               int(ignore_index), cap, bool(shift_labels),
                                               dw_accumulator, grad_scale)

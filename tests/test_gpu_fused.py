@@ -118,6 +118,23 @@ def test_drop_in_reads_grad_scale_kwarg(gpu):
                  grad=torch.full((256,), 0.25))
 
 
+def test_grad_scale_ignored_without_autograd(gpu):
+    # Under no_grad (or with inputs that do not require grad) no backward
+    # follows, so the promise is not acted on: the loss is the same and the
+    # dW accumulator is left untouched.
+    X, W, y = make_case(300, 128, 1000, torch.bfloat16, seed=23)
+    Xd, Wd, yd = X.to(gpu), W.to(gpu), y.to(gpu)
+    acc = torch.full(W.shape, 0.5, dtype=torch.float32, device=gpu)
+    ref = fused_linear_cross_entropy(Xd, Wd, yd)
+    with torch.no_grad():
+        a = fused_linear_cross_entropy(Xd.requires_grad_(True), Wd, yd, dw_accumulator=acc,
+                                       grad_scale=0.01)
+    b = fused_linear_cross_entropy(Xd.detach(), Wd, yd, dw_accumulator=acc, grad_scale=0.01)
+    torch.cuda.synchronize()
+    assert torch.equal(a, ref) and torch.equal(b, ref)
+    assert bool((acc == 0.5).all())
+
+
 def test_fused_concurrent_host_threads(gpu):
     # Two host threads, each on its own stream, share the library's per-device
     # side stream and fork / join events; every call must still order its dW
