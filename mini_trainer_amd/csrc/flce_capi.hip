@@ -421,11 +421,14 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       r.ldg_b = ldg_b;
       r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
-      if constexpr (sizeof(T) == 2)
-        hipLaunchKernelGGL(softcap > 0.f ? recompute_bf16_kernel<true> : recompute_bf16_kernel<false>,
+      if constexpr (sizeof(T) == 2) {
+        static void (*const kerns[2][2])(RecompArgs) = {
+            {recompute_bf16_kernel<false, false>, recompute_bf16_kernel<false, true>},
+            {recompute_bf16_kernel<true, false>, recompute_bf16_kernel<true, true>}};
+        hipLaunchKernelGGL(kerns[softcap > 0.f][cv % 256 != 0],
                            dim3(persistent_grid(r.tiles_m * r.tiles_n)),
                            dim3(kThreadsBf), 0, stream, r);
-      else
+      } else
         hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
                            dim3(kThreads), 0, stream, r);
       MT_TRY(check_launch("recompute_kernel"));
@@ -740,6 +743,10 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
     if (chunk_rows <= 0 || chunk_rows % 256 != 0 || chunk_vocab <= 0 || chunk_vocab % 256 != 0)
       return fail(MT_ERR_INVALID_ARGUMENT,
                   "chunk_rows=%lld / chunk_vocab=%lld must be positive multiples of 256",
+                  (long long)chunk_rows, (long long)chunk_vocab);
+    if (es == 2 && ((uint64_t)chunk_rows * chunk_vocab * 2 > kMaxBufferBytes ||
+                    (uint64_t)H * chunk_rows * 2 > kMaxBufferBytes))
+      return fail(MT_ERR_UNSUPPORTED, "chunk_rows=%lld x chunk_vocab=%lld: G block or X^T beyond 4 GiB",
                   (long long)chunk_rows, (long long)chunk_vocab);
     const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es);
     if (workspace_bytes < need || !workspace)

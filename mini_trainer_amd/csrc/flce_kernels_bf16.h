@@ -94,6 +94,11 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
   const uint32_t scol = (uint32_t)vrow0 + ec.wn * 128u + 8u * (2u * (q & 1u) + (q >> 1));
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
+    // vocabulary columns of this lane below V, re-formed per fragment row
+    // through an empty asm so that the 32 compares are not hoisted out of
+    // the row loop (their masks spilled from the scalar registers)
+    int32_t lim = a.V - ncol0;
+    if (kTail) asm volatile("" : "+v"(lim));
     float v[8][4];
     uint32_t slo[8], shi[8];
     float tmax = -INFINITY;
@@ -111,7 +116,7 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
       for (int r = 0; r < 4; ++r) {
         float x = v[fn][r];
         if (kCap) x = cap * tanh_approx(x * inv_cap);
-        if (kTail) x = ncol0 + fn * 16 + r < a.V ? x : -INFINITY;
+        if (kTail) x = fn * 16 + r < lim ? x : -INFINITY;
         v[fn][r] = x;
         tmax = fmaxf(tmax, x);
       }
@@ -201,9 +206,90 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
       });
 }
 
+// Backward recompute epilogue of the bf16 kernel, one fragment row at a
+// time: G = g (softmax - onehot), times 1 - tanh^2 under softcap, with the
+// arithmetic of recompute_epilogue.  G is written as the fused forward
+// writes S: v_permlane16_swap pairs fragments fn = 2p, 2p + 1 so that each
+// lane stores 8 consecutive columns in one 16-byte store, through one buffer
+// resource at the block's G base (the planner keeps G below 4 GiB).  G holds
+// whole tiles; rows past Cn and (kTail: cv is not a multiple of 256) columns
+// past cv are written as zeros.
+template <bool kCap, bool kTail>
+__device__ __forceinline__ void recompute_epilogue_bf16(const f32x4_t (&acc)[8][8],
+                                                        const RecompArgs& a, const EpiCoordsBf& ec,
+                                                        int32_t row0, int32_t col0) {
+  const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
+  const int32_t ncol0 = col0 + ec.col(0);  // block-local column of fn = 0, r = 0
+  int32_t rel[8], rowl[8];
+  float lse2[8], g[8];
+  bool hit = false;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    rowl[fm] = row0 + ec.row(fm);
+    const bool rv = rowl[fm] < a.Cn;
+    const int32_t rr = rv ? rowl[fm] : 0;
+    lse2[fm] = a.lse[rr] * kLog2e;
+    g[fm] = rv ? a.grad[(int64_t)a.row_index[rr] * a.gstride] : 0.f;
+    rel[fm] = rv ? a.row_label[rr] - a.v0 - ncol0 : -1;
+    hit |= lane_holds<8>(rel[fm]);
+  }
+  const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
+  const rsrc_t grs = make_rsrc(a.G, kWholeRange);
+  const uint32_t q = ec.lane >> 4;
+  const uint32_t gcol = (uint32_t)col0 + ec.wn * 128u + 8u * (2u * (q & 1u) + (q >> 1));
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const bool rv = rowl[fm] < a.Cn;
+    // columns this lane may write, re-formed per fragment row through an
+    // empty asm: otherwise the 32 column compares are hoisted out of the row
+    // loop and their masks spill from the scalar registers
+    int32_t lim = a.cv - ncol0;
+    if (kTail) asm volatile("" : "+v"(lim));
+    uint32_t glo[8], ghi[8];
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+      float xr[4] = {acc[fm][fn][0], acc[fm][fn][1], acc[fm][fn][2], acc[fm][fn][3]};
+      round_pair<__bf16>(xr[0], xr[1]);
+      round_pair<__bf16>(xr[2], xr[3]);
+      float o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = xr[r];
+        float dcap = 1.f;
+        if (kCap) {
+          const float t = tanh_approx(x * inv_cap);
+          x = cap * t;
+          dcap = 1.f - t * t;
+        }
+        float p = fast_exp2(fmaf(x, kLog2e, -lse2[fm]));
+        if (any_hit) p -= (rel[fm] == fn * 16 + r) ? 1.f : 0.f;
+        const bool ok = kTail ? rv && (fn * 16 + r < lim) : rv;
+        o[r] = ok ? p * g[fm] * dcap : 0.f;
+      }
+      glo[fn] = pack_bf16x2(o[0], o[1]);
+      ghi[fn] = pack_bf16x2(o[2], o[3]);
+    }
+    const uint32_t goff = (uint32_t)rowl[fm] * (uint32_t)a.ldg_b + gcol * 2u;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const auto l2 = __builtin_amdgcn_permlane16_swap(glo[2 * p], glo[2 * p + 1], false, false);
+      const auto h2 = __builtin_amdgcn_permlane16_swap(ghi[2 * p], ghi[2 * p + 1], false, false);
+      u32x4_t o;
+      o[0] = l2[0];
+      o[1] = h2[0];
+      o[2] = l2[1];
+      o[3] = h2[1];
+      __builtin_amdgcn_raw_buffer_store_b128(o, grs, goff + (uint32_t)p * 64u, 0, 0);
+    }
+    sched_fence();
+  }
+}
+
 // Backward step 1: A = X rows of the block (256 tokens), B = W rows (256
-// vocabulary entries); the epilogue writes G.
-template <bool kCap>
+// vocabulary entries); the epilogue writes G.  kTail: the block's vocabulary
+// width cv is not a multiple of 256 (only the last block, and only when V is
+// not), so its last tile masks the columns past cv.
+template <bool kCap, bool kTail>
 MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
   const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
@@ -233,7 +319,7 @@ MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t row0 = (int32_t)tm * 256, col0 = (int32_t)tn * 256;
-        recompute_epilogue<__bf16, 8, kCap>(acc, a, ec, row0, col0);
+        recompute_epilogue_bf16<kCap, kTail>(acc, a, ec, row0, col0);
       });
 }
 

@@ -77,6 +77,9 @@ def test_backward_and_misc_host_checks():
     assert lib.mt_flce_backward(*args, 100, 256, 16, 1 << 30, None) == 1
     # workspace too small for the requested blocks
     assert lib.mt_flce_backward(*args, 256, 256, 16, 10, None) == 2
+    # a bf16 G block beyond the 4 GiB reach of 32-bit buffer offsets
+    assert lib.mt_flce_backward(*args, 65536, 65536, 16, 1 << 62, None) == 3
+    assert "4 GiB" in lib.mt_flce_last_error().decode()
     # negative grad stride
     bad = list(args)
     bad[14] = -1
