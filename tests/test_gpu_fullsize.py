@@ -1,4 +1,5 @@
-"""Configs 2-5 at their full sizes (bf16; seeded lengths, masks and labels of
+"""Configs 1-5 at their full sizes (config 1 fp32 against the whole reference
+torch path; configs 2-5 bf16 with seeded lengths, masks and labels of
 each configuration; X and W drawn on the GPU): the HIP paths are checked where
 the oracle can follow them at these sizes and through size-independent
 properties.
@@ -177,3 +178,32 @@ def test_config5_accumulation_full_size(gpu, monkeypatch):
     assert rel_fro(acc_f, acc_g) <= 1e-3
     assert rel_fro(acc_f[vrows.to(gpu)].cpu().double(), ref_rows) <= 1e-2
     check_vocab_sum(acc_f)
+
+
+def test_config1_full_size_against_torch_path(gpu):
+    # Config 1 (fp32; the reference's CPU-runnable case) is small enough for
+    # the whole reference torch path on the CPU: every row at the fp32
+    # tolerances (loss 1e-5 relative, dX / dW 1e-2 relative Frobenius).
+    cfg = synth.CONFIGS[1]
+    print(f"config 1 full size: T={cfg.T} H={cfg.H} V={cfg.V} fp32", flush=True)
+    b = synth.make_batch(cfg)
+    X, W, y, cu = b["X"], b["W"], b["target"], b["cu_seqlens"]
+    valid = y != -100
+    n = int(valid.sum())
+    scale = 1.0 / n
+    Xd = X.to(gpu).requires_grad_(True)
+    Wd = W.to(gpu).requires_grad_(True)
+    loss = fused_linear_cross_entropy(Xd, Wd, y.to(gpu))
+    (loss.sum() * scale).backward()
+    torch.cuda.synchronize()
+    print("gpu done", flush=True)
+    rl, rdX, rdW = torch_path(X, W, y, grad=torch.tensor(scale))
+    sl = loss.detach().cpu()
+    err = ((sl[valid] - rl[valid]).abs() / rl[valid].abs()).max().item()
+    assert err <= 1e-5, f"loss rel err {err:.3e}"
+    assert torch.equal(sl[~valid], torch.zeros(int((~valid).sum())))
+    assert rel_fro(Xd.grad.cpu(), rdX) <= 1e-2
+    assert rel_fro(Wd.grad.cpu(), rdW) <= 1e-2
+    seg_loss, seg_cnt = per_sample_loss_sums(loss.detach(), y.to(gpu), cu.to(gpu))
+    np.testing.assert_allclose(seg_loss.double().sum().item(), sl.double().sum().item(), rtol=1e-5)
+    assert int(seg_cnt.sum()) == n
