@@ -30,6 +30,32 @@ def test_header_symbols_exported():
     assert sorted(_lib.SIGNATURES) == names, "ctypes signatures must mirror the header"
 
 
+def test_integration_stub_matches_binding():
+    # the ctypes stub shown to maintainers declares the same argument and
+    # result types as the package's own binding (which mirrors the header)
+    text = (ROOT / "INTEGRATION.md").read_text()
+    stub = text.split("```python\nimport ctypes\n", 1)[1].split("assert lib.mt_flce_abi_version", 1)[0]
+    stub = stub.replace('lib = ctypes.CDLL("/path/to/libmt_flce.so")', "")
+
+    class Fn:
+        pass
+
+    class Lib:
+        def __getattr__(self, name):
+            f = Fn()
+            object.__setattr__(self, name, f)
+            return f
+
+    ns = {"lib": Lib()}
+    exec("import ctypes\n" + stub, ns)
+    declared = {n: f for n, f in vars(ns["lib"]).items() if hasattr(f, "argtypes")}
+    assert len(declared) >= 7
+    for name, f in declared.items():
+        restype, argtypes = _lib.SIGNATURES[name]
+        assert list(f.argtypes) == list(argtypes), name
+        assert getattr(f, "restype", None) == restype, name
+
+
 def test_abi_version_matches_header():
     m = re.search(r"#define MT_FLCE_ABI_VERSION (\d+)", HEADER.read_text())
     assert _lib.load().mt_flce_abi_version() == int(m.group(1)) == _lib.ABI_VERSION
