@@ -195,6 +195,7 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
             ctx.meta = (n, gstride, hidden.shape)
             ctx.dX = dX
             ctx.dW = None if dw_accumulator is not None else dW
+            ctx.fused_consumed = False
             return loss.view(hidden.shape[:-1])
         ws_bytes = lib.mt_flce_forward_workspace_bytes(T, n, H, V, dt)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -253,8 +254,14 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
                     "the upstream gradient of the loss differs from the grad_scale promised to "
                     "fused_linear_cross_entropy; the fused path has already formed dX and dW "
                     "for the promised one (call without grad_scale for an arbitrary gradient)")
+        if ctx.fused_consumed:
+            raise RuntimeError(
+                "the fused path formed dX and dW once, at the forward, and has already handed "
+                "them to autograd; a second backward through the same loss needs the general "
+                "path (call without grad_scale)")
         dX, dW = ctx.dX, ctx.dW
         ctx.dX = ctx.dW = None
+        ctx.fused_consumed = True
         grad_x = dX.view(hshape) if ctx.needs_input_grad[0] else None
         grad_w = dW if ctx.needs_input_grad[1] else None
         return (grad_x, grad_w) + (None,) * 6

@@ -118,6 +118,18 @@ def test_drop_in_reads_grad_scale_kwarg(gpu):
                  grad=torch.full((256,), 0.25))
 
 
+def test_fused_second_backward_raises(gpu):
+    # dX and dW exist once (formed at the forward): a second backward through
+    # the same graph must fail loudly rather than return no gradient
+    X, W, y = make_case(256, 64, 512, torch.bfloat16, seed=24)
+    Xd = X.to(gpu).requires_grad_(True)
+    loss = fused_linear_cross_entropy(Xd, W.to(gpu), y.to(gpu), grad_scale=0.5)
+    (loss.sum() * 0.5).backward(retain_graph=True)
+    assert Xd.grad is not None
+    with pytest.raises(RuntimeError, match="second backward"):
+        (loss.sum() * 0.5).backward()
+
+
 def test_grad_scale_ignored_without_autograd(gpu):
     # Under no_grad (or with inputs that do not require grad) no backward
     # follows, so the promise is not acted on: the loss is the same and the
