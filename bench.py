@@ -1,30 +1,33 @@
 """Benchmark of the fused LM-head linear + per-token cross-entropy on one MI355X.
 
-One step = the hot path of one training minibatch as train.py:97-104 drives
-it: forward, the caller's sum + .item() sync, and the backward with the
-uniform upstream gradient 1/N into an fp32 dW accumulator.  train.py knows
-that scale before the forward, so the step passes it as grad_scale and bf16
-runs the fused path (each logits tile computed once; dX and dW formed during
-the forward, the backward checks the gradient it receives); the general path
-(forward keeps lse only, backward recomputes the logits) is timed beside it.
-Inputs are seeded synthetic tensors of the named configuration, resident in
-HBM before timing starts.
+One step = the hot path of one optimizer step's minibatches exactly as
+train.py:97-104 drives it, through the drop-in
+liger_fixed_fused_linear_cross_entropy_none_reduction with the reference's
+own arguments: forward, `output.loss.float().sum()`, the `.item()` sync,
+`loss * world_size / batch_num_loss_counted_tokens`, `backward()`; the
+lm_head gradient accumulates into `W.grad` across the minibatches (config 5:
+four) and is cleared after the step, as the optimizer's zero_grad does.
+bf16 shapes where the fused path pays take it without any promise (dX and dW
+formed at the forward for a unit upstream gradient, rescaled in the
+backward).  Inputs are seeded synthetic tensors of the named configuration,
+resident in HBM before timing starts.
 
 Prints ONE JSON line (driver contract) with, in addition:
-  roofline      the logits GEMM (fwd_bf16_kernel: 2*H*V*N MFMA flops per
-                launch, one launch over all valid rows through
-                mt_flce_forward) timed with HIP events through the C ABI on
-                the stream it is launched on, against the bf16 dense peak;
+  roofline      the dominant unit of the timed step (the side-by-side dX and
+                dW GEMMs of each fused chunk: 2*C*V*H flops each, fork to
+                join), timed live with the library's per-launch HIP events on
+                the streams the kernels run on, against the bf16 dense peak;
+                `kernels` lists every kernel of the step the same way;
                 traffic = HBM bytes per launch from the committed rocprofv3
                 FETCH_SIZE / WRITE_SIZE summary (profiles/)
   cpu_baseline  the reference torch path (oracle/torch_path.py) on the host
                 cores over a bounded prefix of the same batch
-  north_star    6*H*V*N / t_step against the same peak, extra HBM, etc.
+  north_star    6*H*V*N / t_step against the same peak, extra HBM, the
+                promised-gradient and general paths, the other configurations
 """
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import sys
@@ -36,12 +39,17 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from mini_trainer_amd import _lib, synth  # noqa: E402
-from mini_trainer_amd.flce import (_dtype_code, _p, _stream, backward_plan,  # noqa: E402
-                                   fused_linear_cross_entropy, fused_plan, prepare_targets)
+from mini_trainer_amd.flce import (FUSED_ENV, _dtype_code, _p, _stream,  # noqa: E402
+                                   backward_plan, fused_linear_cross_entropy, path_of,
+                                   prepare_targets, profile_enable, profile_report)
+from mini_trainer_amd.none_reduction_losses import (  # noqa: E402
+    liger_fixed_fused_linear_cross_entropy_none_reduction as drop_in)
 
 PEAK_BF16 = 2.5166e15  # MI355X dense bf16 MFMA, 256 CU x 2.4 GHz x 4096 flop/clk
 PEAK_FP32 = 157.3e12
+PEAK_HBM = 8.0e12
 METRIC = "fused linear-CE fwd+bwd tokens/s on 1 GPU; MFMA util % of peak; extra HBM GB"
+WORLD_SIZE = 1  # train.py:102's world_size on one GPU
 
 
 def log(*a):
@@ -129,8 +137,8 @@ def torch_gpu_path(data, W, scale: float, steps: int = 2):
             "path": "F.linear -> .float() -> F.cross_entropy(reduction='none') -> backward (torch on the GPU)"}
 
 
-def measured_traffic(key: int, kernel: str):
-    """HBM bytes per launch of the dominant kernel, from the committed
+def measured_traffic(key: int, unit: str):
+    """HBM bytes per launch of the roofline unit, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload (calibrated
     against a 1 GiB device copy), or None when no summary covers it."""
     path = os.path.join(ROOT, "profiles", f"flce_cfg{key}_traffic.json")
@@ -139,7 +147,7 @@ def measured_traffic(key: int, kernel: str):
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    if t.get("kernel") != kernel:
+    if t.get("unit") != unit:
         return None
     return t.get("traffic_bytes")
 
@@ -157,97 +165,131 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": 4 * n}), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3)
-    ap.add_argument("--cpu-budget-s", type=float, default=25.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-torch-gpu", action="store_true",
-                    help="skip the reference torch path on the GPU (a comparator, not the metric)")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a plain 1 GiB device copy (the reference point that scales "
-                         "FETCH_SIZE / WRITE_SIZE counter readings to bytes) and exit")
-    args = ap.parse_args()
-    if args.copy_calibration:
-        copy_calibration()
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the dW reduce-scatter across ranks is design-only). Run with --gpus 1.",
-              file=sys.stderr)
-        sys.exit(2)
+class ForcedPath:
+    """Sets MT_FLCE_FUSED for the duration of a block ("0": general path)."""
 
-    cfg = synth.CONFIGS[args.config]
-    dev = torch.device("cuda", 0)
-    lib = _lib.load()
-    t0 = time.perf_counter()
-    mbs = [synth.make_batch(cfg, j) for j in range(cfg.minibatches)]
-    log(f"inputs for config {cfg.key} generated in {time.perf_counter() - t0:.1f}s")
-    W = mbs[0]["W"].to(dev)
-    data = [(m["X"].to(dev), m["target"].to(dev)) for m in mbs]
-    del mbs
-    V, H = W.shape
-    T = data[0][0].shape[0]
-    dW = torch.zeros(V, H, dtype=torch.float32, device=dev)
-    Wl = W.requires_grad_(True)
-    n_valid = [int((y != -100).sum().item()) for _, y in data]
-    N_total = sum(n_valid)
-    T_total = T * len(data)
+    def __init__(self, value):
+        self.value, self.old = value, None
 
-    scale = 1.0 / N_total  # train.py:102 with world_size 1: known before the forward
+    def __enter__(self):
+        self.old = os.environ.get(FUSED_ENV)
+        if self.value is not None:
+            os.environ[FUSED_ENV] = self.value
 
-    def make_step(fused: bool):
-        def step():
-            # one optimizer step's worth of minibatches (config 5: 4 grad-accum minibatches)
-            for X, y in data:
-                Xl = X.detach().requires_grad_(True)
-                loss = fused_linear_cross_entropy(Xl, Wl, y, dw_accumulator=dW,
-                                                  grad_scale=scale if fused else None)
-                s = loss.float().sum()
-                s.item()  # the caller's sync (train.py:99)
-                torch.autograd.grad(s * scale, (Xl,))
-        return step
+    def __exit__(self, *exc):
+        if self.old is None:
+            os.environ.pop(FUSED_ENV, None)
+        else:
+            os.environ[FUSED_ENV] = self.old
 
-    def timed(step):
-        for _ in range(args.warmup):
-            step()
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        ev0.record()
-        for _ in range(args.steps):
-            step()
-        ev1.record()
-        torch.cuda.synchronize()
-        return ev0.elapsed_time(ev1) / args.steps
 
-    fused = cfg.dtype == torch.bfloat16
-    step = make_step(fused)
-    for _ in range(args.warmup):
+def reference_step(data, Wl, n_counted: int, paths=None):
+    """train.py:97-104 for each minibatch through the drop-in, W.grad
+    accumulating across them, cleared at the end (the optimizer's zero_grad)."""
+    for X, y in data:
+        Xl = X.detach().requires_grad_(True)
+        out_loss = drop_in(Xl, Wl, y)
+        if paths is not None:
+            paths.append(path_of(out_loss))
+        loss = out_loss.float().sum()
+        loss.item()  # train.py:99
+        loss = loss * WORLD_SIZE / n_counted  # train.py:102
+        loss.backward()  # train.py:104
+    Wl.grad = None
+
+
+def promise_step(data, Wl, n_counted: int, dW):
+    """The same chain with the scale promised at the forward (grad_scale) and
+    the lm_head gradient accumulated in fp32 into dW (no rescaling pass)."""
+    scale = WORLD_SIZE / n_counted
+    for X, y in data:
+        Xl = X.detach().requires_grad_(True)
+        loss = fused_linear_cross_entropy(Xl, Wl, y, dw_accumulator=dW, grad_scale=scale)
+        s = loss.float().sum()
+        s.item()
+        (s * WORLD_SIZE / n_counted).backward()
+
+
+def timed(step, steps: int, warmup: int) -> float:
+    """ms per step over `steps` steps after `warmup` untimed ones, between
+    device synchronisations."""
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps
 
-    # extra HBM of one step: allocator peak - live inputs/outputs
+
+def extra_hbm(data, Wl, n_counted: int, dtype) -> dict:
+    """Allocator peak of one minibatch of the reference step minus the live
+    inputs and the required outputs: loss [T] fp32, dX [T, H] (X.grad), the
+    fp32 dW the library forms and W.grad in the weight's dtype (the
+    parameter gradient the reference holds too)."""
+    X, y = data[0]
+    T, H = X.shape
+    V = Wl.shape[0]
+    es = torch.finfo(dtype).bits // 8
+    dev = X.device
+    Wl.grad = None
+    torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats(dev)
     base = torch.cuda.memory_allocated(dev)
-    step()
+    reference_step([(X, y)], Wl, n_counted)
     torch.cuda.synchronize()
     peak = torch.cuda.max_memory_allocated(dev)
-    es = torch.finfo(cfg.dtype).bits // 8
-    outputs = T * 4 + T * H * es  # loss + dX of the live minibatch (dW fp32 is preallocated)
-    extra = peak - base - outputs
-    budget = 0.05 * T * V * es
+    outputs = T * 4 + T * H * es + V * H * 4 + V * H * es
+    return {"extra_hbm_GB": (peak - base - outputs) / 1e9,
+            "extra_hbm_budget_GB": 0.05 * T * V * es / 1e9,
+            "peak_memory_GB": peak / 1e9}
 
-    ms = timed(step)
-    t_step = ms / 1e3
-    # the general path (gradient not known at the forward: recompute in the backward)
-    ms_general = timed(make_step(False)) if fused else ms
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    # dominant kernel: fwd_kernel via mt_flce_forward on the current stream
-    X, y = data[0]
+def roofline_of(report: dict, peak_flops: float, steps: int) -> tuple:
+    """(roofline entry of the dominant unit, per-kernel table) from a
+    mt_flce_profile_report over `steps` steps."""
+    kernels = {}
+    for name, r in report.items():
+        n, ms = r["launches"], r["ms_total"]
+        if r["flops"] > 0:
+            ach = r["flops"] / (ms / 1e3)
+            kernels[name] = {"launches_per_step": n / steps, "ms_per_launch": ms / n,
+                             "ms_per_step": ms / steps, "achieved_TFLOPs": ach / 1e12,
+                             "frac": ach / peak_flops, "bound": "mfma"}
+        else:
+            ach = r["bytes"] / (ms / 1e3)
+            kernels[name] = {"launches_per_step": n / steps, "ms_per_launch": ms / n,
+                             "ms_per_step": ms / steps, "achieved_GBs": ach / 1e9,
+                             "frac": ach / PEAK_HBM, "bound": "hbm"}
+    if "dx_dw_phase" in report:
+        unit = "dx_dw_phase"
+    else:
+        gemms = {k: v for k, v in report.items() if v["flops"] > 0}
+        unit = max(gemms, key=lambda k: gemms[k]["ms_total"]) if gemms else None
+    if unit is None:
+        return None, kernels
+    r = report[unit]
+    per_launch_s = r["ms_total"] / r["launches"] / 1e3
+    flops_per_launch = r["flops"] / r["launches"]
+    ach = flops_per_launch / per_launch_s
+    return {"bound": "mfma", "kernel": unit, "achieved": ach / 1e12, "peak": peak_flops / 1e12,
+            "unit": "TFLOP/s", "frac": ach / peak_flops, "traffic": None,
+            "ms_per_launch": per_launch_s * 1e3, "flops_per_launch": flops_per_launch,
+            "launches_per_step": r["launches"] / steps,
+            "share_of_step": r["ms_total"] / steps}, kernels
+
+
+def general_forward_roofline(X, W, y, peak_flops: float, reps: int) -> dict:
+    """The general path's logits GEMM alone (fwd_bf16_kernel through
+    mt_flce_forward, one launch over all valid rows), HIP events on the
+    current stream, which is the stream it is launched on."""
+    lib = _lib.load()
+    dev = X.device
+    T, H = X.shape
+    V = W.shape[0]
     ri, rl, n = prepare_targets(y, V)
     dt = _dtype_code(X.dtype)
     loss = torch.empty(T, dtype=torch.float32, device=dev)
@@ -263,22 +305,154 @@ def main():
 
     fwd_call()
     torch.cuda.synchronize()
-    reps = max(3, args.steps)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
     for _ in range(reps):
         fwd_call()
     ev1.record()
     torch.cuda.synchronize()
-    fwd_s = ev0.elapsed_time(ev1) / reps / 1e3
-    fwd_flops = 2.0 * H * V * n
+    s = ev0.elapsed_time(ev1) / reps / 1e3
+    flops = 2.0 * H * V * n
+    return {"kernel": "fwd_bf16_kernel (mt_flce_forward)", "ms_per_launch": s * 1e3,
+            "achieved": flops / s / 1e12, "frac": flops / s / peak_flops,
+            "flops_per_launch": flops}
+
+
+def device_inputs(cfg, dev):
+    """Seeded inputs generated on the device (fast for the extra
+    configurations): labels, masks and packing from synth (CPU numpy), X and
+    W from a device generator in fp32, cast to the config dtype."""
+    data = []
+    g = torch.Generator(device=dev).manual_seed(1000 + cfg.key)
+    W = (torch.randn(cfg.V, cfg.H, device=dev, generator=g) * cfg.w_std).to(cfg.dtype)
+    for j in range(cfg.minibatches):
+        b = synth.make_batch(cfg, j, with_tensors=False)
+        gx = torch.Generator(device=dev).manual_seed(cfg.key if cfg.minibatches == 1 else 50 + j)
+        X = torch.empty(cfg.T, cfg.H, dtype=cfg.dtype, device=dev)
+        for r0 in range(0, cfg.T, 8192):  # fp32 draws in slabs keep the peak low
+            r1 = min(cfg.T, r0 + 8192)
+            X[r0:r1] = torch.randn(r1 - r0, cfg.H, device=dev, generator=gx).to(cfg.dtype)
+        data.append((X, b["target"].to(dev)))
+    return W, data
+
+
+def other_config(key: int, dev, steps: int, warmup: int) -> dict:
+    cfg = synth.CONFIGS[key]
+    W, data = device_inputs(cfg, dev)
+    Wl = W.requires_grad_(True)
+    n_counted = sum(int((y != -100).sum().item()) for _, y in data)
+    paths = []
+    reference_step(data[:1], Wl, n_counted, paths)
+    ms = timed(lambda: reference_step(data, Wl, n_counted), steps, warmup)
+    mem = extra_hbm(data, Wl, n_counted, cfg.dtype)
+    peak = PEAK_BF16 if cfg.dtype == torch.bfloat16 else PEAK_FP32
+    T_total = cfg.T * len(data)
+    out = {"workload": cfg.name, "T": cfg.T, "H": cfg.H, "V": cfg.V, "minibatches": len(data),
+           "n_valid": n_counted, "path": paths[0], "steps": steps, "ms_per_step": ms,
+           "tokens_per_s": T_total / (ms / 1e3),
+           "frac_of_peak_6HVN": 6.0 * cfg.H * cfg.V * n_counted / (ms / 1e3) / peak, **mem}
+    del W, Wl, data
+    torch.cuda.empty_cache()
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-torch-gpu", action="store_true",
+                    help="skip the reference torch path on the GPU (a comparator, not the metric)")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="time the reference step only (no promised-gradient / general path)")
+    ap.add_argument("--other-configs", default="2,4,5",
+                    help="comma-separated configurations also timed (reference step, 3 steps "
+                         "on device-generated inputs) when --config is 3; '' for none")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (the reference point that scales "
+                         "FETCH_SIZE / WRITE_SIZE counter readings to bytes) and exit")
+    args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the dW reduce-scatter across ranks is design-only). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    cfg = synth.CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    _lib.load()
+    t0 = time.perf_counter()
+    mbs = [synth.make_batch(cfg, j) for j in range(cfg.minibatches)]
+    log(f"inputs for config {cfg.key} generated in {time.perf_counter() - t0:.1f}s")
+    W = mbs[0]["W"].to(dev)
+    data = [(m["X"].to(dev), m["target"].to(dev)) for m in mbs]
+    del mbs
+    V, H = W.shape
+    T = data[0][0].shape[0]
+    Wl = W.requires_grad_(True)
+    n_valid = [int((y != -100).sum().item()) for _, y in data]
+    N_total = sum(n_valid)
+    T_total = T * len(data)
     peak_flops = PEAK_BF16 if cfg.dtype == torch.bfloat16 else PEAK_FP32
-    C, Cv, bws = backward_plan(T, n, H, V, cfg.dtype)
-
-    fwd_kernel_name = "fwd_bf16_kernel" if cfg.dtype == torch.bfloat16 else "fwd_kernel"
-    fused_taken = fused and fused_plan(T, n_valid[0], H, V)[2]
-    traffic = measured_traffic(cfg.key, fwd_kernel_name)
-
     alg_flops = 6.0 * H * V * N_total
+
+    paths = []
+    reference_step(data, Wl, N_total, paths)
+    torch.cuda.synchronize()
+    mem = extra_hbm(data, Wl, N_total, cfg.dtype)
+    log(f"reference step: path {paths[0]}, extra HBM {mem['extra_hbm_GB']:.3f} GB")
+
+    ms = timed(lambda: reference_step(data, Wl, N_total), args.steps, args.warmup)
+    t_step = ms / 1e3
+    log(f"reference step: {ms:.2f} ms")
+
+    # the same steps again with the library's per-launch events: the roofline
+    # unit and the per-kernel table of the timed step
+    profile_enable(True)
+    ms_prof = timed(lambda: reference_step(data, Wl, N_total), args.steps, 0)
+    profile_enable(False)
+    report = profile_report()
+    roof, kernels = roofline_of(report, peak_flops, args.steps)
+    if roof is not None:
+        roof["traffic"] = measured_traffic(cfg.key, roof["kernel"])
+    log(f"profiled step: {ms_prof:.2f} ms; roofline unit {roof and roof['kernel']}")
+
+    north = {
+        "alg_flops_6HVN": alg_flops,
+        "achieved_TFLOPs": alg_flops / t_step / 1e12,
+        "frac_of_peak": alg_flops / t_step / peak_flops,
+        "dense_convention_frac": 6.0 * H * V * T_total / t_step / peak_flops,
+        "path": paths[0],
+        "call": ("liger_fixed_fused_linear_cross_entropy_none_reduction(hidden, W, target) -> "
+                 ".float().sum() -> .item() -> * world_size / batch_num_loss_counted_tokens -> "
+                 "backward(), W.grad accumulated across minibatches (train.py:97-104)"),
+        "profiled_ms_per_step": ms_prof,
+        **mem,
+    }
+    if not args.no_variants and cfg.dtype == torch.bfloat16:
+        dW = torch.zeros(V, H, dtype=torch.float32, device=dev)
+        ms_p = timed(lambda: promise_step(data, Wl, N_total, dW), args.steps, 1)
+        Wl.grad = None
+        del dW
+        with ForcedPath("0"):
+            ms_g = timed(lambda: reference_step(data, Wl, N_total), args.steps, 1)
+        north["promised_grad_ms_per_step"] = ms_p
+        north["promised_grad_frac_of_peak"] = alg_flops / (ms_p / 1e3) / peak_flops
+        north["general_path_ms_per_step"] = ms_g
+        north["general_path_frac_of_peak"] = alg_flops / (ms_g / 1e3) / peak_flops
+        log(f"promised-gradient step {ms_p:.2f} ms, general path {ms_g:.2f} ms")
+        torch.cuda.empty_cache()
+    C, Cv, _ = backward_plan(T, n_valid[0], H, V, cfg.dtype)
+    gen_fwd = general_forward_roofline(data[0][0], W.detach(), data[0][1], peak_flops,
+                                       max(3, min(args.steps, 5)))
+    torch.cuda.empty_cache()
+
     out = {
         "metric": METRIC,
         "value": T_total / t_step,
@@ -295,39 +469,24 @@ def main():
         "config": {
             "workload": f"config {cfg.key}: {cfg.name} fused LM-head linear + CE fwd+bwd",
             "T": T, "H": H, "V": V, "minibatches": len(data), "n_valid": N_total,
-            "bwd_chunk_rows": C, "bwd_chunk_vocab": Cv,
+            "general_bwd_chunk_rows": C, "general_bwd_chunk_vocab": Cv,
         },
-        "roofline": {
-            "bound": "mfma",
-            "kernel": f"{fwd_kernel_name} (mt_flce_forward)",
-            "achieved": fwd_flops / fwd_s / 1e12,
-            "peak": peak_flops / 1e12,
-            "unit": "TFLOP/s",
-            "frac": fwd_flops / fwd_s / peak_flops,
-            "traffic": traffic,
-            "ms_per_launch": fwd_s * 1e3,
-            "flops_per_launch": fwd_flops,
-        },
-        "north_star": {
-            "alg_flops_6HVN": alg_flops,
-            "achieved_TFLOPs": alg_flops / t_step / 1e12,
-            "frac_of_peak": alg_flops / t_step / peak_flops,
-            "dense_convention_frac": 6.0 * H * V * T_total / t_step / peak_flops,
-            "path": ("fused: grad_scale = 1/N passed at the forward (mt_flce_fused, 6HVN)"
-                     if fused_taken else
-                     "general (mt_flce_forward + mt_flce_backward, 8HVN)"
-                     + ("; the planner declined the fused path for this budget" if fused else "")),
-            "general_path_ms_per_step": ms_general,
-            "general_path_frac_of_peak": alg_flops / (ms_general / 1e3) / peak_flops,
-            "extra_hbm_GB": extra / 1e9,
-            "extra_hbm_budget_GB": budget / 1e9,
-            "peak_memory_GB": peak / 1e9,
-        },
+        "roofline": roof,
+        "kernels": kernels,
+        "roofline_general_forward": gen_fwd,
+        "north_star": north,
     }
+    if args.config == 3 and args.other_configs.strip():
+        others = {}
+        for k in [int(x) for x in args.other_configs.split(",") if x.strip()]:
+            t1 = time.perf_counter()
+            others[f"config {k}"] = other_config(k, dev, steps=3, warmup=1)
+            log(f"config {k}: {others[f'config {k}']['ms_per_step']:.2f} ms "
+                f"({others[f'config {k}']['path']}) in {time.perf_counter() - t1:.1f}s")
+        out["other_configs"] = others
     if not args.no_torch_gpu:
-        del ws
         torch.cuda.empty_cache()
-        tg = torch_gpu_path(data, W, scale)
+        tg = torch_gpu_path(data, W.detach(), WORLD_SIZE / N_total)
         if "ms_per_step" in tg:
             tg["speedup_of_value"] = out["value"] / tg["tokens_per_s"]
         out["torch_gpu_path"] = tg

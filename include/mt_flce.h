@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define MT_FLCE_ABI_VERSION 2
+#define MT_FLCE_ABI_VERSION 3
 
 typedef struct ihipStream_t* mt_stream_t; /* == hipStream_t */
 
@@ -191,15 +191,57 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
  * packed layout of sampler.py:182-188 and the cu_seqlens derivation of
  * TF/modeling_flash_attention_utils.py:458-481).
  *   cu_seqlens int32 [S+1], non-decreasing, cu[0] = 0, cu[S] = T
+ *   shift      0: position t's target is target[t]; != 0: it is target[t + 1]
+ *              (ignore_index at t = T - 1), the causal shift of
+ *              TF/loss/loss_utils.py:61-64 applied to unshifted labels
  *   seg_loss   fp32 [S] out: sum of loss over [cu[s], cu[s+1])
- *   seg_count  int32 [S] out: number of t in that range with target != ignore_index
+ *   seg_count  int32 [S] out: number of t in that range whose target != ignore_index
  *   status     int32 [1] out (device): 0, or 1 if cu_seqlens is malformed
  *              (then seg_loss / seg_count are zero)
  */
 int mt_segment_sum(const float* loss, const int64_t* target, int64_t T,
-                   int64_t ignore_index, const int32_t* cu_seqlens, int64_t S,
-                   float* seg_loss, int32_t* seg_count, int32_t* status,
-                   mt_stream_t stream);
+                   int64_t ignore_index, int shift, const int32_t* cu_seqlens,
+                   int64_t S, float* seg_loss, int32_t* seg_count,
+                   int32_t* status, mt_stream_t stream);
+
+/*
+ * Rescale gradients formed for a unit upstream gradient once the real
+ * (uniform) one is known: dX *= scale in place, dW_out = scale * dW.
+ * Replaces the backward of the reference's fused loss,
+ * LIGER:ops/fused_linear_cross_entropy.py::fused_linear_cross_entropy_backward
+ * (element_mul_kernel: grad_input and grad_weight times grad_output[0]),
+ * reached from none_reduction_losses.py:16-23 -- the gradients were formed
+ * in the forward (mt_flce_fused with grad_loss = 1, grad_stride = 0).
+ *   scale      fp32 [1] (device): read by the kernels, no host sync
+ *   dX         [T, H] of dtype_x, leading dimension lddx, scaled in place
+ *   dW         fp32 [V, H], leading dimension lddw
+ *   dW_out     [V, H] of dtype_out, leading dimension ldo: either dW itself
+ *              (fp32, same pitch: in place) or a separate buffer (bf16 output
+ *              rounds to nearest even; it may not partially overlap dW)
+ * T = 0 or V = 0 skips that tensor.
+ */
+int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H,
+                        int64_t lddx, int dtype_x, const float* dW, int64_t V,
+                        int64_t lddw, void* dW_out, int64_t ldo, int dtype_out,
+                        mt_stream_t stream);
+
+/*
+ * Measurement hook (no counterpart in the reference; for benchmarks and
+ * profilers).  While enabled, every kernel launch of mt_flce_forward,
+ * mt_flce_backward, mt_flce_fused and mt_flce_scale_grads made on the device
+ * that was current at enable time is bracketed by two timing events on the
+ * stream it runs on, tagged with the kernel's name and algorithmic work
+ * (flops of the unpadded GEMM, or bytes of an HBM pass); the dX and dW
+ * GEMMs that run side by side are also recorded as one "dx_dw_phase" from
+ * the fork to the join.  mt_flce_profile_report synchronises on the recorded
+ * events, writes a JSON object {name: {launches, ms_total, ms_min, ms_max,
+ * flops, bytes}} into buf (needed = its size including the terminating
+ * zero; MT_ERR_INVALID_ARGUMENT if len is smaller, keeping the records for
+ * a retry with a larger buffer) and releases the records.
+ * Call the report only when no call of this library is in flight.
+ */
+int mt_flce_profile_enable(int enable);
+int mt_flce_profile_report(char* buf, size_t len, size_t* needed);
 
 /*
  * Cross-entropy over materialised logits, reduction 'none' -- the HF slot of

@@ -7,11 +7,14 @@ include/mt_flce.h); this package is the PyTorch-facing host side.
 from .causal_lm import (
     causal_lm_loss,
     cu_seqlens_from_lengths,
+    cu_seqlens_from_minibatch,
     cu_seqlens_from_position_ids,
     patch_causal_lm,
+    sample_loss_sums,
 )
 from .flce import (
     backward_plan,
+    path_of,
     cross_entropy_none,
     fused_linear_cross_entropy,
     per_sample_loss_sums,
@@ -26,9 +29,12 @@ from .utils import patch_target_module
 __all__ = [
     "causal_lm_loss",
     "cu_seqlens_from_lengths",
+    "cu_seqlens_from_minibatch",
     "cu_seqlens_from_position_ids",
+    "sample_loss_sums",
     "patch_causal_lm",
     "backward_plan",
+    "path_of",
     "cross_entropy_none",
     "fused_linear_cross_entropy",
     "per_sample_loss_sums",

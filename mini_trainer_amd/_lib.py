@@ -10,7 +10,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p, c_char_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmt_flce.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MT_DTYPE_F32 = 0
 MT_DTYPE_BF16 = 1
@@ -45,8 +45,12 @@ SIGNATURES = {
                               c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
                               c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int,
                               c_int64, c_void_p, c_size_t, c_void_p]),
-    "mt_segment_sum": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p,
-                               c_void_p, c_void_p, c_void_p]),
+    "mt_segment_sum": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_int64,
+                               c_void_p, c_void_p, c_void_p, c_void_p]),
+    "mt_flce_scale_grads": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p,
+                                    c_int64, c_int64, c_void_p, c_int64, c_int, c_void_p]),
+    "mt_flce_profile_enable": (c_int, [c_int]),
+    "mt_flce_profile_report": (c_int, [c_char_p, c_size_t, POINTER(c_size_t)]),
     "mt_ce_forward": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p, c_int64,
                               c_void_p, c_void_p, c_void_p]),
     "mt_ce_backward": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p, c_int64,

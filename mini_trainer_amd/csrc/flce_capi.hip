@@ -7,8 +7,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/mt_flce.h"
 #include "flce_kernels.h"
@@ -102,6 +104,65 @@ int side_stream(SideStream** out) {
   return MT_OK;
 }
 
+// Measurement hook (mt_flce_profile_enable / mt_flce_profile_report): while
+// enabled, every GEMM-shaped launch and HBM pass of the forward, backward and
+// fused paths is bracketed by a pair of timing events recorded on the stream
+// it is launched on, tagged with the kernel's name and its algorithmic work
+// (flops, or bytes for HBM passes).  The report synchronises on the events,
+// aggregates per name and releases them for reuse.  Only launches on the
+// device that was current at enable time are recorded.  Off by default: a
+// disabled scope costs one relaxed atomic load.
+struct ProfRec {
+  hipEvent_t b, e;
+  const char* name;
+  double flops, bytes;
+};
+struct Profiler {
+  std::mutex mu;
+  std::atomic<bool> on{false};
+  int device = -1;
+  std::vector<ProfRec> recs;
+  std::vector<hipEvent_t> pool;
+};
+Profiler& profiler() {
+  static Profiler p;
+  return p;
+}
+
+hipEvent_t prof_event(Profiler& p) {
+  if (!p.pool.empty()) {
+    hipEvent_t e = p.pool.back();
+    p.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+}
+
+// Opens a record on `stream`; returns its index (or -1 when disabled).
+int prof_begin(const char* name, double flops, double bytes, hipStream_t stream) {
+  Profiler& p = profiler();
+  if (!p.on.load(std::memory_order_relaxed)) return -1;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != p.device) return -1;
+  std::lock_guard<std::mutex> lock(p.mu);
+  ProfRec r{prof_event(p), prof_event(p), name, flops, bytes};
+  if (!r.b || !r.e || hipEventRecord(r.b, stream) != hipSuccess) {
+    if (r.b) p.pool.push_back(r.b);
+    if (r.e) p.pool.push_back(r.e);
+    return -1;
+  }
+  p.recs.push_back(r);
+  return (int)p.recs.size() - 1;
+}
+
+void prof_end(int idx, hipStream_t stream) {
+  if (idx < 0) return;
+  Profiler& p = profiler();
+  std::lock_guard<std::mutex> lock(p.mu);
+  if (idx < (int)p.recs.size()) (void)hipEventRecord(p.recs[idx].e, stream);
+}
+
 // Test hook: MT_FLCE_GRID_CAP=n (> 0) caps the persistent bf16 GEMM grids
 // (logits, recompute) and the dW grids at n workgroups, so that small
 // problems run the multi-tile paths (tile-to-tile pipelining, the dW
@@ -160,6 +221,16 @@ inline Geometry geometry(int es) {
   return es == 2 ? Geometry{256, 256, kCUs, kThreadsBf} : Geometry{256, 256, kCUs, kThreads};
 }
 
+// Algorithmic flops of one dX / dW launch (2 x rows x K x columns of the
+// unpadded block) and the name a measurement record carries.
+inline double dx_flops(const DxArgs& x) { return 2.0 * x.Cn * (double)x.kv * x.H; }
+inline double dw_flops(const DwArgs& w) { return 2.0 * w.cv * (double)w.H * w.kt_rows; }
+inline const char* dx_name(int mode) {
+  static const char* const n[4] = {"dx_bf16_kernel<store>", "dx_bf16_kernel<add>",
+                                   "dx_bf16_kernel<add_emit>", "dx_bf16_kernel<emit>"};
+  return n[mode & 3];
+}
+
 // One dX kernel instantiation per accumulation mode (uniform per launch); one
 // workgroup per output tile (the kernel multiplies exactly one tile, so the
 // grid is never capped).
@@ -180,16 +251,22 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream) {
   SideStream* side = nullptr;
   MT_TRY(side_stream(&side));
   std::lock_guard<std::mutex> lock(side->use);
+  const double fx = dx_flops(x), fw = dw_flops(w);
+  const int ph = prof_begin("dx_dw_phase", fx + fw, 0, stream);
   MT_TRY(hipEventRecord(side->fork, stream) == hipSuccess ? MT_OK
                                                            : fail(MT_ERR_HIP, "hipEventRecord"));
   MT_TRY(hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess
              ? MT_OK
              : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
+  const int px = prof_begin(dx_name(x.mode), fx, 0, stream);
   launch_dx_bf16(x, stream);
+  prof_end(px, stream);
   MT_TRY(check_launch("dx_bf16_kernel"));
   const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
+  const int pw = prof_begin("dw_bf16_kernel", fw, 0, side->stream);
   hipLaunchKernelGGL(dw_bf16_kernel, dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
                      dim3(kThreadsBf), 0, side->stream, w);
+  prof_end(pw, side->stream);
   MT_TRY(check_launch("dw_bf16_kernel"));
   MT_TRY(hipEventRecord(side->join, side->stream) == hipSuccess
              ? MT_OK
@@ -197,6 +274,7 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream) {
   MT_TRY(hipStreamWaitEvent(stream, side->join, 0) == hipSuccess
              ? MT_OK
              : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
+  prof_end(ph, stream);
   return MT_OK;
 }
 
@@ -364,8 +442,10 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
         {fwd_bf16_kernel<false, false, false>, fwd_bf16_kernel<false, false, true>},
         {fwd_bf16_kernel<true, false, false>, fwd_bf16_kernel<true, false, true>}};
     void (*kern)(FwdArgs) = kerns[softcap > 0.f][V % 256 != 0];
+    const int pf = prof_begin("fwd_bf16_kernel", 2.0 * H * (double)V * n_valid, 0, stream);
     hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * p.vt_total)), dim3(kThreadsBf), 0,
                        stream, a);
+    prof_end(pf, stream);
   } else {
     hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
                        stream, a);
@@ -425,9 +505,11 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
         static void (*const kerns[2][2])(RecompArgs) = {
             {recompute_bf16_kernel<false, false>, recompute_bf16_kernel<false, true>},
             {recompute_bf16_kernel<true, false>, recompute_bf16_kernel<true, true>}};
+        const int pr = prof_begin("recompute_bf16_kernel", 2.0 * H * (double)cn * cv, 0, stream);
         hipLaunchKernelGGL(kerns[softcap > 0.f][cv % 256 != 0],
                            dim3(persistent_grid(r.tiles_m * r.tiles_n)),
                            dim3(kThreadsBf), 0, stream, r);
+        prof_end(pr, stream);
       } else
         hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
                            dim3(kThreads), 0, stream, r);
@@ -461,9 +543,11 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       const int64_t cus = grid_cap() > 0 ? std::min(grid_cap(), device_cus()) : device_cus();
       const bool beside = sizeof(T) == 2 && (int64_t)x.tiles_m * x.tiles_n < cus;
       if (!beside) {
-        if constexpr (sizeof(T) == 2)
+        if constexpr (sizeof(T) == 2) {
+          const int px = prof_begin(dx_name(x.mode), dx_flops(x), 0, stream);
           launch_dx_bf16(x, stream);
-        else
+          prof_end(px, stream);
+        } else
           hipLaunchKernelGGL(dx_kernel<T>, dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreads), 0,
                              stream, x);
         MT_TRY(check_launch("dx_kernel"));
@@ -489,10 +573,12 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
         // the next block's recompute (G) and gather (X^T) follow the join
         MT_TRY(launch_dx_dw_bf16(x, w, stream));
       } else {
-        if constexpr (sizeof(T) == 2)
+        if constexpr (sizeof(T) == 2) {
+          const int pw = prof_begin("dw_bf16_kernel", dw_flops(w), 0, stream);
           hipLaunchKernelGGL(dw_bf16_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)),
                              dim3(kThreadsBf), 0, stream, w);
-        else
+          prof_end(pw, stream);
+        } else
           hipLaunchKernelGGL(dw_kernel<T>, dim3((uint32_t)(w.tiles_m * w.tiles_n)), dim3(kThreads), 0,
                              stream, w);
         MT_TRY(check_launch("dw_kernel"));
@@ -592,15 +678,19 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
         {fwd_bf16_kernel<false, true, false>, fwd_bf16_kernel<false, true, true>},
         {fwd_bf16_kernel<true, true, false>, fwd_bf16_kernel<true, true, true>}};
     void (*kern)(FwdArgs) = kerns[softcap > 0.f][V % 256 != 0];
+    const int pf = prof_begin("fwd_bf16_kernel<store_s>", 2.0 * H * (double)V * cn, 0, stream);
     hipLaunchKernelGGL(kern, dim3(persistent_grid(tm * vt)), dim3(kThreadsBf), 0, stream, a);
+    prof_end(pf, stream);
     MT_TRY(check_launch("fwd_bf16_kernel"));
     hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(cn, 4)), dim3(256), 0, stream,
                        part, xy, (int32_t)cn, (int32_t)vt, row_index + c0, loss, lse + c0);
     MT_TRY(check_launch("fwd_finalize_kernel"));
+    const int ps = prof_begin("softmax_grad_kernel", 0, 2.0 * 2.0 * (double)cn_pad * Vp, stream);
     hipLaunchKernelGGL(softcap > 0.f ? softmax_grad_kernel<true> : softmax_grad_kernel<false>,
                        dim3((uint32_t)cn_pad), dim3(256), 0, stream, S, lds_b,
                        (int32_t)Vp, (int32_t)cn, (int32_t)V, lse + c0, grad, gstride,
                        row_index + c0, row_label + c0, softcap);
+    prof_end(ps, stream);
     MT_TRY(check_launch("softmax_grad_kernel"));
 
     DxArgs x;
@@ -853,8 +943,8 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
 }
 
 int mt_segment_sum(const float* loss, const int64_t* target, int64_t T, int64_t ignore_index,
-                   const int32_t* cu_seqlens, int64_t S, float* seg_loss, int32_t* seg_count,
-                   int32_t* status, mt_stream_t stream) {
+                   int shift, const int32_t* cu_seqlens, int64_t S, float* seg_loss,
+                   int32_t* seg_count, int32_t* status, mt_stream_t stream) {
   if (T < 0 || T > INT32_MAX || S < 0 || S > INT32_MAX)
     return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld S=%lld", (long long)T, (long long)S);
   if (!cu_seqlens || !status || (S > 0 && (!seg_loss || !seg_count)) || (T > 0 && (!loss || !target)))
@@ -863,9 +953,124 @@ int mt_segment_sum(const float* loss, const int64_t* target, int64_t T, int64_t 
   hipLaunchKernelGGL(segment_check_kernel, dim3(1), dim3(256), 0, s, cu_seqlens, S, T, status);
   MT_TRY(check_launch("segment_check_kernel"));
   if (S == 0) return MT_OK;
-  hipLaunchKernelGGL(segment_sum_kernel, dim3((uint32_t)S), dim3(256), 0, s, loss, target,
-                     ignore_index, cu_seqlens, status, seg_loss, seg_count);
+  hipLaunchKernelGGL(segment_sum_kernel, dim3((uint32_t)S), dim3(256), 0, s, loss, target, T,
+                     ignore_index, shift, cu_seqlens, status, seg_loss, seg_count);
   return check_launch("segment_sum_kernel");
+}
+
+int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H, int64_t lddx,
+                        int dtype_x, const float* dW, int64_t V, int64_t lddw, void* dW_out,
+                        int64_t ldo, int dtype_out, mt_stream_t stream) {
+  const int esx = esize_of(dtype_x), eso = esize_of(dtype_out);
+  if (!esx || !eso) return fail(MT_ERR_INVALID_ARGUMENT, "dtype_x / dtype_out must be MT_DTYPE_F32 or MT_DTYPE_BF16");
+  if (T < 0 || V < 0 || H <= 0 || H > INT32_MAX)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld H=%lld V=%lld", (long long)T, (long long)H,
+                (long long)V);
+  if (!scale) return fail(MT_ERR_INVALID_ARGUMENT, "null scale");
+  if ((T > 0 && (!dX || lddx < H)) || (V > 0 && (!dW || !dW_out || lddw < H || ldo < H)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer or leading dimension below H");
+  if ((reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(dW) |
+       reinterpret_cast<uintptr_t>(dW_out)) % 16 != 0 ||
+      (lddx * esx) % 16 != 0 || (lddw * 4) % 16 != 0 || (ldo * eso) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dX / dW / dW_out must be 16-byte aligned with 16-byte row pitches");
+  if (dW_out == dW && (dtype_out != MT_DTYPE_F32 || ldo != lddw))
+    return fail(MT_ERR_INVALID_ARGUMENT, "in-place dW scaling needs fp32 output with the same pitch");
+  if (dW_out != dW && V > 0) {
+    const char *a0 = static_cast<const char*>(static_cast<const void*>(dW)), *a1 = a0 + (size_t)V * lddw * 4;
+    const char *b0 = static_cast<const char*>(dW_out), *b1 = b0 + (size_t)V * ldo * eso;
+    if (a0 < b1 && b0 < a1) return fail(MT_ERR_INVALID_ARGUMENT, "dW_out partially overlaps dW");
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (T > 0) {
+    const int p = prof_begin("scale_rows_kernel<dX>", 0, 2.0 * T * H * esx, s);
+    if (esx == 2)
+      hipLaunchKernelGGL(scale_rows_bf16_kernel, dim3((uint32_t)std::min<int64_t>(T, 16384)), dim3(256), 0,
+                         s, static_cast<char*>(dX), lddx * 2, T, H, scale);
+    else
+      hipLaunchKernelGGL(scale_rows_f32_kernel<false>, dim3((uint32_t)std::min<int64_t>(T, 16384)),
+                         dim3(256), 0, s, static_cast<const float*>(dX), lddx, dX, lddx, T, H, scale);
+    prof_end(p, s);
+    MT_TRY(check_launch("scale_rows_kernel"));
+  }
+  if (V > 0) {
+    const int p = prof_begin("scale_rows_kernel<dW>", 0, (double)V * H * (4 + eso), s);
+    if (eso == 2)
+      hipLaunchKernelGGL(scale_rows_f32_kernel<true>, dim3((uint32_t)std::min<int64_t>(V, 16384)), dim3(256),
+                         0, s, dW, lddw, dW_out, ldo, V, H, scale);
+    else
+      hipLaunchKernelGGL(scale_rows_f32_kernel<false>, dim3((uint32_t)std::min<int64_t>(V, 16384)), dim3(256),
+                         0, s, dW, lddw, dW_out, ldo, V, H, scale);
+    prof_end(p, s);
+    MT_TRY(check_launch("scale_rows_kernel"));
+  }
+  return MT_OK;
+}
+
+int mt_flce_profile_enable(int enable) {
+  Profiler& p = profiler();
+  std::lock_guard<std::mutex> lock(p.mu);
+  if (enable) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(MT_ERR_HIP, "hipGetDevice failed");
+    p.device = dev;
+  }
+  p.on.store(enable != 0, std::memory_order_relaxed);
+  return MT_OK;
+}
+
+int mt_flce_profile_report(char* buf, size_t len, size_t* needed) {
+  Profiler& p = profiler();
+  std::lock_guard<std::mutex> lock(p.mu);
+  struct Agg {
+    const char* name;
+    long n;
+    double ms, ms_min, ms_max, flops, bytes;
+  };
+  std::vector<Agg> agg;
+  int rc = MT_OK;
+  for (const ProfRec& r : p.recs) {
+    float ms = 0.f;
+    if (hipEventSynchronize(r.e) != hipSuccess || hipEventElapsedTime(&ms, r.b, r.e) != hipSuccess) {
+      rc = fail(MT_ERR_HIP, "timing event query failed: %s", hipGetErrorString(hipGetLastError()));
+      continue;
+    }
+    Agg* a = nullptr;
+    for (Agg& x : agg)
+      if (std::string(x.name) == r.name) a = &x;
+    if (!a) {
+      agg.push_back(Agg{r.name, 0, 0.0, 1e300, 0.0, 0.0, 0.0});
+      a = &agg.back();
+    }
+    a->n += 1;
+    a->ms += ms;
+    a->ms_min = std::min(a->ms_min, (double)ms);
+    a->ms_max = std::max(a->ms_max, (double)ms);
+    a->flops += r.flops;
+    a->bytes += r.bytes;
+  }
+  if (rc != MT_OK) return rc;
+  std::string out = "{";
+  char item[512];
+  for (size_t i = 0; i < agg.size(); ++i) {
+    const Agg& a = agg[i];
+    snprintf(item, sizeof item,
+             "%s\"%s\": {\"launches\": %ld, \"ms_total\": %.6f, \"ms_min\": %.6f, "
+             "\"ms_max\": %.6f, \"flops\": %.6e, \"bytes\": %.6e}",
+             i ? ", " : "", a.name, a.n, a.ms, a.ms_min, a.ms_max, a.flops, a.bytes);
+    out += item;
+  }
+  out += "}";
+  if (needed) *needed = out.size() + 1;
+  // a buffer too small keeps the records for the retry
+  if (!buf || len < out.size() + 1)
+    return fail(MT_ERR_INVALID_ARGUMENT, "report needs %zu bytes", out.size() + 1);
+  memcpy(buf, out.c_str(), out.size() + 1);
+  for (const ProfRec& r : p.recs) {
+    p.pool.push_back(r.b);
+    p.pool.push_back(r.e);
+  }
+  p.recs.clear();
+  return MT_OK;
 }
 
 int mt_ce_forward(const void* logits, int64_t T, int64_t V, int64_t ld, int dtype,

@@ -665,9 +665,11 @@ __global__ __launch_bounds__(256) void segment_check_kernel(const int32_t* cu, i
 }
 
 // One workgroup per sample: fixed-order tree sum of loss and count of valid
-// targets over [cu[s], cu[s+1]).
+// targets over [cu[s], cu[s+1]).  With shift, the target of position t is
+// labels[t + 1] (ignore_index at t = T - 1), as the causal shift forms it.
 __global__ __launch_bounds__(256) void segment_sum_kernel(const float* loss, const int64_t* target,
-                                                          int64_t ignore, const int32_t* cu,
+                                                          int64_t T, int64_t ignore, int shift,
+                                                          const int32_t* cu,
                                                           const int32_t* status, float* seg_loss,
                                                           int32_t* seg_count) {
   __shared__ float sl[256];
@@ -678,7 +680,8 @@ __global__ __launch_bounds__(256) void segment_sum_kernel(const float* loss, con
   if (*status == 0) {
     for (int64_t t = cu[s] + threadIdx.x; t < cu[s + 1]; t += 256) {
       acc += loss[t];
-      cnt += target[t] != ignore ? 1 : 0;
+      const int64_t src = t + (shift ? 1 : 0);
+      cnt += (src < T && target[src] != ignore) ? 1 : 0;
     }
   }
   sl[threadIdx.x] = acc;
@@ -694,6 +697,74 @@ __global__ __launch_bounds__(256) void segment_sum_kernel(const float* loss, con
   if (threadIdx.x == 0) {
     seg_loss[s] = sl[0];
     seg_count[s] = sc[0];
+  }
+}
+
+// ===========================================================================
+// Gradients formed for a unit upstream gradient, rescaled once the real one
+// is known: the reference's fused loss computes dX and dW in its forward and
+// multiplies them by the scalar grad_output in its backward.  The scale is
+// read from device memory (no host sync).  Rows are a grid-stride loop, 16
+// bytes per thread and access; a column tail that is not a whole vector
+// goes element by element.
+// ===========================================================================
+
+// dst[r, c] = scale * src[r, c] for an fp32 matrix; dst fp32 (may be src:
+// every element is read and written by the same thread) or bf16 (round to
+// nearest even).
+template <bool kOutBf16>
+__global__ __launch_bounds__(256) void scale_rows_f32_kernel(const float* src, int64_t ld_src,
+                                                             void* dst, int64_t ld_dst,
+                                                             int64_t rows, int64_t cols,
+                                                             const float* scale) {
+  const float c = *scale;
+  const int64_t nv = cols / 4;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const float* s = src + r * ld_src;
+    for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
+      const f32x4_t x = reinterpret_cast<const f32x4_t*>(s)[v];
+      const float y0 = x[0] * c, y1 = x[1] * c, y2 = x[2] * c, y3 = x[3] * c;
+      if (kOutBf16) {
+        u32x2_t o;
+        o[0] = pack_bf16x2(y0, y1);
+        o[1] = pack_bf16x2(y2, y3);
+        reinterpret_cast<u32x2_t*>(static_cast<char*>(dst) + r * ld_dst * 2)[v] = o;
+      } else {
+        reinterpret_cast<f32x4_t*>(static_cast<float*>(dst) + r * ld_dst)[v] =
+            f32x4_t{y0, y1, y2, y3};
+      }
+    }
+    for (int64_t k = nv * 4 + threadIdx.x; k < cols; k += blockDim.x) {
+      const float y = s[k] * c;
+      if (kOutBf16)
+        reinterpret_cast<__bf16*>(static_cast<char*>(dst) + r * ld_dst * 2)[k] = (__bf16)y;
+      else
+        (static_cast<float*>(dst) + r * ld_dst)[k] = y;
+    }
+  }
+}
+
+// In place: p[r, c] = bf16(scale * p[r, c]) for a bf16 matrix of row pitch
+// ld_b bytes.
+__global__ __launch_bounds__(256) void scale_rows_bf16_kernel(char* p, int64_t ld_b, int64_t rows,
+                                                              int64_t cols, const float* scale) {
+  const float c = *scale;
+  const int64_t nv = cols / 8;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    u32x4_t* row = reinterpret_cast<u32x4_t*>(p + r * ld_b);
+    for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
+      u32x4_t w = row[v];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = __builtin_bit_cast(float, w[j] << 16) * c;
+        const float hi = __builtin_bit_cast(float, w[j] & 0xffff0000u) * c;
+        w[j] = pack_bf16x2(lo, hi);
+      }
+      row[v] = w;
+    }
+    __bf16* e = reinterpret_cast<__bf16*>(p + r * ld_b);
+    for (int64_t k = nv * 8 + threadIdx.x; k < cols; k += blockDim.x)
+      e[k] = (__bf16)((float)e[k] * c);
   }
 }
 

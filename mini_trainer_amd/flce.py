@@ -19,6 +19,9 @@ from ._lib import MT_DTYPE_BF16, MT_DTYPE_F32, check, load
 
 __all__ = [
     "fused_linear_cross_entropy",
+    "path_of",
+    "profile_enable",
+    "profile_report",
     "cross_entropy_none",
     "prepare_targets",
     "per_sample_loss_sums",
@@ -152,33 +155,48 @@ def _check_inputs(hidden, weight, target):
 
 
 class _FusedLinearCrossEntropyNone(torch.autograd.Function):
-    """Per-token loss; two paths over the same arithmetic.
+    """Per-token loss; three paths over the same arithmetic (ctx.path).
 
-    general  forward keeps lse (mt_flce_forward); the backward recomputes the
-             logits for whatever upstream gradient arrives (mt_flce_backward).
-    fused    grad_scale promised the upstream gradient at the forward and the
-             planner expects the fused path to pay (bf16, mt_flce_fused_plan):
-             the forward also forms dX and dW (mt_flce_fused); the backward
-             checks the gradient it receives against the promise and hands the
-             stored gradients to autograd.
+    general     forward keeps lse (mt_flce_forward); the backward recomputes
+                the logits for whatever upstream gradient arrives
+                (mt_flce_backward).
+    fused       grad_scale promised the upstream gradient at the forward and
+                the planner expects the fused path to pay (bf16,
+                mt_flce_fused_plan): the forward also forms dX and dW for it
+                (mt_flce_fused); the backward checks the gradient it receives
+                against the promise and hands the stored gradients to autograd.
+    fused_unit  no promise, no dw_accumulator, bf16, the planner expects the
+                fused path to pay: the forward forms dX and dW for a unit
+                upstream gradient -- the structure of the reference's fused
+                loss (none_reduction_losses.py:16-23 -> Liger's
+                fused_linear_cross_entropy_forward), which train.py:97-104
+                drives unchanged.  The backward multiplies them by the upstream
+                gradient when it is one scalar for every token (stride 0, what
+                sum() / mean() and train.py's scaling give; mt_flce_scale_grads
+                reads it on the device), and otherwise recomputes with the
+                saved lse (mt_flce_backward), exact for any per-token gradient.
     """
 
     @staticmethod
     def forward(ctx, hidden, weight, target, ignore_index, softcap, shift, dw_accumulator,
-                grad_scale):
+                grad_scale, allow_unit):
         X, W, T, H, V, dt = _check_inputs(hidden, weight, target)
         lib = load()
         dev = X.device
         row_index, row_label, n = prepare_targets(target, V, ignore_index, shift)
         loss = torch.empty(T, dtype=torch.float32, device=dev)
         lse = torch.empty(n, dtype=torch.float32, device=dev)
-        ctx.fused = False
-        if grad_scale is not None and dt == MT_DTYPE_BF16 and n > 0:
+        ctx.path = "general"
+        if dt == MT_DTYPE_BF16 and n > 0 and (grad_scale is not None or allow_unit):
             C, ws_bytes, pays = fused_plan(T, n, H, V)
-            ctx.fused = _use_fused(pays)
+            if _use_fused(pays):
+                ctx.path = "fused" if grad_scale is not None else "fused_unit"
         ctx.dw_accumulator = dw_accumulator
-        if ctx.fused:
-            g, gstride = _promised_grad(grad_scale, T, dev)
+        if ctx.path != "general":
+            if ctx.path == "fused":
+                g, gstride = _promised_grad(grad_scale, T, dev)
+            else:
+                g, gstride = torch.ones(1, dtype=torch.float32, device=dev), 0
             dX = torch.empty((T, H), dtype=X.dtype, device=dev)
             if dw_accumulator is not None:
                 dW, accumulate = dw_accumulator, 1
@@ -191,8 +209,11 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
                                     dW.stride(0), accumulate, C, _p(ws), ws_bytes, _stream(dev)),
                   "mt_flce_fused")
             del ws
-            ctx.save_for_backward(row_index, g)
-            ctx.meta = (n, gstride, hidden.shape)
+            if ctx.path == "fused":
+                ctx.save_for_backward(row_index, g)
+            else:  # kept for the recompute fallback of a per-token gradient
+                ctx.save_for_backward(X, W, row_index, row_label, lse)
+            ctx.meta = (n, gstride, hidden.shape, float(softcap), dt)
             ctx.dX = dX
             ctx.dW = None if dw_accumulator is not None else dW
             ctx.fused_consumed = False
@@ -209,13 +230,15 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_loss):
-        if ctx.fused:
+        if ctx.path == "fused":
             return _FusedLinearCrossEntropyNone._backward_fused(ctx, grad_loss)
+        if ctx.path == "fused_unit":
+            return _FusedLinearCrossEntropyNone._backward_fused_unit(ctx, grad_loss)
         X, W, row_index, row_label, lse = ctx.saved_tensors
         n, softcap, hshape, dt = ctx.meta
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         acc = ctx.dw_accumulator
-        none = (None,) * 6
+        none = (None,) * 7
         if not need_x and not need_w and acc is None:
             return (None, None) + none
         lib = load()
@@ -241,19 +264,24 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
     @staticmethod
     def _backward_fused(ctx, grad_loss):
         row_index, g = ctx.saved_tensors
-        n, gstride, hshape = ctx.meta
+        n, gstride, hshape, _, _ = ctx.meta
         T = row_index.numel()
         if n > 0:
             gl = grad_loss.reshape(-1)
             if gl.numel() == 1:
                 gl = gl.expand(T)
-            valid = row_index[:n].long()
-            want = g.expand(n) if gstride == 0 else g[valid]
-            if not bool(torch.equal(gl[valid].float(), want)):
+            if gl.stride(0) == 0 and gstride == 0:  # one scalar against one scalar
+                got, want = gl[:1].float(), g
+            else:
+                valid = row_index[:n].long()
+                got, want = gl[valid].float(), (g.expand(n) if gstride == 0 else g[valid])
+            if not _within_promise(got, want):
                 raise RuntimeError(
                     "the upstream gradient of the loss differs from the grad_scale promised to "
-                    "fused_linear_cross_entropy; the fused path has already formed dX and dW "
-                    "for the promised one (call without grad_scale for an arbitrary gradient)")
+                    "fused_linear_cross_entropy by more than "
+                    f"{PROMISE_ULPS} fp32 ulp; the fused path has already formed dX and dW "
+                    "for the promised one (and added dW into dw_accumulator, if one was given): "
+                    "call without grad_scale for an arbitrary gradient")
         if ctx.fused_consumed:
             raise RuntimeError(
                 "the fused path formed dX and dW once, at the forward, and has already handed "
@@ -264,7 +292,97 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         ctx.fused_consumed = True
         grad_x = dX.view(hshape) if ctx.needs_input_grad[0] else None
         grad_w = dW if ctx.needs_input_grad[1] else None
-        return (grad_x, grad_w) + (None,) * 6
+        return (grad_x, grad_w) + (None,) * 7
+
+
+    @staticmethod
+    def _backward_fused_unit(ctx, grad_loss):
+        X, W, row_index, row_label, lse = ctx.saved_tensors
+        n, _, hshape, softcap, dt = ctx.meta
+        if ctx.fused_consumed:
+            raise RuntimeError(
+                "the fused path formed dX and dW once, at the forward, and has already handed "
+                "them to autograd; a second backward through the same loss needs the general "
+                "path (call under MT_FLCE_FUSED=0)")
+        ctx.fused_consumed = True
+        dX, dW = ctx.dX, ctx.dW
+        ctx.dX = ctx.dW = None
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        T, H = X.shape
+        V = W.shape[0]
+        dev = X.device
+        lib = load()
+        g, gstride = _grad_vector(grad_loss, T)
+        if gstride == 0:
+            # one upstream scalar for every token: rescale the unit-gradient
+            # dX and dW (dW straight into the weight's dtype)
+            scale = g.reshape(-1)[:1]
+            if W.dtype == torch.float32:
+                dW_out, out_dt = dW, MT_DTYPE_F32
+            else:
+                dW_out, out_dt = torch.empty((V, H), dtype=W.dtype, device=dev), _dtype_code(W.dtype)
+            check(lib.mt_flce_scale_grads(_p(scale), _p(dX) if need_x else None,
+                                          T if need_x else 0, H, dX.stride(0), dt, _p(dW),
+                                          V if need_w else 0, dW.stride(0),
+                                          _p(dW_out), dW_out.stride(0), out_dt, _stream(dev)),
+                  "mt_flce_scale_grads")
+            del dW
+        else:
+            # a per-token gradient: the unit-gradient results cannot be
+            # rescaled; recompute into the same buffers
+            C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
+                                       softcap, _p(row_index), _p(row_label), n, _p(lse), _p(g),
+                                       gstride, _p(dX), dX.stride(0), _p(dW), dW.stride(0), 0, C,
+                                       Cv, _p(ws), ws_bytes, _stream(dev)), "mt_flce_backward")
+            dW_out = dW
+        grad_x = dX.view(hshape) if need_x else None
+        grad_w = dW_out if need_w else None
+        return (grad_x, grad_w) + (None,) * 7
+
+
+# A promised gradient is accepted when every token's received gradient is
+# within this many fp32 ulp of the promise: train.py:102's literal
+# `loss * world_size / batch_num_loss_counted_tokens` back-propagates
+# fl32(fl32(1 / n) * world_size), one or two ulp from fl32(world_size / n).
+PROMISE_ULPS = 4
+
+
+def _within_promise(got: torch.Tensor, want: torch.Tensor) -> bool:
+    tol = want.abs() * (PROMISE_ULPS * 2.0 ** -23)
+    return bool(((got - want).abs() <= tol).all())
+
+
+def path_of(loss: torch.Tensor) -> Optional[str]:
+    """The path ("general", "fused" or "fused_unit") that produced a loss
+    returned by fused_linear_cross_entropy (looked up through its autograd
+    node and the view / reshape nodes in front of it), or None."""
+    fn = loss.grad_fn
+    while fn is not None:
+        if hasattr(fn, "path"):
+            return fn.path
+        nxt = [f for f, _ in fn.next_functions if f is not None]
+        fn = nxt[0] if len(nxt) == 1 else None
+    return None
+
+
+def profile_enable(enable: bool = True) -> None:
+    """Turn the library's per-launch timing events on or off (mt_flce_profile_enable)."""
+    check(load().mt_flce_profile_enable(int(bool(enable))), "mt_flce_profile_enable")
+
+
+def profile_report() -> dict:
+    """Per-kernel timing of the launches recorded since the last report
+    (synchronises; mt_flce_profile_report)."""
+    import json
+
+    lib = load()
+    need = ctypes.c_size_t(0)
+    lib.mt_flce_profile_report(None, 0, ctypes.byref(need))
+    buf = ctypes.create_string_buffer(max(int(need.value), 2) + 256)
+    check(lib.mt_flce_profile_report(buf, len(buf), ctypes.byref(need)), "mt_flce_profile_report")
+    return json.loads(buf.value.decode())
 
 
 def fused_plan(T: int, n_valid: int, H: int, V: int,
@@ -313,16 +431,27 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     hidden_states and lm_head_weight; the gradient of the weight is formed in
     fp32.  With dw_accumulator (fp32 [V, H]) the weight gradient is added into
     that tensor instead of being returned to autograd.  shift_labels applies
-    the causal shift (target[t] = labels[t + 1]) on the device.
+    the causal shift (target[t] = labels[t + 1]) on the device; with target of
+    shape [B, T'] and B > 1 every row is shifted on its own (its last
+    position gets ignore_index), as transformers' ForCausalLMLoss does.
+
+    bf16 inputs whose shapes make the fused path pay (mt_flce_fused_plan: each
+    logits tile computed once, dX and dW formed during the forward) take it
+    without any promise when no dw_accumulator is given: the forward forms
+    the gradients for a unit upstream gradient and the backward rescales
+    them when the gradient it receives is one scalar for every token (what
+    train.py:97-104's sum and scaling produce), or recomputes for a per-token
+    one -- see _FusedLinearCrossEntropyNone.
 
     grad_scale (a float, or a [T] tensor of per-token values) promises the
     upstream gradient of the returned loss -- train.py:97-104 knows it before
     the forward: world_size / batch_num_loss_counted_tokens for every token.
-    bf16 inputs then take the fused path (each logits tile computed once, dX
-    and dW formed during the forward) when the planner expects it to beat the
-    general one under the workspace budget (mt_flce_fused_plan); the backward
-    of the fused path checks that the gradient it receives is the promised one
-    and raises otherwise.
+    The fused path then forms dX and dW for it directly (no rescaling pass)
+    and may add dW into dw_accumulator during the forward; the backward
+    checks that the gradient it receives is within PROMISE_ULPS fp32 ulp of
+    the promise and raises otherwise.  dw_accumulator has then already been
+    updated (at the forward), also when that check raises or when no
+    backward follows.
     """
     if dw_accumulator is not None:
         V, H = lm_head_weight.shape
@@ -333,14 +462,21 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     cap = 0.0 if softcap is None else float(softcap)
     if cap < 0:
         raise ValueError("softcap must be positive (or None)")
-    if not (torch.is_grad_enabled()
-            and (hidden_states.requires_grad or lm_head_weight.requires_grad)):
+    recording = torch.is_grad_enabled() and (hidden_states.requires_grad
+                                             or lm_head_weight.requires_grad)
+    if not recording:
         # no backward will follow (no_grad / evaluation): the fused path would
         # form dX and dW nobody asked for and add into dw_accumulator
         grad_scale = None
+    # the unit-gradient fused path needs the weight's gradient to be wanted
+    # (else dW is waste) and no accumulator (which would need the scale now)
+    allow_unit = recording and lm_head_weight.requires_grad and dw_accumulator is None
+    if shift_labels and target.dim() >= 2 and target.shape[0] > 1:
+        target = torch.nn.functional.pad(target, (0, 1), value=int(ignore_index))[..., 1:]
+        shift_labels = False
     return _FusedLinearCrossEntropyNone.apply(hidden_states, lm_head_weight, target,
                                               int(ignore_index), cap, bool(shift_labels),
-                                              dw_accumulator, grad_scale)
+                                              dw_accumulator, grad_scale, allow_unit)
 
 
 class _CrossEntropyNone(torch.autograd.Function):
@@ -391,12 +527,15 @@ def cross_entropy_none(source: torch.Tensor, target: torch.Tensor,
 
 
 def per_sample_loss_sums(loss: torch.Tensor, target: torch.Tensor, cu_seqlens: torch.Tensor,
-                         ignore_index: int = -100,
-                         validate: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+                         ignore_index: int = -100, validate: bool = True,
+                         shift: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-sample (sum of loss, number of counted tokens) over a packed batch.
 
     cu_seqlens (int32 [S+1]) partitions the T packed positions into samples.
-    With validate, a malformed cu_seqlens raises ValueError (one sync).
+    With shift, `target` holds the unshifted labels and position t counts when
+    labels[t + 1] is not ignore_index (the causal shift the loss applied).
+    With validate, a malformed cu_seqlens raises ValueError (one sync);
+    without it nothing synchronises.
     """
     for name, t in (("loss", loss), ("target", target), ("cu_seqlens", cu_seqlens)):
         _require_device(name, t)
@@ -412,8 +551,9 @@ def per_sample_loss_sums(loss: torch.Tensor, target: torch.Tensor, cu_seqlens: t
     seg_loss = torch.empty(S, dtype=torch.float32, device=dev)
     seg_cnt = torch.empty(S, dtype=torch.int32, device=dev)
     status = torch.empty(1, dtype=torch.int32, device=dev)
-    check(lib.mt_segment_sum(_p(ls), _p(tgt), T, int(ignore_index), _p(cu), S, _p(seg_loss),
-                             _p(seg_cnt), _p(status), _stream(dev)), "mt_segment_sum")
+    check(lib.mt_segment_sum(_p(ls), _p(tgt), T, int(ignore_index), int(bool(shift)), _p(cu), S,
+                             _p(seg_loss), _p(seg_cnt), _p(status), _stream(dev)),
+          "mt_segment_sum")
     if validate and int(status.item()) != 0:
         raise ValueError(f"cu_seqlens is not a partition of [0, {T}): must start at 0, be "
                          f"non-decreasing and end at {T}")

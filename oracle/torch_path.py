@@ -1,4 +1,6 @@
-"""The reference's torch path on the CPU (test infrastructure only).
+"""The reference's torch path (test infrastructure only).  It runs where its
+inputs live: on the CPU, or on the GPU as the full-size checker of the
+HIP kernels (never as the path under test).
 
 Forward, per row chunk (rows are independent, so chunking is exact for the
 loss and dX and only reorders the fp32 sum of dW):
@@ -43,21 +45,23 @@ def torch_path(X: torch.Tensor, W: torch.Tensor, target: torch.Tensor,
     """
     T, H = X.shape
     V = W.shape[0]
+    dev = X.device
     n = T if rows is None else min(rows, T)
-    y_all = target.reshape(-1).to(torch.int64)
+    y_all = target.reshape(-1).to(device=dev, dtype=torch.int64)
     if grad is None:
-        g_all = torch.ones(T, dtype=torch.float32)
+        g_all = torch.ones(T, dtype=torch.float32, device=dev)
     else:
-        g_all = grad.reshape(-1).float()
+        g_all = grad.reshape(-1).to(device=dev, dtype=torch.float32)
         if g_all.numel() == 1:
             g_all = g_all.expand(T)
-    loss = torch.zeros(n, dtype=torch.float32)
-    dX = torch.zeros(n, H, dtype=X.dtype) if need_grads else None
-    dW = torch.zeros(V, H, dtype=torch.float32) if need_grads else None
+    loss = torch.zeros(n, dtype=torch.float32, device=dev)
+    dX = torch.zeros(n, H, dtype=X.dtype, device=dev) if need_grads else None
+    dW = torch.zeros(V, H, dtype=torch.float32, device=dev) if need_grads else None
+    Wf = W.float() if upcast else None
     for a in range(0, n, chunk_rows):
         b = min(a + chunk_rows, n)
         Xc, y = X[a:b], y_all[a:b]
-        logits = (F.linear(Xc.float(), W.float()).to(X.dtype) if upcast and X.dtype != torch.float32
+        logits = (F.linear(Xc.float(), Wf).to(X.dtype) if upcast and X.dtype != torch.float32
                   else F.linear(Xc, W))
         z0 = logits.float().requires_grad_(need_grads)
         z = softcap * torch.tanh(z0 / softcap) if softcap else z0
@@ -66,7 +70,7 @@ def torch_path(X: torch.Tensor, W: torch.Tensor, target: torch.Tensor,
         if need_grads:
             (G,) = torch.autograd.grad(lc, z0, g_all[a:b])
             Gd = G.to(X.dtype)
-            dX[a:b] = (Gd.float() @ W.float()).to(X.dtype) if upcast else Gd @ W
+            dX[a:b] = (Gd.float() @ Wf).to(X.dtype) if upcast else Gd @ W
             dW += Gd.float().t() @ Xc.float()
     return loss, dX, dW
 

@@ -115,3 +115,85 @@ def test_batch_rows_shift_per_row(gpu):
     l2 = out2.loss.detach().cpu().view(2, 40)
     assert torch.count_nonzero(l2[:, [i for i in range(40) if i != 3]]) == 0
     assert bool((l2[:, 3] > 0).all())
+
+
+def one_layer_llama(vocab=1500, hidden=128, seed=0):
+    """A Llama with one real decoder layer (attention + MLP) kept in fp32 and
+    a bf16 lm_head: attention's batched products stay in fp32."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(seed)
+    cfg = LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=256,
+                      num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
+                      max_position_embeddings=4096, tie_word_embeddings=False,
+                      attn_implementation="eager")
+    m = LlamaForCausalLM(cfg).float()
+    with torch.no_grad():
+        m.lm_head.weight.normal_(0, 0.05)
+    m.lm_head.to(torch.bfloat16)
+    return m
+
+
+@pytest.mark.parametrize("world_size", [1, 3])
+def test_decoder_layer_train_py_chain_with_sample_sums(gpu, world_size, monkeypatch):
+    """A packed minibatch with a dummy sample (all labels ignored, as the
+    collator pads with, sampler.py:193-194) through a model with a real
+    decoder layer, driven as train.py:97-104 drives it (no grad_scale): the
+    fused kernels run (path fused_unit), the loss, the lm_head gradient and a
+    decoder weight's gradient match the unpatched model on the CPU, and the
+    per-sample sums over the collator's cu_seqlens match the C restatement,
+    with exactly 0 / 0 for the dummy sample."""
+    import copy
+
+    import numpy as np
+
+    from mini_trainer_amd import cu_seqlens_from_minibatch, path_of
+    from mini_trainer_amd.flce import FUSED_ENV
+    from oracle import ref
+
+    monkeypatch.setenv(FUSED_ENV, "1")
+    model = one_layer_llama()
+    ref_model = copy.deepcopy(model)
+    lengths = [37, 120, 5, 64, 90]
+    ids, labels, pos = packed_batch(lengths, 1500)
+    labels[0, 157:162] = -100  # the 5-token dummy sample
+    minibatch = [{"input_ids": ids[0, a:a + L].tolist()}
+                 for a, L in zip(np.cumsum([0] + lengths[:-1]), lengths)]
+    cu = cu_seqlens_from_minibatch(minibatch)
+    assert cu.tolist() == [0, 37, 157, 162, 226, 316]
+
+    shifted = F.pad(labels, (0, 1), value=-100)[..., 1:].reshape(-1)
+    n = int((shifted != -100).sum())
+    # unpatched model on the CPU: hidden (fp32) -> bf16 -> F.linear -> .float() -> CE
+    hidden = ref_model.model(input_ids=ids, position_ids=pos).last_hidden_state
+    logits = F.linear(hidden.reshape(-1, 128).to(torch.bfloat16), ref_model.lm_head.weight).float()
+    rl = F.cross_entropy(logits, shifted, ignore_index=-100, reduction="none")
+    (rl.sum() * world_size / n).backward()
+
+    model = patch_causal_lm(model.to(gpu))
+    out = model(input_ids=ids.to(gpu), labels=labels.to(gpu), position_ids=pos.to(gpu),
+                cu_seqlens=cu)
+    assert path_of(out.loss) == "fused_unit"
+    loss = out.loss.float().sum()
+    loss.detach().item()
+    (loss * world_size / n).backward()
+    torch.cuda.synchronize()
+
+    valid = shifted != -100
+    l = out.loss.detach().cpu()
+    r = rl.detach()
+    assert torch.equal(l[~valid], torch.zeros(int((~valid).sum())))
+    assert ((l[valid] - r[valid]).abs() / r[valid].abs()).max().item() <= 2e-3
+    assert rel_fro(model.lm_head.weight.grad.float().cpu(),
+                   ref_model.lm_head.weight.grad.float()) <= 1e-2
+    q_gpu = model.model.layers[0].self_attn.q_proj.weight.grad.cpu()
+    q_ref = ref_model.model.layers[0].self_attn.q_proj.weight.grad
+    assert rel_fro(q_gpu, q_ref) <= 1e-2
+
+    want_l, want_c, st = ref.segment_sum(l.numpy(), shifted.numpy(), cu.numpy())
+    assert st == 0
+    seg_l, seg_c = out.seg_loss.cpu().numpy(), out.seg_cnt.cpu().numpy()
+    assert np.array_equal(seg_c, want_c)
+    assert np.allclose(seg_l, want_l, rtol=1e-6, atol=0)
+    assert seg_c[2] == 0 and seg_l[2] == 0.0  # the dummy sample
+    assert int(seg_c.sum()) == n

@@ -1,0 +1,220 @@
+"""The reference's unchanged caller reaches the fused kernels.
+
+train.py:97-104 calls the drop-in with the reference's own arguments
+(none_reduction_losses.py:5-13, no extra keyword), sums the per-token loss,
+syncs with .item(), scales by world_size / batch_num_loss_counted_tokens and
+calls backward().  Where the fused path pays, the forward forms dX and dW
+for a unit upstream gradient (path "fused_unit", the structure of the
+reference's Liger call at none_reduction_losses.py:16-23) and the backward
+rescales them on the device (mt_flce_scale_grads).  Checked against the
+reference's torch path with the north-star tolerances (loss 2e-3 relative,
+dX and dW 1e-2 relative Frobenius, ignored rows exactly +0.0 / 0), for
+world sizes that make the scale a non-power of two, for a per-token
+gradient (recompute fallback), softcap, several chunks, and the C-ABI pieces
+this path adds: the rescale kernels (bit-exact against torch's fp32 multiply
+and round-to-nearest-even), the shifted per-sample sums (against the C
+restatement) and the per-launch timing hook.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from mini_trainer_amd import _lib, fused_linear_cross_entropy, path_of, per_sample_loss_sums
+from mini_trainer_amd.flce import (BACKWARD_BUDGET_ENV, FUSED_ENV, PROMISE_ULPS, _p, _stream,
+                                   fused_plan, profile_enable, profile_report)
+from mini_trainer_amd.none_reduction_losses import (
+    liger_fixed_fused_linear_cross_entropy_none_reduction as drop_in)
+from oracle import ref
+from oracle.torch_path import rel_fro
+
+from test_gpu_parity import check_parity, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _fused(monkeypatch):
+    # the fused kernels whatever the planner prefers at these small sizes
+    monkeypatch.setenv(FUSED_ENV, "1")
+
+
+def train_py_chain(dev, X, W, y, world_size, n_counted, softcap=None):
+    """train.py:97-104, literally, over the drop-in."""
+    Xd = X.to(dev).requires_grad_(True)
+    Wd = W.to(dev).requires_grad_(True)
+    out = drop_in(Xd, Wd, y.to(dev), None, -100, softcap)
+    path = path_of(out)
+    loss = out.float().sum()
+    loss.detach().item()
+    loss = loss * world_size / n_counted
+    loss.backward()
+    torch.cuda.synchronize()
+    return path, out.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu()
+
+
+@pytest.mark.parametrize("world_size", [1, 3, 6])
+@pytest.mark.parametrize("T,H,V", [(300, 128, 1000), (513, 192, 2065), (700, 256, 2560)])
+def test_reference_chain_takes_the_fused_kernels(gpu, world_size, T, H, V):
+    print(f"case unit path T={T} H={H} V={V} world_size={world_size}", flush=True)
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=T + world_size)
+    n = int((y != -100).sum())
+    path, loss, dX, dW = train_py_chain(gpu, X, W, y, world_size, n)
+    assert path == "fused_unit"
+    check_parity(X, W, y, loss, dX, dW, grad=torch.full((T,), world_size / n))
+
+
+def test_unit_path_softcap_and_many_chunks(gpu, monkeypatch):
+    # tiny budget -> 256-row chunks (uneven last one), dW accumulated across
+    # chunks before the rescale
+    monkeypatch.setenv(BACKWARD_BUDGET_ENV, "1")
+    X, W, y = make_case(1100, 128, 1300, torch.bfloat16, seed=7, mask_frac=0.2, w_std=0.2)
+    n = int((y != -100).sum())
+    assert fused_plan(1100, n, 128, 1300)[0] == 256
+    path, loss, dX, dW = train_py_chain(gpu, X, W, y, 3, n, softcap=3.0)
+    assert path == "fused_unit"
+    check_parity(X, W, y, loss, dX, dW, grad=torch.full((1100,), 3.0 / n), softcap=3.0)
+
+
+@pytest.mark.parametrize("softcap", [None, 2.5])
+def test_unit_path_per_token_gradient_recomputes(gpu, softcap):
+    # a gradient that differs per token cannot be a rescale of the unit one:
+    # the backward recomputes with the saved lse
+    X, W, y = make_case(400, 128, 3000, torch.bfloat16, seed=11, w_std=0.2)
+    grad = torch.rand(400, generator=torch.Generator().manual_seed(3)) * 2 - 0.5
+    Xd, Wd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True)
+    out = drop_in(Xd, Wd, y.to(gpu), None, -100, softcap)
+    assert path_of(out) == "fused_unit"
+    out.backward(grad.to(gpu))
+    torch.cuda.synchronize()
+    check_parity(X, W, y, out.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(), grad=grad,
+                 softcap=softcap)
+
+
+def test_unit_path_only_when_the_weight_gradient_is_wanted(gpu):
+    X, W, y = make_case(256, 64, 512, torch.bfloat16, seed=22)
+    Xd = X.to(gpu).requires_grad_(True)
+    out = drop_in(Xd, W.to(gpu), y.to(gpu))  # frozen lm_head: dW would be waste
+    assert path_of(out) == "general"
+    acc = torch.zeros(W.shape, dtype=torch.float32, device=gpu)
+    out2 = fused_linear_cross_entropy(Xd, W.to(gpu).requires_grad_(True), y.to(gpu),
+                                      dw_accumulator=acc)
+    assert path_of(out2) == "general"  # an accumulator needs the scale at the forward
+
+
+def test_unit_path_second_backward_raises(gpu):
+    X, W, y = make_case(256, 64, 512, torch.bfloat16, seed=24)
+    Xd, Wd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True)
+    out = drop_in(Xd, Wd, y.to(gpu))
+    (out.sum() * 0.5).backward(retain_graph=True)
+    with pytest.raises(RuntimeError, match="second backward"):
+        (out.sum() * 0.5).backward()
+
+
+@pytest.mark.parametrize("world_size", [3, 6])
+def test_promise_accepts_train_py_rounding(gpu, world_size):
+    # grad_scale = world_size / n promised, the literal train.py expression
+    # back-propagated: fl32(fl32(1 / n) * world_size) may differ from
+    # fl32(world_size / n) by an ulp -- accepted; a 1e-3 relative miss is not
+    X, W, y = make_case(300, 128, 1000, torch.bfloat16, seed=31)
+    n = int((y != -100).sum())
+    Xd, Wd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True)
+    out = fused_linear_cross_entropy(Xd, Wd, y.to(gpu), grad_scale=world_size / n)
+    assert path_of(out) == "fused"
+    loss = out.float().sum()
+    (loss * world_size / n).backward()
+    torch.cuda.synchronize()
+    check_parity(X, W, y, out.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(),
+                 grad=torch.full((300,), world_size / n))
+    out = fused_linear_cross_entropy(Xd, Wd, y.to(gpu), grad_scale=world_size / n)
+    with pytest.raises(RuntimeError, match=f"{PROMISE_ULPS} fp32 ulp"):
+        (out.float().sum() * (world_size / n * (1 + 1e-3))).backward()
+
+
+@pytest.mark.parametrize("H,ld", [(64, 64), (66, 72)])
+def test_scale_grads_bit_exact(gpu, H, ld):
+    """mt_flce_scale_grads against torch: bf16 dX in place, fp32 dW in place
+    and fp32 dW -> bf16; columns between H and the pitch are left alone."""
+    lib = _lib.load()
+    g = torch.Generator(device=gpu).manual_seed(5)
+    T, V = 333, 517
+    dX = torch.randn(T, ld, device=gpu, generator=g).to(torch.bfloat16)
+    dW = torch.randn(V, ld, device=gpu, generator=g)
+    scale = torch.tensor([0.37], device=gpu)
+    want_x = dX.clone()
+    want_x[:, :H] = (dX[:, :H].float() * 0.37).to(torch.bfloat16)
+    want_w32 = dW.clone()
+    want_w32[:, :H] = dW[:, :H] * scale
+    out16 = torch.full((V, ld), 7.0, device=gpu, dtype=torch.bfloat16)
+    want_w16 = out16.clone()
+    want_w16[:, :H] = (dW[:, :H] * scale).to(torch.bfloat16)
+    s = _stream(gpu)
+    _lib.check(lib.mt_flce_scale_grads(_p(scale), _p(dX), T, H, ld, _lib.MT_DTYPE_BF16, _p(dW),
+                                       V, ld, _p(out16), ld, _lib.MT_DTYPE_BF16, s), "scale")
+    _lib.check(lib.mt_flce_scale_grads(_p(scale), None, 0, H, ld, _lib.MT_DTYPE_BF16, _p(dW),
+                                       V, ld, _p(dW), ld, _lib.MT_DTYPE_F32, s), "scale")
+    torch.cuda.synchronize()
+    assert torch.equal(dX, want_x)
+    assert torch.equal(out16, want_w16)
+    assert torch.equal(dW, want_w32)
+
+
+def test_segment_sums_of_shifted_labels(gpu):
+    """mt_segment_sum with shift counts position t when labels[t + 1] is
+    valid; against the C restatement over the shifted target."""
+    rng = np.random.default_rng(4)
+    lengths = [5, 40, 1, 77, 5, 20]  # the 5-token samples are dummies
+    T = sum(lengths)
+    labels = rng.integers(0, 50, T).astype(np.int64)
+    labels[rng.random(T) < 0.3] = -100
+    labels[:5] = -100
+    labels[123:128] = -100
+    loss = rng.random(T).astype(np.float32)
+    shifted = np.concatenate([labels[1:], [-100]])
+    loss[shifted == -100] = 0.0
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    want_l, want_c, st = ref.segment_sum(loss, shifted, cu)
+    assert st == 0
+    sl, sc = per_sample_loss_sums(torch.from_numpy(loss).to(gpu), torch.from_numpy(labels).to(gpu),
+                                  torch.from_numpy(cu).to(gpu), shift=True)
+    assert np.array_equal(sc.cpu().numpy(), want_c)
+    assert np.allclose(sl.cpu().numpy(), want_l, rtol=1e-6, atol=0)
+
+
+def test_profile_hook_reports_the_fused_step(gpu):
+    X, W, y = make_case(700, 128, 2560, torch.bfloat16, seed=41)
+    n = int((y != -100).sum())
+    profile_enable(True)
+    try:
+        path, *_ = train_py_chain(gpu, X, W, y, 1, n)
+    finally:
+        profile_enable(False)
+    rep = profile_report()
+    assert path == "fused_unit"
+    for k in ("fwd_bf16_kernel<store_s>", "softmax_grad_kernel", "dx_bf16_kernel<emit>",
+              "dw_bf16_kernel", "dx_dw_phase", "scale_rows_kernel<dX>", "scale_rows_kernel<dW>"):
+        assert k in rep and rep[k]["launches"] >= 1 and rep[k]["ms_total"] > 0, k
+    # algorithmic work: 2 H V n for each GEMM over all chunks, their sum for the phase
+    f = 2.0 * 128 * 2560 * n
+    for k in ("fwd_bf16_kernel<store_s>", "dx_bf16_kernel<emit>", "dw_bf16_kernel"):
+        assert rep[k]["flops"] == pytest.approx(f, rel=1e-9)
+    assert rep["dx_dw_phase"]["flops"] == pytest.approx(2 * f, rel=1e-9)
+    assert rep["dx_dw_phase"]["ms_total"] >= rep["dw_bf16_kernel"]["ms_total"] * 0.5
+    # the report released its records; a disabled hook records nothing
+    assert profile_report() == {}
+    train_py_chain(gpu, X, W, y, 1, n)
+    assert profile_report() == {}
+    # a too-small buffer is an error that names the size it needs and keeps
+    # the records for the retry
+    profile_enable(True)
+    try:
+        train_py_chain(gpu, X, W, y, 1, n)
+    finally:
+        profile_enable(False)
+    lib = _lib.load()
+    need = ctypes.c_size_t(0)
+    assert lib.mt_flce_profile_report(None, 0, ctypes.byref(need)) == 1 and need.value > 100
+    assert "dw_bf16_kernel" in profile_report()
