@@ -227,9 +227,9 @@ def timed(step, steps: int, warmup: int) -> float:
 
 def extra_hbm(data, Wl, n_counted: int, dtype) -> dict:
     """Allocator peak of one minibatch of the reference step minus the live
-    inputs and the required outputs: loss [T] fp32, dX [T, H] (X.grad), the
-    fp32 dW the library forms and W.grad in the weight's dtype (the
-    parameter gradient the reference holds too)."""
+    inputs and the required outputs: loss [T] fp32, dX [T, H] (X.grad) and
+    the fp32 dW the library forms (W.grad, in the weight's dtype, is narrowed
+    into that same allocation)."""
     X, y = data[0]
     T, H = X.shape
     V = Wl.shape[0]
@@ -242,7 +242,7 @@ def extra_hbm(data, Wl, n_counted: int, dtype) -> dict:
     reference_step([(X, y)], Wl, n_counted)
     torch.cuda.synchronize()
     peak = torch.cuda.max_memory_allocated(dev)
-    outputs = T * 4 + T * H * es + V * H * 4 + V * H * es
+    outputs = T * 4 + T * H * es + V * H * 4
     return {"extra_hbm_GB": (peak - base - outputs) / 1e9,
             "extra_hbm_budget_GB": 0.05 * T * V * es / 1e9,
             "peak_memory_GB": peak / 1e9}
@@ -371,10 +371,17 @@ def main():
     ap.add_argument("--other-configs", default="2,4,5",
                     help="comma-separated configurations also timed (reference step, 3 steps "
                          "on device-generated inputs) when --config is 3; '' for none")
+    ap.add_argument("--step-only", action="store_true",
+                    help="only the reference step (timed, then profiled): no variants, no "
+                         "general-forward roofline, no other configurations or comparators "
+                         "(what the committed rocprofv3 summaries run)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (the reference point that scales "
                          "FETCH_SIZE / WRITE_SIZE counter readings to bytes) and exit")
     args = ap.parse_args()
+    if args.step_only:
+        args.no_variants = args.no_torch_gpu = args.no_cpu_baseline = True
+        args.other_configs = ""
     if args.copy_calibration:
         copy_calibration()
         return
@@ -449,9 +456,11 @@ def main():
         log(f"promised-gradient step {ms_p:.2f} ms, general path {ms_g:.2f} ms")
         torch.cuda.empty_cache()
     C, Cv, _ = backward_plan(T, n_valid[0], H, V, cfg.dtype)
-    gen_fwd = general_forward_roofline(data[0][0], W.detach(), data[0][1], peak_flops,
-                                       max(3, min(args.steps, 5)))
-    torch.cuda.empty_cache()
+    gen_fwd = None
+    if not args.step_only:
+        gen_fwd = general_forward_roofline(data[0][0], W.detach(), data[0][1], peak_flops,
+                                           max(3, min(args.steps, 5)))
+        torch.cuda.empty_cache()
 
     out = {
         "metric": METRIC,

@@ -215,9 +215,15 @@ int mt_segment_sum(const float* loss, const int64_t* target, int64_t T,
  *   scale      fp32 [1] (device): read by the kernels, no host sync
  *   dX         [T, H] of dtype_x, leading dimension lddx, scaled in place
  *   dW         fp32 [V, H], leading dimension lddw
- *   dW_out     [V, H] of dtype_out, leading dimension ldo: either dW itself
- *              (fp32, same pitch: in place) or a separate buffer (bf16 output
- *              rounds to nearest even; it may not partially overlap dW)
+ *   dW_out     [V, H] of dtype_out, leading dimension ldo: a separate buffer
+ *              (it may not partially overlap dW), or dW itself (ldo == lddw):
+ *              fp32 is then scaled in place, and bf16 is narrowed in place --
+ *              bf16 row r goes to element offset r * ldo (bf16 units) from
+ *              dW's base, i.e. the first half of dW's bytes when lddw == H,
+ *              so the weight gradient in the weight's dtype needs no second
+ *              allocation (H <= 16384; rows are processed in launches of
+ *              doubling length so that no fp32 row is overwritten before it
+ *              is read).  bf16 output rounds to nearest even.
  * T = 0 or V = 0 skips that tensor.
  */
 int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H,

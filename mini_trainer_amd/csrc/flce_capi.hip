@@ -958,6 +958,37 @@ int mt_segment_sum(const float* loss, const int64_t* target, int64_t T, int64_t 
   return check_launch("segment_sum_kernel");
 }
 
+}  // extern "C"
+
+namespace {
+
+constexpr int kMaxNarrowCols = 16 * 1024;
+
+// Phases {0}, {1}, [2, 4), [4, 8), ... of narrow_rows_inplace_kernel (see
+// there): each launch overwrites only rows that an earlier launch on the
+// same stream has read.
+int launch_narrow_inplace(float* base, int64_t ld, int64_t V, int64_t H, const float* scale,
+                          hipStream_t s) {
+  const int64_t nv = cdiv(H, 4);
+  void (*kern)(float*, int64_t, int64_t, int64_t, int64_t, const float*) =
+      nv <= 256    ? narrow_rows_inplace_kernel<1>
+      : nv <= 512  ? narrow_rows_inplace_kernel<2>
+      : nv <= 1024 ? narrow_rows_inplace_kernel<4>
+      : nv <= 2048 ? narrow_rows_inplace_kernel<8>
+                   : narrow_rows_inplace_kernel<16>;
+  for (int64_t lo = 0, hi = 1; lo < V; lo = hi, hi = std::max<int64_t>(2 * lo, lo + 1)) {
+    const int64_t r1 = std::min(hi, V);
+    hipLaunchKernelGGL(kern, dim3((uint32_t)std::min<int64_t>(r1 - lo, 16384)), dim3(256), 0, s,
+                       base, ld, lo, r1, H, scale);
+    MT_TRY(check_launch("narrow_rows_inplace_kernel"));
+  }
+  return MT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H, int64_t lddx,
                         int dtype_x, const float* dW, int64_t V, int64_t lddw, void* dW_out,
                         int64_t ldo, int dtype_out, mt_stream_t stream) {
@@ -973,8 +1004,11 @@ int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H, int6
        reinterpret_cast<uintptr_t>(dW_out)) % 16 != 0 ||
       (lddx * esx) % 16 != 0 || (lddw * 4) % 16 != 0 || (ldo * eso) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "dX / dW / dW_out must be 16-byte aligned with 16-byte row pitches");
-  if (dW_out == dW && (dtype_out != MT_DTYPE_F32 || ldo != lddw))
-    return fail(MT_ERR_INVALID_ARGUMENT, "in-place dW scaling needs fp32 output with the same pitch");
+  if (dW_out == dW && ldo != lddw)
+    return fail(MT_ERR_INVALID_ARGUMENT, "in-place dW scaling needs ldo == lddw");
+  if (dW_out == dW && eso == 2 && H > kMaxNarrowCols)
+    return fail(MT_ERR_UNSUPPORTED, "in-place narrowing to bf16 supports H <= %d (H=%lld)",
+                kMaxNarrowCols, (long long)H);
   if (dW_out != dW && V > 0) {
     const char *a0 = static_cast<const char*>(static_cast<const void*>(dW)), *a1 = a0 + (size_t)V * lddw * 4;
     const char *b0 = static_cast<const char*>(dW_out), *b1 = b0 + (size_t)V * ldo * eso;
@@ -992,7 +1026,11 @@ int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H, int6
     prof_end(p, s);
     MT_TRY(check_launch("scale_rows_kernel"));
   }
-  if (V > 0) {
+  if (V > 0 && dW_out == dW && eso == 2) {
+    const int p = prof_begin("narrow_rows_inplace_kernel<dW>", 0, (double)V * H * 6, s);
+    MT_TRY(launch_narrow_inplace(const_cast<float*>(dW), lddw, V, H, scale, s));
+    prof_end(p, s);
+  } else if (V > 0) {
     const int p = prof_begin("scale_rows_kernel<dW>", 0, (double)V * H * (4 + eso), s);
     if (eso == 2)
       hipLaunchKernelGGL(scale_rows_f32_kernel<true>, dim3((uint32_t)std::min<int64_t>(V, 16384)), dim3(256),
@@ -1055,7 +1093,7 @@ int mt_flce_profile_report(char* buf, size_t len, size_t* needed) {
     const Agg& a = agg[i];
     snprintf(item, sizeof item,
              "%s\"%s\": {\"launches\": %ld, \"ms_total\": %.6f, \"ms_min\": %.6f, "
-             "\"ms_max\": %.6f, \"flops\": %.6e, \"bytes\": %.6e}",
+             "\"ms_max\": %.6f, \"flops\": %.17g, \"bytes\": %.17g}",
              i ? ", " : "", a.name, a.n, a.ms, a.ms_min, a.ms_max, a.flops, a.bytes);
     out += item;
   }

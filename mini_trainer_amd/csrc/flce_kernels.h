@@ -768,6 +768,48 @@ __global__ __launch_bounds__(256) void scale_rows_bf16_kernel(char* p, int64_t l
   }
 }
 
+// In-place narrowing: bf16 row r = scale * fp32 row r, written to the first
+// bytes of the same allocation (bf16 row r at element offset r * ld in bf16
+// units, i.e. bytes [2 r ld, 2 r ld + 2 cols)), so the weight gradient in the
+// weight's dtype needs no second buffer.  bf16 row r overlaps fp32 row
+// floor(r / 2) only, so one launch per phase of rows -- {0}, {1}, [2, 4),
+// [4, 8), ... -- overwrites only rows an earlier phase has consumed; within a
+// row (row 0 overlaps itself) the workgroup reads the whole row before any of
+// it is written.  kPer 16-byte vectors per thread cover cols <= 1024 kPer.
+template <int kPer>
+__global__ __launch_bounds__(256) void narrow_rows_inplace_kernel(float* base, int64_t ld,
+                                                                  int64_t r0, int64_t r1,
+                                                                  int64_t cols,
+                                                                  const float* scale) {
+  const float c = *scale;
+  const int64_t nv = cols / 4, nt = cols - nv * 4;
+  for (int64_t r = r0 + blockIdx.x; r < r1; r += gridDim.x) {
+    const float* src = base + r * ld;
+    f32x4_t v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int64_t idx = threadIdx.x + (int64_t)i * 256;
+      v[i] = idx < nv ? reinterpret_cast<const f32x4_t*>(src)[idx] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    const float t = (int64_t)threadIdx.x < nt ? src[nv * 4 + threadIdx.x] : 0.f;
+    __syncthreads();
+    char* dst = reinterpret_cast<char*>(base) + r * ld * 2;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int64_t idx = threadIdx.x + (int64_t)i * 256;
+      if (idx < nv) {
+        u32x2_t o;
+        o[0] = pack_bf16x2(v[i][0] * c, v[i][1] * c);
+        o[1] = pack_bf16x2(v[i][2] * c, v[i][3] * c);
+        reinterpret_cast<u32x2_t*>(dst)[idx] = o;
+      }
+    }
+    if ((int64_t)threadIdx.x < nt)
+      reinterpret_cast<__bf16*>(dst)[nv * 4 + threadIdx.x] = (__bf16)(t * c);
+    __syncthreads();
+  }
+}
+
 // ===========================================================================
 // Cross-entropy over materialised logits [T, V] (reduction 'none').
 // One workgroup of 256 threads per row; 16-byte loads along V.

@@ -214,6 +214,7 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
             else:  # kept for the recompute fallback of a per-token gradient
                 ctx.save_for_backward(X, W, row_index, row_label, lse)
             ctx.meta = (n, gstride, hidden.shape, float(softcap), dt)
+            ctx.w_dtype = weight.dtype
             ctx.dX = dX
             ctx.dW = None if dw_accumulator is not None else dW
             ctx.fused_consumed = False
@@ -258,7 +259,7 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
                                    _p(dX), dX.stride(0), _p(dW), dW.stride(0), accumulate, C, Cv,
                                    _p(ws), ws_bytes, _stream(dev)), "mt_flce_backward")
         grad_x = dX.view(hshape) if need_x else None
-        grad_w = dW if (need_w and acc is None) else None
+        grad_w = _weight_grad_in_dtype(dW, W.dtype) if (need_w and acc is None) else None
         return (grad_x, grad_w) + none
 
     @staticmethod
@@ -291,7 +292,8 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         ctx.dX = ctx.dW = None
         ctx.fused_consumed = True
         grad_x = dX.view(hshape) if ctx.needs_input_grad[0] else None
-        grad_w = dW if ctx.needs_input_grad[1] else None
+        grad_w = (_weight_grad_in_dtype(dW, ctx.w_dtype)
+                  if ctx.needs_input_grad[1] and dW is not None else None)
         return (grad_x, grad_w) + (None,) * 7
 
 
@@ -315,17 +317,14 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         g, gstride = _grad_vector(grad_loss, T)
         if gstride == 0:
             # one upstream scalar for every token: rescale the unit-gradient
-            # dX and dW (dW straight into the weight's dtype)
+            # dX and dW, dW straight into the weight's dtype in place
             scale = g.reshape(-1)[:1]
-            if W.dtype == torch.float32:
-                dW_out, out_dt = dW, MT_DTYPE_F32
-            else:
-                dW_out, out_dt = torch.empty((V, H), dtype=W.dtype, device=dev), _dtype_code(W.dtype)
             check(lib.mt_flce_scale_grads(_p(scale), _p(dX) if need_x else None,
                                           T if need_x else 0, H, dX.stride(0), dt, _p(dW),
-                                          V if need_w else 0, dW.stride(0),
-                                          _p(dW_out), dW_out.stride(0), out_dt, _stream(dev)),
+                                          V if need_w else 0, dW.stride(0), _p(dW), dW.stride(0),
+                                          _dtype_code(W.dtype), _stream(dev)),
                   "mt_flce_scale_grads")
+            dW_out = _narrowed_view(dW, W.dtype)
             del dW
         else:
             # a per-token gradient: the unit-gradient results cannot be
@@ -340,6 +339,32 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         grad_x = dX.view(hshape) if need_x else None
         grad_w = dW_out if need_w else None
         return (grad_x, grad_w) + (None,) * 7
+
+
+def _narrowed_view(dW: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """The [V, H] gradient in `dtype` that mt_flce_scale_grads narrowed into
+    the first bytes of the fp32 dW's own storage (bf16 row r at element
+    offset r * dW.stride(0)); fp32 is dW itself."""
+    if dtype == torch.float32:
+        return dW
+    V, H = dW.shape
+    out = torch.empty(0, dtype=dtype, device=dW.device)
+    # storage offsets count elements: one fp32 element is two 16-bit ones
+    out.set_(dW.untyped_storage(), 2 * dW.storage_offset(), (V, H), (dW.stride(0), 1))
+    return out
+
+
+def _weight_grad_in_dtype(dW: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """fp32 dW -> the weight's dtype inside dW's own allocation (autograd
+    would otherwise cast it into a second buffer while dW is still alive)."""
+    if dtype == torch.float32:
+        return dW
+    one = torch.ones(1, dtype=torch.float32, device=dW.device)
+    V, H = dW.shape
+    check(load().mt_flce_scale_grads(_p(one), None, 0, H, H, MT_DTYPE_F32, _p(dW), V,
+                                     dW.stride(0), _p(dW), dW.stride(0), _dtype_code(dtype),
+                                     _stream(dW.device)), "mt_flce_scale_grads")
+    return _narrowed_view(dW, dtype)
 
 
 # A promised gradient is accepted when every token's received gradient is

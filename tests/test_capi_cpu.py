@@ -112,10 +112,14 @@ def test_backward_and_misc_host_checks():
     assert lib.mt_flce_backward(*bad, 256, 256, 16, 1 << 30, None) == 1
     assert lib.mt_flce_prepare(None, -1, 10, -100, 0, None, None, None, None) == 1
     assert lib.mt_segment_sum(None, None, 4, -100, 0, None, 1, None, None, None, None) == 1
-    # scale_grads: null scale, and an fp32 in-place request with a bf16 output
+    # scale_grads: null scale; in place with another pitch; in-place narrowing
+    # beyond the row width one workgroup holds
     assert lib.mt_flce_scale_grads(None, None, 0, 64, 64, 1, None, 0, 64, None, 64, 0, None) == 1
-    assert lib.mt_flce_scale_grads(16, None, 0, 64, 64, 1, 16, 4, 64, 16, 64, 1, None) == 1
-    assert "in-place" in lib.mt_flce_last_error().decode()
+    assert lib.mt_flce_scale_grads(16, None, 0, 64, 64, 1, 16, 4, 64, 16, 72, 1, None) == 1
+    assert "ldo == lddw" in lib.mt_flce_last_error().decode()
+    assert lib.mt_flce_scale_grads(16, None, 0, 20000, 20000, 1, 16, 4, 20000, 16, 20000, 1,
+                                   None) == 3
+    assert "H <= 16384" in lib.mt_flce_last_error().decode()
     assert lib.mt_ce_forward(None, 4, 10, 5, 1, None, -100, None, None, None, None) == 1
 
 

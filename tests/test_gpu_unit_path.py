@@ -162,6 +162,45 @@ def test_scale_grads_bit_exact(gpu, H, ld):
     assert torch.equal(dW, want_w32)
 
 
+@pytest.mark.parametrize("V,H,ld", [(1, 64, 64), (517, 66, 72), (1031, 4096, 4096)])
+def test_narrow_in_place_bit_exact(gpu, V, H, ld):
+    """fp32 dW -> bf16 scaled, written into the first bytes of dW's own
+    allocation (row r at bf16 offset r * ld): every row, including those whose
+    bytes are reused, equals torch's fp32 multiply rounded to nearest even."""
+    lib = _lib.load()
+    g = torch.Generator(device=gpu).manual_seed(V)
+    dW = torch.randn(V, ld, device=gpu, generator=g)
+    scale = torch.tensor([1.7], device=gpu)
+    want = (dW[:, :H] * scale).to(torch.bfloat16)
+    _lib.check(lib.mt_flce_scale_grads(_p(scale), None, 0, H, ld, _lib.MT_DTYPE_BF16, _p(dW), V,
+                                       ld, _p(dW), ld, _lib.MT_DTYPE_BF16, _stream(gpu)), "narrow")
+    torch.cuda.synchronize()
+    got = dW.view(torch.uint8).view(-1)[: V * ld * 2].view(torch.bfloat16).view(V, ld)[:, :H]
+    assert torch.equal(got, want)
+
+
+def test_reference_chain_extra_memory(gpu):
+    """The reference chain on the fused kernels allocates, beyond its inputs
+    and required outputs (loss, dX, the fp32 dW whose storage then holds
+    W.grad in bf16), only the fused workspace."""
+    T, H, V = 4096, 512, 32000
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=51)
+    n = int((y != -100).sum())
+    C, ws, _ = fused_plan(T, n, H, V)
+    Xd, Wd, yd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True), y.to(gpu)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(gpu)
+    base = torch.cuda.memory_allocated(gpu)
+    out = drop_in(Xd, Wd, yd)
+    assert path_of(out) == "fused_unit"
+    (out.float().sum() / n).backward()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(gpu)
+    outputs = T * 4 + T * H * 2 + V * H * 4
+    assert peak - base - outputs <= ws + (4 << 20), (peak - base - outputs, ws)
+    assert Wd.grad.dtype == torch.bfloat16 and Wd.grad.is_contiguous()
+
+
 def test_segment_sums_of_shifted_labels(gpu):
     """mt_segment_sum with shift counts position t when labels[t + 1] is
     valid; against the C restatement over the shifted target."""
@@ -195,7 +234,7 @@ def test_profile_hook_reports_the_fused_step(gpu):
     rep = profile_report()
     assert path == "fused_unit"
     for k in ("fwd_bf16_kernel<store_s>", "softmax_grad_kernel", "dx_bf16_kernel<emit>",
-              "dw_bf16_kernel", "dx_dw_phase", "scale_rows_kernel<dX>", "scale_rows_kernel<dW>"):
+              "dw_bf16_kernel", "dx_dw_phase", "scale_rows_kernel<dX>", "narrow_rows_inplace_kernel<dW>"):
         assert k in rep and rep[k]["launches"] >= 1 and rep[k]["ms_total"] > 0, k
     # algorithmic work: 2 H V n for each GEMM over all chunks, their sum for the phase
     f = 2.0 * 128 * 2560 * n
