@@ -113,6 +113,28 @@ int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H,
                     mt_stream_t stream);
 
 /*
+ * Forward without allocation (no counterpart in the reference): the same
+ * results as mt_flce_forward -- bit-identical for bf16 -- for callers that
+ * cannot allocate device memory or hand the library a workspace (code under
+ * HIP graph capture, tight serving and evaluation loops, harnesses that
+ * forbid hipMalloc).  Its scratch (the forward's (max, sum) partials and
+ * label logits) is a static device array of mt_flce_noalloc_scratch_bytes()
+ * bytes (16 MiB) per GPU, held until the process ends; valid rows are
+ * processed in chunks that fit it.  A V whose single row of partials does
+ * not fit is rejected with MT_ERR_UNSUPPORTED.  The call allocates and frees
+ * nothing.  Every call on one GPU shares that GPU's scratch, which keeps the
+ * last call's contents (nothing in it needs clearing: each chunk writes what
+ * it reads), so calls that overlap on one GPU -- on different streams, or
+ * from different host threads -- race; serialise them.
+ */
+size_t mt_flce_noalloc_scratch_bytes(void);
+int mt_flce_forward_noalloc(const void* X, const void* W, int64_t T, int64_t H,
+                            int64_t V, int64_t ldx, int64_t ldw, int dtype,
+                            float softcap, const int32_t* row_index,
+                            const int32_t* row_label, int64_t n_valid,
+                            float* loss, float* lse, mt_stream_t stream);
+
+/*
  * Backward blocking plan.  The backward recomputes logit tiles block by
  * block (chunk_rows valid tokens x chunk_vocab vocabulary entries); this
  * picks the largest blocks whose workspace fits budget_bytes (0 = default:

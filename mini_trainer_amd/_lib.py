@@ -33,6 +33,10 @@ SIGNATURES = {
     "mt_flce_forward": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                                 c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                 c_void_p, c_size_t, c_void_p]),
+    "mt_flce_noalloc_scratch_bytes": (c_size_t, []),
+    "mt_flce_forward_noalloc": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                        c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
+                                        c_void_p, c_void_p, c_void_p]),
     "mt_flce_backward_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t,
                                       POINTER(c_int64), POINTER(c_int64), POINTER(c_size_t)]),
     "mt_flce_backward": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,

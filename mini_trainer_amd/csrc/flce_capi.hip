@@ -791,6 +791,102 @@ int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H, int64_t 
                                lse, p, static_cast<char*>(workspace), s);
 }
 
+}  // extern "C"
+
+// ------------------------------------------------- forward without allocation
+// Scratch of mt_flce_forward_noalloc: the (max, sum) partials and label
+// logits of one row chunk, in a file-scope device array (one copy per GPU the
+// library runs on, held until the process ends).  Host code never passes the
+// array's name to a kernel: its device address comes from
+// hipGetSymbolAddress, once per device with that device current.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+namespace {
+
+int scratch_ptr(char** out) {
+  static std::mutex mu;
+  static char* ptrs[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(MT_ERR_HIP, "hipGetDevice failed or device id out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MT_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    ptrs[dev] = static_cast<char*>(p);
+  }
+  *out = ptrs[dev];
+  return MT_OK;
+}
+
+// Valid rows per chunk whose forward workspace fits the scratch (a multiple
+// of 256 rows, the row tile, when more than one tile fits), or 0.
+int64_t noalloc_rows(int64_t n_valid, int64_t V, int es) {
+  const int64_t cap = std::min<int64_t>(round_up(n_valid, 256), INT32_MAX);
+  int64_t lo = 0, hi = cap;
+  while (lo < hi) {  // largest r <= cap with forward_ws(plan(r), r) <= scratch
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (forward_ws(plan_forward(mid, V, es), mid) <= kScratchBytes) lo = mid;
+    else hi = mid - 1;
+  }
+  if (lo >= 256 && lo < n_valid) {
+    const int64_t r = lo / 256 * 256;
+    if (forward_ws(plan_forward(r, V, es), r) <= kScratchBytes) lo = r;
+  }
+  return lo;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mt_flce_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int mt_flce_forward_noalloc(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
+                            int64_t ldx, int64_t ldw, int dtype, float softcap,
+                            const int32_t* row_index, const int32_t* row_label, int64_t n_valid,
+                            float* loss, float* lse, mt_stream_t stream) {
+  MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
+  if (n_valid < 0 || n_valid > T)
+    return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
+  if (T == 0) return MT_OK;
+  if (!row_index || !loss || (n_valid > 0 && (!row_label || !lse)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const int es = esize_of(dtype);
+  const int64_t rows = n_valid > 0 ? noalloc_rows(n_valid, V, es) : 0;
+  if (n_valid > 0 && rows == 0)
+    return fail(MT_ERR_UNSUPPORTED,
+                "V=%lld: one row's forward partials exceed the %zu-byte scratch of "
+                "mt_flce_forward_noalloc; use mt_flce_forward with a workspace",
+                (long long)V, kScratchBytes);
+  char* ws = nullptr;
+  MT_TRY(scratch_ptr(&ws));
+  hipStream_t s = (hipStream_t)stream;
+  if (T - n_valid > 0) {
+    const int64_t n0 = T - n_valid;
+    hipLaunchKernelGGL(zero_scatter_f32_kernel, dim3((uint32_t)std::min<int64_t>(cdiv(n0, 256), 4096)),
+                       dim3(256), 0, s, loss, row_index + n_valid, n0);
+    MT_TRY(check_launch("zero_scatter_f32_kernel"));
+  }
+  // every partial and label logit a chunk reads is written by that chunk's
+  // own forward kernel first, so the scratch needs no clearing between calls
+  for (int64_t c0 = 0; c0 < n_valid; c0 += rows) {
+    const int64_t cn = std::min(rows, n_valid - c0);
+    const FwdPlan p = plan_forward(cn, V, es);
+    if (dtype == MT_DTYPE_BF16)
+      MT_TRY(launch_forward<__bf16>(X, W, H, V, ldx, ldw, softcap, row_index + c0, row_label + c0,
+                                    cn, loss, lse + c0, p, ws, s));
+    else
+      MT_TRY(launch_forward<float>(X, W, H, V, ldx, ldw, softcap, row_index + c0, row_label + c0,
+                                   cn, loss, lse + c0, p, ws, s));
+  }
+  return MT_OK;
+}
+
 int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
                           size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
                           size_t* workspace_bytes) {
