@@ -25,8 +25,10 @@
  *     human-readable description of the last non-zero status.
  *   - Layouts: X [T, H] with leading dimension ldx (elements), W [V, H] with
  *     leading dimension ldw, both row-major with unit stride along H.
- *     ldx and ldw must be multiples of 8 and the base pointers 16-byte aligned.
- *     H must be a multiple of 64.  dtype selects bf16 (MFMA path) or fp32
+ *     Row pitches (ldx, ldw times the element size) must be multiples of 16
+ *     bytes and the base pointers 16-byte aligned; H must be a multiple of 8
+ *     (bf16) or 4 (fp32), i.e. whole 16-byte chunks -- a partial last K
+ *     stage is masked inside the kernels.  dtype selects bf16 (MFMA path) or fp32
  *     inputs; loss / lse / dW are always fp32, dX has the dtype of X.
  *   - mt_flce_fused and the bf16 mt_flce_backward run their dW GEMMs on a
  *     second stream of the library's own (one per device, created on first
@@ -111,6 +113,17 @@ int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H,
                     const int32_t* row_label, int64_t n_valid, float* loss,
                     float* lse, void* workspace, size_t workspace_bytes,
                     mt_stream_t stream);
+
+/*
+ * Bytes one bf16 operand buffer may span (the kernels address X, the
+ * weight's vocabulary blocks, G, the fused logits chunk and X^T with 32-bit
+ * offsets): 4 GiB - 1, lowered by the test hook MT_FLCE_MAX_BUFFER_BYTES.
+ * bf16 X beyond it is rejected (MT_ERR_UNSUPPORTED: the caller splits the
+ * call over row ranges); a weight beyond it runs in vocabulary blocks on
+ * mt_flce_forward / mt_flce_backward, and mt_flce_fused rejects it.
+ * No counterpart in the reference.
+ */
+uint64_t mt_flce_max_buffer_bytes(void);
 
 /*
  * Forward without allocation (no counterpart in the reference): the same
@@ -246,7 +259,8 @@ int mt_segment_sum(const float* loss, const int64_t* target, int64_t T,
  *              allocation (H <= 16384; rows are processed in launches of
  *              doubling length so that no fp32 row is overwritten before it
  *              is read).  bf16 output rounds to nearest even.
- * T = 0 or V = 0 skips that tensor.
+ * Base pointers 16-byte aligned; row pitches multiples of 16 bytes (of 8
+ * bytes for a bf16 dW_out).  T = 0 or V = 0 skips that tensor.
  */
 int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H,
                         int64_t lddx, int dtype_x, const float* dW, int64_t V,

@@ -34,6 +34,7 @@ SIGNATURES = {
                                 c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                 c_void_p, c_size_t, c_void_p]),
     "mt_flce_noalloc_scratch_bytes": (c_size_t, []),
+    "mt_flce_max_buffer_bytes": (ctypes.c_uint64, []),
     "mt_flce_forward_noalloc": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                         c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
                                         c_void_p, c_void_p, c_void_p]),

@@ -50,6 +50,16 @@ constexpr int64_t kCUs = 256;
 constexpr size_t kAlign = 256;
 constexpr uint64_t kMaxBufferBytes = 0xffffffffull;  // reach of a 32-bit buffer offset
 
+// Bytes one buffer resource may span (the bf16 kernels address X, W blocks, G,
+// S and X^T with 32-bit offsets).  Test hook: MT_FLCE_MAX_BUFFER_BYTES=n
+// lowers it, so that small problems take the paths that split a weight
+// beyond it into vocabulary blocks.  Read at each call.
+uint64_t buffer_limit() {
+  const char* e = std::getenv("MT_FLCE_MAX_BUFFER_BYTES");
+  const unsigned long long v = e ? std::strtoull(e, nullptr, 10) : 0ull;
+  return v > 0 ? std::min<uint64_t>(v, kMaxBufferBytes) : kMaxBufferBytes;
+}
+
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Compute units of the current device (cached per device id): the grid size
@@ -191,9 +201,11 @@ int check_common(const void* X, const void* W, int64_t T, int64_t H, int64_t V, 
   if (T < 0 || T > INT32_MAX) return fail(MT_ERR_INVALID_ARGUMENT, "T=%lld out of range", (long long)T);
   if (V <= 0 || V > INT32_MAX) return fail(MT_ERR_INVALID_ARGUMENT, "V=%lld out of range", (long long)V);
   if (H <= 0 || H > INT32_MAX) return fail(MT_ERR_INVALID_ARGUMENT, "H=%lld out of range", (long long)H);
-  const int64_t hmul = dtype == MT_DTYPE_BF16 ? 64 : 32;
+  // K advances in whole 16-byte chunks; a partial last K stage is masked
+  const int64_t hmul = 16 / es;
   if (H % hmul != 0)
-    return fail(MT_ERR_UNSUPPORTED, "H=%lld must be a multiple of %lld", (long long)H, (long long)hmul);
+    return fail(MT_ERR_UNSUPPORTED, "H=%lld must be a multiple of %lld (pad the rows)", (long long)H,
+                (long long)hmul);
   if (ldx < H || ldw < H)
     return fail(MT_ERR_INVALID_ARGUMENT, "leading dimensions (ldx=%lld, ldw=%lld) must be >= H=%lld",
                 (long long)ldx, (long long)ldw, (long long)H);
@@ -203,12 +215,33 @@ int check_common(const void* X, const void* W, int64_t T, int64_t H, int64_t V, 
   if ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(W)) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "X and W must be 16-byte aligned");
   if (!(softcap >= 0.f)) return fail(MT_ERR_INVALID_ARGUMENT, "softcap must be >= 0 (0 = off)");
-  // bf16 kernels address X and W rows with 32-bit buffer offsets
-  if (es == 2 && ((uint64_t)T * ldx * es > kMaxBufferBytes || (uint64_t)V * ldw * es > kMaxBufferBytes))
+  // bf16 kernels address X rows with 32-bit buffer offsets (the host layer
+  // splits larger X over row ranges); W is taken in vocabulary blocks of at
+  // most that reach, each at least one 256-row tile
+  if (es == 2 && (uint64_t)T * ldx * es > buffer_limit())
     return fail(MT_ERR_UNSUPPORTED,
-                "bf16 X (T x ldx) and W (V x ldw) must each span at most 4 GiB - 1; split the call "
-                "over row ranges");
+                "bf16 X (T x ldx) spans %llu bytes, beyond the %llu-byte reach of one buffer; "
+                "split the call over row ranges",
+                (unsigned long long)((uint64_t)T * ldx * es), (unsigned long long)buffer_limit());
+  if (es == 2 && (uint64_t)256 * ldw * es > buffer_limit())
+    return fail(MT_ERR_UNSUPPORTED, "bf16 W rows of %lld bytes: 256 of them exceed one buffer's reach",
+                (long long)(ldw * es));
   return MT_OK;
+}
+
+// Vocabulary rows per block of a bf16 weight (a multiple of 256 whose rows
+// fit one buffer's reach; V itself when the whole weight does).
+int64_t vocab_block_rows(int64_t V, int64_t ldw) {
+  const uint64_t lim = buffer_limit();
+  if ((uint64_t)V * ldw * 2 <= lim) return V;
+  return std::max<int64_t>(256, (int64_t)(lim / ((uint64_t)ldw * 2)) / 256 * 256);
+}
+
+// Bytes a kernel may address from `base` when `rows` rows of pitch ld_b
+// follow it (clamped to one buffer's reach; every access is in range by
+// construction, the resource bound backs that up).
+inline uint32_t range_of(int64_t rows, int64_t ld_b) {
+  return (uint32_t)std::min<uint64_t>((uint64_t)std::max<int64_t>(rows, 0) * (uint64_t)ld_b, kMaxBufferBytes);
 }
 
 // Output tiles are 256 x 256 with one workgroup per CU of four waves (bf16
@@ -397,7 +430,11 @@ BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t
       const int64_t Cv = round_up(cdiv(V, nv), 256);
       const size_t ws = backward_ws(C, Cv, H, V, es);
       // G and X^T are read through 32-bit buffer offsets
-      if ((uint64_t)C * Cv * es > kMaxBufferBytes || (uint64_t)H * C * es > kMaxBufferBytes) continue;
+      // G, X^T and the block's weight rows (bf16) within one buffer's reach
+      const uint64_t lim = buffer_limit();
+      if ((uint64_t)C * Cv * es > lim || (uint64_t)H * C * es > lim ||
+          (es == 2 && (uint64_t)Cv * H * es > lim))
+        continue;
       if (ws > budget) continue;
       const double cost = backward_cost(N, H, V, C, Cv, es);
       if (cost < best_cost * 0.999) {
@@ -413,8 +450,8 @@ BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t
 }
 
 template <typename T>
-int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx, int64_t ldw,
-                   float softcap, const int32_t* row_index, const int32_t* row_label,
+int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V, int64_t ldx,
+                   int64_t ldw, float softcap, const int32_t* row_index, const int32_t* row_label,
                    int64_t n_valid, float* loss, float* lse, const FwdPlan& p, char* ws,
                    hipStream_t stream) {
   constexpr int es = sizeof(T);
@@ -426,6 +463,10 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
   a.H = (int32_t)H;
   a.V = (int32_t)V;
   a.N = (int32_t)n_valid;
+  a.vcol0 = 0;
+  a.x_range = range_of(Tn, ldx * es);
+  a.w_range = range_of(V, ldw * es);
+  a.s_range = 0;
   a.row_index = row_index;
   a.row_label = row_label;
   a.softcap = softcap;
@@ -437,27 +478,43 @@ int launch_forward(const void* X, const void* W, int64_t H, int64_t V, int64_t l
   a.xy = reinterpret_cast<float*>(ws + align_up((size_t)p.splits * n_valid * 2 * sizeof(float)));
   a.S = nullptr;
   a.lds_b = 0;
+  const bool ktail = H % (sizeof(T) == 2 ? kBKBf : Elt<float>::kBK) != 0;
   if constexpr (sizeof(T) == 2) {
-    static void (*const kerns[2][2])(FwdArgs) = {
-        {fwd_bf16_kernel<false, false, false>, fwd_bf16_kernel<false, false, true>},
-        {fwd_bf16_kernel<true, false, false>, fwd_bf16_kernel<true, false, true>}};
-    void (*kern)(FwdArgs) = kerns[softcap > 0.f][V % 256 != 0];
-    const int pf = prof_begin("fwd_bf16_kernel", 2.0 * H * (double)V * n_valid, 0, stream);
-    hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * p.vt_total)), dim3(kThreadsBf), 0,
-                       stream, a);
-    prof_end(pf, stream);
+    // vocabulary blocks of at most one buffer's reach; each writes the
+    // partials of its own tiles, the finalize merges them all
+    static void (*const kerns[2][2][2])(FwdArgs) = {
+        {{fwd_bf16_kernel<false, false, false, false>, fwd_bf16_kernel<false, false, false, true>},
+         {fwd_bf16_kernel<false, false, true, false>, fwd_bf16_kernel<false, false, true, true>}},
+        {{fwd_bf16_kernel<true, false, false, false>, fwd_bf16_kernel<true, false, false, true>},
+         {fwd_bf16_kernel<true, false, true, false>, fwd_bf16_kernel<true, false, true, true>}}};
+    const int64_t vb = vocab_block_rows(V, ldw);
+    for (int64_t v0 = 0; v0 < V; v0 += vb) {
+      const int64_t vn = std::min(vb, V - v0);
+      a.W = static_cast<const char*>(W) + v0 * ldw * es;
+      a.V = (int32_t)vn;
+      a.vcol0 = (int32_t)v0;
+      a.w_range = range_of(vn, ldw * es);
+      a.vt_total = (int32_t)cdiv(vn, geometry(es).tile_n);
+      void (*kern)(FwdArgs) = kerns[softcap > 0.f][vn % 256 != 0][ktail];
+      const int pf = prof_begin("fwd_bf16_kernel", 2.0 * H * (double)vn * n_valid, 0, stream);
+      hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * a.vt_total)), dim3(kThreadsBf), 0,
+                         stream, a);
+      prof_end(pf, stream);
+      MT_TRY(check_launch("fwd_bf16_kernel"));
+    }
   } else {
-    hipLaunchKernelGGL(fwd_kernel<T>, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0,
-                       stream, a);
+    void (*kern)(FwdArgs) = ktail ? fwd_kernel<T, true> : fwd_kernel<T, false>;
+    hipLaunchKernelGGL(kern, dim3((uint32_t)(p.tiles_m * p.splits)), dim3(kThreads), 0, stream, a);
+    MT_TRY(check_launch("fwd_kernel"));
   }
-  MT_TRY(check_launch("fwd_kernel"));
   hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(n_valid, 4)), dim3(256), 0, stream,
                      a.part, a.xy, a.N, a.splits, row_index, loss, lse);
   return check_launch("fwd_finalize_kernel");
 }
 
 template <typename T>
-int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx, int64_t ldw,
+int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V, int64_t ldx,
+                    int64_t ldw,
                     float softcap, const int32_t* row_index, const int32_t* row_label,
                     int64_t N, const float* lse, const float* grad, int64_t gstride, void* dX,
                     int64_t lddx, float* dW, int64_t lddw, int accumulate, int64_t C, int64_t Cv,
@@ -481,13 +538,18 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
     int64_t j = 0;
     for (int64_t v0 = 0; v0 < V; v0 += Cv, ++j) {
       const int64_t cv = std::min(Cv, V - v0);
+      // the block's weight rows start at v0 (W rebased: 32-bit offsets)
+      const char* Wv = static_cast<const char*>(W) + v0 * ldw * es;
       RecompArgs r;
       r.X = static_cast<const char*>(X);
-      r.W = static_cast<const char*>(W);
+      r.W = Wv;
       r.ldx_b = ldx * es;
       r.ldw_b = ldw * es;
       r.H = (int32_t)H;
       r.V = (int32_t)V;
+      r.x_range = range_of(Tn, ldx * es);
+      r.w_range = range_of(cv, ldw * es);
+      r.g_range = range_of(round_up(cn, 256), ldg_b);
       r.row_index = row_index + c0;
       r.row_label = row_label + c0;
       r.lse = lse + c0;
@@ -502,25 +564,31 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
       if constexpr (sizeof(T) == 2) {
-        static void (*const kerns[2][2])(RecompArgs) = {
-            {recompute_bf16_kernel<false, false>, recompute_bf16_kernel<false, true>},
-            {recompute_bf16_kernel<true, false>, recompute_bf16_kernel<true, true>}};
+        static void (*const kerns[2][2][2])(RecompArgs) = {
+            {{recompute_bf16_kernel<false, false, false>, recompute_bf16_kernel<false, false, true>},
+             {recompute_bf16_kernel<false, true, false>, recompute_bf16_kernel<false, true, true>}},
+            {{recompute_bf16_kernel<true, false, false>, recompute_bf16_kernel<true, false, true>},
+             {recompute_bf16_kernel<true, true, false>, recompute_bf16_kernel<true, true, true>}}};
         const int pr = prof_begin("recompute_bf16_kernel", 2.0 * H * (double)cn * cv, 0, stream);
-        hipLaunchKernelGGL(kerns[softcap > 0.f][cv % 256 != 0],
+        hipLaunchKernelGGL(kerns[softcap > 0.f][cv % 256 != 0][H % kBKBf != 0],
                            dim3(persistent_grid(r.tiles_m * r.tiles_n)),
                            dim3(kThreadsBf), 0, stream, r);
         prof_end(pr, stream);
-      } else
-        hipLaunchKernelGGL(recompute_kernel<T>, dim3((uint32_t)(r.tiles_m * r.tiles_n)),
-                           dim3(kThreads), 0, stream, r);
+      } else {
+        void (*kern)(RecompArgs) =
+            H % Elt<float>::kBK != 0 ? recompute_kernel<T, true> : recompute_kernel<T, false>;
+        hipLaunchKernelGGL(kern, dim3((uint32_t)(r.tiles_m * r.tiles_n)), dim3(kThreads), 0, stream, r);
+      }
       MT_TRY(check_launch("recompute_kernel"));
 
       DxArgs x;
       x.G = G;
       x.ldg_b = ldg_b;
-      x.W = static_cast<const char*>(W);
+      x.W = Wv;
       x.ldw_b = ldw * es;
-      x.V = (int32_t)V;
+      x.g_range = r.g_range;
+      x.w_range = r.w_range;
+      x.V = (int32_t)(v0 + cv);  // K rows past the block's end repeat its last row (times zero G)
       x.v0 = (int32_t)v0;
       x.kv = (int32_t)cv;
       x.H = (int32_t)H;
@@ -560,6 +628,8 @@ int launch_backward(const void* X, const void* W, int64_t H, int64_t V, int64_t 
       w.g_cols = (int32_t)Cv;
       w.XcT = XcT;
       w.ldxt_b = ldxt_b;
+      w.g_range = r.g_range;
+      w.xt_range = range_of(H, ldxt_b);
       w.kt_rows = (int32_t)cn;
       w.H = (int32_t)H;
       w.cv = (int32_t)cv;
@@ -610,11 +680,15 @@ size_t fused_ws(int64_t C, int64_t H, int64_t V) {
 FusedPlan plan_fused(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) {
   FusedPlan p;
   if (N <= 0) return p;
+  // the fused dX contracts over the whole vocabulary in one launch: the
+  // weight must lie within one buffer's reach (else the general path, which
+  // takes it in vocabulary blocks)
+  if ((uint64_t)V * H * 2 > buffer_limit()) return p;
   if (budget == 0) budget = (size_t)((double)T * V * 2 * 0.05);
   int64_t best = 256;
   for (int64_t C = 256; C <= round_up(N, 256); C += 256) {
     if (fused_ws(C, H, V) > budget) break;
-    if ((uint64_t)C * vocab_pad(V) * 2 > kMaxBufferBytes || (uint64_t)H * C * 2 > kMaxBufferBytes) break;
+    if ((uint64_t)C * vocab_pad(V) * 2 > buffer_limit() || (uint64_t)H * C * 2 > buffer_limit()) break;
     best = C;
   }
   // equal chunks: same number of chunks, the smallest 256-multiple that covers N
@@ -635,7 +709,8 @@ bool fused_pays(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) {
   return fused_cost(N, H, V, f.C) < 0.97 * (forward_cost(N, H, V) + backward_cost(N, H, V, b.C, b.Cv, 2));
 }
 
-int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx, int64_t ldw,
+int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V, int64_t ldx,
+                 int64_t ldw,
                  float softcap, const int32_t* row_index, const int32_t* row_label, int64_t N,
                  const float* grad, int64_t gstride, float* loss, float* lse, void* dX,
                  int64_t lddx, float* dW, int64_t lddw, int accumulate, int64_t C, char* ws,
@@ -663,6 +738,10 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     a.H = (int32_t)H;
     a.V = (int32_t)V;
     a.N = (int32_t)cn;
+    a.vcol0 = 0;
+    a.x_range = range_of(Tn, ldx * 2);
+    a.w_range = range_of(V, ldw * 2);
+    a.s_range = range_of(C, lds_b);
     a.row_index = row_index + c0;
     a.row_label = row_label + c0;
     a.softcap = softcap;
@@ -674,10 +753,12 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     a.xy = xy;
     a.S = S;
     a.lds_b = lds_b;
-    static void (*const kerns[2][2])(FwdArgs) = {
-        {fwd_bf16_kernel<false, true, false>, fwd_bf16_kernel<false, true, true>},
-        {fwd_bf16_kernel<true, true, false>, fwd_bf16_kernel<true, true, true>}};
-    void (*kern)(FwdArgs) = kerns[softcap > 0.f][V % 256 != 0];
+    static void (*const kerns[2][2][2])(FwdArgs) = {
+        {{fwd_bf16_kernel<false, true, false, false>, fwd_bf16_kernel<false, true, false, true>},
+         {fwd_bf16_kernel<false, true, true, false>, fwd_bf16_kernel<false, true, true, true>}},
+        {{fwd_bf16_kernel<true, true, false, false>, fwd_bf16_kernel<true, true, false, true>},
+         {fwd_bf16_kernel<true, true, true, false>, fwd_bf16_kernel<true, true, true, true>}}};
+    void (*kern)(FwdArgs) = kerns[softcap > 0.f][V % 256 != 0][H % kBKBf != 0];
     const int pf = prof_begin("fwd_bf16_kernel<store_s>", 2.0 * H * (double)V * cn, 0, stream);
     hipLaunchKernelGGL(kern, dim3(persistent_grid(tm * vt)), dim3(kThreadsBf), 0, stream, a);
     prof_end(pf, stream);
@@ -698,6 +779,8 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     x.ldg_b = lds_b;
     x.W = static_cast<const char*>(W);
     x.ldw_b = ldw * 2;
+    x.g_range = a.s_range;
+    x.w_range = a.w_range;
     x.V = (int32_t)V;
     x.v0 = 0;
     x.kv = (int32_t)V;
@@ -718,6 +801,8 @@ int launch_fused(const void* X, const void* W, int64_t H, int64_t V, int64_t ldx
     w.g_cols = (int32_t)Vp;
     w.XcT = XcT;
     w.ldxt_b = ldxt_b;
+    w.g_range = a.s_range;
+    w.xt_range = range_of(H, ldxt_b);
     w.kt_rows = (int32_t)cn;
     w.H = (int32_t)H;
     w.cv = (int32_t)V;
@@ -785,9 +870,9 @@ int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H, int64_t 
   }
   if (n_valid == 0) return MT_OK;
   if (dtype == MT_DTYPE_BF16)
-    return launch_forward<__bf16>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid,
+    return launch_forward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid,
                                   loss, lse, p, static_cast<char*>(workspace), s);
-  return launch_forward<float>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, loss,
+  return launch_forward<float>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, loss,
                                lse, p, static_cast<char*>(workspace), s);
 }
 
@@ -846,6 +931,8 @@ extern "C" {
 
 size_t mt_flce_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
+uint64_t mt_flce_max_buffer_bytes(void) { return buffer_limit(); }
+
 int mt_flce_forward_noalloc(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
                             int64_t ldx, int64_t ldw, int dtype, float softcap,
                             const int32_t* row_index, const int32_t* row_label, int64_t n_valid,
@@ -878,10 +965,10 @@ int mt_flce_forward_noalloc(const void* X, const void* W, int64_t T, int64_t H, 
     const int64_t cn = std::min(rows, n_valid - c0);
     const FwdPlan p = plan_forward(cn, V, es);
     if (dtype == MT_DTYPE_BF16)
-      MT_TRY(launch_forward<__bf16>(X, W, H, V, ldx, ldw, softcap, row_index + c0, row_label + c0,
+      MT_TRY(launch_forward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index + c0, row_label + c0,
                                     cn, loss, lse + c0, p, ws, s));
     else
-      MT_TRY(launch_forward<float>(X, W, H, V, ldx, ldw, softcap, row_index + c0, row_label + c0,
+      MT_TRY(launch_forward<float>(X, W, T, H, V, ldx, ldw, softcap, row_index + c0, row_label + c0,
                                    cn, loss, lse + c0, p, ws, s));
   }
   return MT_OK;
@@ -930,9 +1017,12 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
       return fail(MT_ERR_INVALID_ARGUMENT,
                   "chunk_rows=%lld / chunk_vocab=%lld must be positive multiples of 256",
                   (long long)chunk_rows, (long long)chunk_vocab);
-    if (es == 2 && ((uint64_t)chunk_rows * chunk_vocab * 2 > kMaxBufferBytes ||
-                    (uint64_t)H * chunk_rows * 2 > kMaxBufferBytes))
-      return fail(MT_ERR_UNSUPPORTED, "chunk_rows=%lld x chunk_vocab=%lld: G block or X^T beyond 4 GiB",
+    if (es == 2 && ((uint64_t)chunk_rows * chunk_vocab * 2 > buffer_limit() ||
+                    (uint64_t)H * chunk_rows * 2 > buffer_limit() ||
+                    (uint64_t)chunk_vocab * ldw * 2 > buffer_limit()))
+      return fail(MT_ERR_UNSUPPORTED,
+                  "chunk_rows=%lld x chunk_vocab=%lld: G block, X^T or the block's weight rows beyond "
+                  "one buffer's reach (4 GiB, or MT_FLCE_MAX_BUFFER_BYTES)",
                   (long long)chunk_rows, (long long)chunk_vocab);
     const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es);
     if (workspace_bytes < need || !workspace)
@@ -955,10 +1045,10 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
     return MT_OK;
   }
   if (dtype == MT_DTYPE_BF16)
-    return launch_backward<__bf16>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
+    return launch_backward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                    grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW,
                                    chunk_rows, chunk_vocab, static_cast<char*>(workspace), s);
-  return launch_backward<float>(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
+  return launch_backward<float>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                 grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, chunk_rows,
                                 chunk_vocab, static_cast<char*>(workspace), s);
 }
@@ -989,6 +1079,10 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "the fused path is bf16 only (dtype %d)", dtype);
   MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
+  if ((uint64_t)V * ldw * 2 > buffer_limit())
+    return fail(MT_ERR_UNSUPPORTED,
+                "the fused path needs W (V x ldw bf16) within one buffer's reach (4 GiB, or "
+                "MT_FLCE_MAX_BUFFER_BYTES); use mt_flce_forward + mt_flce_backward");
   if (n_valid < 0 || n_valid > T)
     return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
   if (lddx < H || lddw < H)
@@ -1006,9 +1100,10 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
     if (chunk_rows <= 0 || chunk_rows % 256 != 0)
       return fail(MT_ERR_INVALID_ARGUMENT, "chunk_rows=%lld must be a positive multiple of 256",
                   (long long)chunk_rows);
-    if ((uint64_t)chunk_rows * vocab_pad(V) * 2 > kMaxBufferBytes ||
-        (uint64_t)H * chunk_rows * 2 > kMaxBufferBytes)
-      return fail(MT_ERR_UNSUPPORTED, "chunk_rows=%lld: logits chunk or X^T beyond 4 GiB",
+    if ((uint64_t)chunk_rows * vocab_pad(V) * 2 > buffer_limit() ||
+        (uint64_t)H * chunk_rows * 2 > buffer_limit())
+      return fail(MT_ERR_UNSUPPORTED,
+                  "chunk_rows=%lld: logits chunk or X^T beyond one buffer's reach (4 GiB)",
                   (long long)chunk_rows);
     const size_t need = fused_ws(chunk_rows, H, V);
     if (workspace_bytes < need || !workspace)
@@ -1033,7 +1128,7 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
     }
     return MT_OK;
   }
-  return launch_fused(X, W, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, grad_loss,
+  return launch_fused(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, grad_loss,
                       grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, chunk_rows,
                       static_cast<char*>(workspace), s);
 }
@@ -1096,10 +1191,13 @@ int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H, int6
   if (!scale) return fail(MT_ERR_INVALID_ARGUMENT, "null scale");
   if ((T > 0 && (!dX || lddx < H)) || (V > 0 && (!dW || !dW_out || lddw < H || ldo < H)))
     return fail(MT_ERR_INVALID_ARGUMENT, "null pointer or leading dimension below H");
+  // dX and fp32 rows go in 16-byte vectors, bf16 output rows in 8-byte ones
   if ((reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(dW) |
        reinterpret_cast<uintptr_t>(dW_out)) % 16 != 0 ||
-      (lddx * esx) % 16 != 0 || (lddw * 4) % 16 != 0 || (ldo * eso) % 16 != 0)
-    return fail(MT_ERR_INVALID_ARGUMENT, "dX / dW / dW_out must be 16-byte aligned with 16-byte row pitches");
+      (lddx * esx) % 16 != 0 || (lddw * 4) % 16 != 0 || (ldo * eso) % (eso == 2 ? 8 : 16) != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "dX / dW / dW_out must be 16-byte aligned, with 16-byte row pitches (8 for a bf16 "
+                "dW_out)");
   if (dW_out == dW && ldo != lddw)
     return fail(MT_ERR_INVALID_ARGUMENT, "in-place dW scaling needs ldo == lddw");
   if (dW_out == dW && eso == 2 && H > kMaxNarrowCols)

@@ -21,6 +21,7 @@ __device__ __forceinline__ uint32_t wave_id() {
 // ---------------------------------------------------------------------------
 struct DirectLoader {
   const char* p[8];
+  uint32_t tail_bad;  // bit i: load i's chunk lies past K in the last stage
 
   // Tile row handled by load instruction i of this lane.
   __device__ __forceinline__ static uint32_t row_of(uint32_t i) {
@@ -46,6 +47,24 @@ struct DirectLoader {
     for (uint32_t i = 0; i < 8; ++i) {
       __builtin_amdgcn_global_load_lds(p[i] + koff, (lds_void_t*)(lds_tile + (w * 8 + i) * 1024u),
                                        16, 0, 0);
+    }
+  }
+  // c_lim: 16-byte chunks of the last K stage that lie below K.
+  __device__ __forceinline__ void set_tail(uint32_t c_lim) {
+    uint32_t m = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) m |= (chunk_of(i) >= c_lim ? 1u : 0u) << i;
+    tail_bad = m;
+  }
+  // The last (partial) K stage: chunks past K re-read chunk 0 of their row
+  // (in bounds); the fragments holding them are zeroed after the LDS read.
+  __device__ __forceinline__ void issue_tail(char* lds_tile, int kt) const {
+    const uint32_t w = wave_id();
+    const int64_t koff = (int64_t)kt * kRowBytes;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      const char* src = ((tail_bad >> i) & 1u) ? p[i] - chunk_of(i) * 16u : p[i] + koff;
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(lds_tile + (w * 8 + i) * 1024u), 16, 0, 0);
     }
   }
   __device__ __forceinline__ void commit(char*) {}
@@ -153,9 +172,12 @@ struct FragOffsets {
   }
 };
 
+// tail: the stage's 16-byte chunks at or past c_lim lie past K; lane l holds
+// chunk kk * 4 + (l >> 4), zeroed in both operands when it does.
 template <typename T>
 __device__ __forceinline__ void compute_stage(const char* ldsA, const char* ldsB,
-                                              f32x4_t (&acc)[8][8], const FragOffsets& fo) {
+                                              f32x4_t (&acc)[8][8], const FragOffsets& fo,
+                                              bool tail = false, uint32_t c_lim = 8) {
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
     u32x4_t a[8], b[8];
@@ -163,6 +185,13 @@ __device__ __forceinline__ void compute_stage(const char* ldsA, const char* ldsB
     for (int f = 0; f < 8; ++f) a[f] = lds_read16(ldsA, fo.a[kk] + f * 2048u);
 #pragma unroll
     for (int f = 0; f < 8; ++f) b[f] = lds_read16(ldsB, fo.b[kk] + f * 2048u);
+    if (tail && (uint32_t)kk * 4u + (lane_id() >> 4) >= c_lim) {
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        a[f] = u32x4_t{0u, 0u, 0u, 0u};
+        b[f] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm)
 #pragma unroll
@@ -171,17 +200,29 @@ __device__ __forceinline__ void compute_stage(const char* ldsA, const char* ldsB
 }
 
 // C_tile[256 x 256] = sum over KT slabs of A_tile * B_tile^T, fp32 in acc.
-template <typename T, class LA, class LB>
+// kKTail (both loaders DirectLoader): the last slab holds only c_lim of its
+// 8 chunks below K (DirectLoader::issue_tail, compute_stage's mask).
+template <typename T, bool kKTail = false, class LA, class LB>
 __device__ __forceinline__ void mainloop(char* lds, f32x4_t (&acc)[8][8], LA& la, LB& lb, int KT,
-                                         const FragOffsets& fo) {
+                                         const FragOffsets& fo, uint32_t c_lim = 8) {
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm)
 #pragma unroll
     for (int fn = 0; fn < 8; ++fn) acc[fm][fn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   if (KT <= 0) return;
 
-  la.issue(lds, 0);
-  lb.issue(lds + kTileBytes, 0);
+  if constexpr (kKTail) {
+    if (KT == 1) {
+      la.issue_tail(lds, 0);
+      lb.issue_tail(lds + kTileBytes, 0);
+    } else {
+      la.issue(lds, 0);
+      lb.issue(lds + kTileBytes, 0);
+    }
+  } else {
+    la.issue(lds, 0);
+    lb.issue(lds + kTileBytes, 0);
+  }
   la.commit(lds);
   lb.commit(lds + kTileBytes);
   __builtin_amdgcn_s_waitcnt(0);
@@ -192,10 +233,17 @@ __device__ __forceinline__ void mainloop(char* lds, f32x4_t (&acc)[8][8], LA& la
     char* nxt = lds + ((kt + 1) & 1) * kStageBytes;
     const bool more = kt + 1 < KT;
     if (more) {
-      la.issue(nxt, kt + 1);
-      lb.issue(nxt + kTileBytes, kt + 1);
+      if (kKTail && kt + 1 == KT - 1) {
+        if constexpr (kKTail) {
+          la.issue_tail(nxt, kt + 1);
+          lb.issue_tail(nxt + kTileBytes, kt + 1);
+        }
+      } else {
+        la.issue(nxt, kt + 1);
+        lb.issue(nxt + kTileBytes, kt + 1);
+      }
     }
-    compute_stage<T>(cur, cur + kTileBytes, acc, fo);
+    compute_stage<T>(cur, cur + kTileBytes, acc, fo, kKTail && kt == KT - 1, c_lim);
     if (more) {
       la.commit(nxt);
       lb.commit(nxt + kTileBytes);

@@ -120,7 +120,6 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
-constexpr uint32_t kWholeRange = 0xffffffffu;
 
 // 16-byte LDS DMA of one lane: LDS[dst + 16 lane] = mem[rsrc + voff + soff].
 __device__ __forceinline__ void dma16(rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
@@ -136,6 +135,7 @@ struct KcOp {
   rsrc_t rsrc;
   uint32_t off[kNIBf];
   uint32_t frag[2];  // LDS offset of this lane's fragment 0 for K halves 0, 1
+  uint32_t tail_bad;  // bit i: DMA instruction i's chunk lies past K in the last stage
 
   __device__ __forceinline__ static uint32_t row_of(uint32_t i) {
     const uint32_t l = lane_id(), q = wave_id() * kNIBf + i;
@@ -152,6 +152,13 @@ struct KcOp {
 #pragma unroll
     for (uint32_t i = 0; i < kNIBf; ++i) off[i] = row_off(row_of(i)) + chunk_of(i) * 16u;
   }
+  // c_lim: 16-byte chunks (of 8) of the last K stage that lie below K.
+  __device__ __forceinline__ void set_tail(uint32_t c_lim) {
+    uint32_t m = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kNIBf; ++i) m |= (chunk_of(i) >= c_lim ? 1u : 0u) << i;
+    tail_bad = m;
+  }
   // wave_row0: first tile row of this wave's fragments.
   __device__ __forceinline__ void init_frag(uint32_t wave_row0) {
     const uint32_t l = lane_id();
@@ -166,10 +173,33 @@ struct KcOp {
 #pragma unroll
     for (int i = 0; i < kNIBf; ++i) issue_one(tile, kt, i);
   }
+  // The same with a possibly partial last K stage (tail: kt is that stage):
+  // chunks past K re-read chunk 0 of their row, which is in bounds, and the
+  // fragments holding them are zeroed after they are read (mask_tail), so no
+  // byte past a row's K extent -- past the end of the array for its last
+  // row -- is touched.  Branch-free: the choice is a select on the offsets.
+  __device__ __forceinline__ void issue_one_k(char* tile, int kt, int i, bool tail) const {
+    const bool bad = tail && ((tail_bad >> i) & 1u);
+    const uint32_t voff = bad ? off[i] - chunk_of(i) * 16u : (tail ? off[i] + (uint32_t)kt * 128u : off[i]);
+    dma16(rsrc, tile + (wave_id() * kNIBf + (uint32_t)i) * 1024u, voff, tail ? 0u : (uint32_t)kt * 128u);
+  }
+  __device__ __forceinline__ void issue_k(char* tile, int kt, bool tail) const {
+#pragma unroll
+    for (int i = 0; i < kNIBf; ++i) issue_one_k(tile, kt, i, tail);
+  }
   __device__ __forceinline__ u32x4_t read(const char* tile, int kk, int f) const {
     return lds_read16(tile, frag[kk] + (uint32_t)f * 2048u);
   }
 };
+
+// Zero the fragments of K half kk of the last (partial) K stage in the lanes
+// whose 8 K values lie at or past K: lane l holds K chunk kk * 4 + (l >> 4)
+// of the stage, and the stage's first c_lim chunks lie below K.
+__device__ __forceinline__ void mask_tail(u32x4_t (&fr)[8], int kk, uint32_t c_lim) {
+  const bool bad = (uint32_t)kk * 4u + (lane_id() >> 4) >= c_lim;
+#pragma unroll
+  for (int f = 0; f < 8; ++f) fr[f] = bad ? u32x4_t{0u, 0u, 0u, 0u} : fr[f];
+}
 
 // Operand stored K-major: row-major [K, 256-column tile].  Instruction q of
 // the tile covers K rows 2 q and 2 q + 1; lane l writes LDS chunk l & 31 of
@@ -291,9 +321,14 @@ __device__ __forceinline__ void wait_vm8() {
 // Each phase is one basic block: the retarget branch sits before phase 1,
 // and every phase issues its DMA -- the two stages past the end reload the
 // last tile's final stage into slots that are never read again.
-template <bool kThreeA, class A, class B, class Retarget, class Epi, class Init = ZeroInit>
+// kKTail (both operands KcOp, K contiguous in their rows): the last K stage
+// holds only c_lim of its 8 chunks below K; its DMA keeps to the rows' K
+// extent and its fragments are masked (KcOp::issue_one_k, mask_tail).
+template <bool kThreeA, bool kKTail = false, class A, class B, class Retarget, class Epi,
+          class Init = ZeroInit>
 __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int ntiles,
-                                              Retarget retarget, Epi epilogue, Init init = Init()) {
+                                              Retarget retarget, Epi epilogue, Init init = Init(),
+                                              uint32_t c_lim = 8) {
   if (KT <= 0 || ntiles <= 0) return;
   // (tile2, kt2) = coordinates of stage g + 2, the next stage to be loaded;
   // they stop at the last stage of the last tile
@@ -316,12 +351,29 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
   auto slot_b = [&](int s2, int s3) __attribute__((always_inline)) {
     return kThreeA ? two0 + s2 * kTileBf : three0 + s3 * kTileBf;
   };
+  // DMA of stage kt2 of the current tile: the last stage may be partial
+  auto issue_a = [&](char* dst, int kt) __attribute__((always_inline)) {
+    if constexpr (kKTail) a.issue_k(dst, kt, kt == KT - 1);
+    else a.issue(dst, kt);
+  };
+  auto issue_b = [&](char* dst, int kt) __attribute__((always_inline)) {
+    if constexpr (kKTail) b.issue_k(dst, kt, kt == KT - 1);
+    else b.issue(dst, kt);
+  };
+  auto issue_one_a = [&](char* dst, int kt, int i) __attribute__((always_inline)) {
+    if constexpr (kKTail) a.issue_one_k(dst, kt, i, kt == KT - 1);
+    else a.issue_one(dst, kt, i);
+  };
+  auto issue_one_b = [&](char* dst, int kt, int i) __attribute__((always_inline)) {
+    if constexpr (kKTail) b.issue_one_k(dst, kt, i, kt == KT - 1);
+    else b.issue_one(dst, kt, i);
+  };
   retarget(0);
-  a.issue(slot_a(0, 0), kt2);
-  b.issue(slot_b(0, 0), kt2);
+  issue_a(slot_a(0, 0), kt2);
+  issue_b(slot_b(0, 0), kt2);
   advance();
-  a.issue(slot_a(1, 1), kt2);
-  b.issue(slot_b(1, 1), kt2);
+  issue_a(slot_a(1, 1), kt2);
+  issue_b(slot_b(1, 1), kt2);
   wait_vm0();
   __builtin_amdgcn_s_barrier();
   u32x4_t fa0[8], fb0[8], fa1[8], fb1[8];
@@ -339,6 +391,12 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
     init(tile, acc);
     for (int kt = 0; kt < KT; ++kt, ++g, g3 = (g3 == 2 ? 0 : g3 + 1)) {
       advance();
+      if constexpr (kKTail) {
+        if (kt == KT - 1) {
+          mask_tail(fa0, 0, c_lim);
+          mask_tail(fb0, 0, c_lim);
+        }
+      }
       sched_fence();
       const int g2 = g & 1, g2n = g2 ^ 1;
       const int g3n = g3 == 2 ? 0 : g3 + 1, g3p = g3 == 0 ? 2 : g3 - 1;  // (g+1)%3, (g+2)%3
@@ -354,8 +412,8 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
         if (i & 1) fb1[i >> 1] = b.read(rb, 1, i >> 1);
         else fa1[i >> 1] = a.read(ra, 1, i >> 1);
         if (i & 1) {
-          if (kThreeA) a.issue_one(w3, kt2, i >> 1);
-          else b.issue_one(w3, kt2, i >> 1);
+          if (kThreeA) issue_one_a(w3, kt2, i >> 1);
+          else issue_one_b(w3, kt2, i >> 1);
         }
         sched_fence();
       }
@@ -369,6 +427,12 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
       tie_frags<B>(fb1);
       wait_vm8();
       __builtin_amdgcn_s_barrier();
+      if constexpr (kKTail) {
+        if (kt == KT - 1) {
+          mask_tail(fa1, 1, c_lim);
+          mask_tail(fb1, 1, c_lim);
+        }
+      }
       sched_fence();
       // phase 2: MFMAs on F1(g), DMA of the two-slot operand's stage g + 2
       // into the slot of its stage g, LDS reads of F0(g + 1) (stale after the
@@ -381,8 +445,8 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
 #pragma unroll
         for (int j = 0; j < kMpg; ++j) mfma_one(acc, fa1, fb1, kMpg * i + j);
         if (i & 1) {
-          if (kThreeA) b.issue_one(w2, kt2, i >> 1);
-          else a.issue_one(w2, kt2, i >> 1);
+          if (kThreeA) issue_one_b(w2, kt2, i >> 1);
+          else issue_one_a(w2, kt2, i >> 1);
         }
         if (i & 1) fb0[i >> 1] = b.read(rb1, 0, i >> 1);
         else fa0[i >> 1] = a.read(ra1, 0, i >> 1);

@@ -56,9 +56,11 @@ __device__ __forceinline__ bool lane_holds(int rel) {
 // ===========================================================================
 struct FwdArgs {
   const char* X;
-  const char* W;
+  const char* W;  // vocabulary row vcol0 of the weight
   int64_t ldx_b, ldw_b;
-  int32_t H, V, N;
+  int32_t H, V, N;  // V: vocabulary rows from W on (this launch's block)
+  int32_t vcol0;    // global vocabulary index of W's row 0 (a multiple of 256)
+  uint32_t x_range, w_range, s_range;  // bytes addressable from X, W, S
   const int32_t* row_index;
   const int32_t* row_label;
   float softcap;
@@ -177,7 +179,8 @@ __device__ __forceinline__ void fwd_final_merge(char* lds, float (&m2)[8], float
   }
 }
 
-template <typename T>
+// kKTail: H is not a multiple of the K slab (the last slab is partial).
+template <typename T, bool kKTail>
 MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   uint32_t tm, ts;
@@ -204,7 +207,9 @@ MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
     d[fm] = 0.f;
   }
 
-  const int KT = a.H / Elt<T>::kBK;
+  const int KT = (a.H + Elt<T>::kBK - 1) / Elt<T>::kBK;
+  const uint32_t c_lim = (uint32_t)(a.H - (KT - 1) * Elt<T>::kBK) / Elt<T>::kPerChunk;
+  if constexpr (kKTail) la.set_tail(c_lim);
   const int vt0 = (int)ts * a.vt_per_split;
   const int vt1 = min(vt0 + a.vt_per_split, a.vt_total);
   f32x4_t acc[8][8];
@@ -216,7 +221,8 @@ MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
       v = v < a.V ? v : a.V - 1;
       return a.W + (int64_t)v * a.ldw_b;
     });
-    mainloop<T>(lds, acc, la, lb, KT, fo);
+    if constexpr (kKTail) lb.set_tail(c_lim);
+    mainloop<T, kKTail>(lds, acc, la, lb, KT, fo, c_lim);
 
     if (a.softcap > 0.f) fwd_tile_update<T, true>(acc, m2, d, lbl, rglob, vrow0, ec, a);
     else fwd_tile_update<T, false>(acc, m2, d, lbl, rglob, vrow0, ec, a);
@@ -251,9 +257,10 @@ __global__ __launch_bounds__(256) void fwd_finalize_kernel(const float* part, co
 // ===========================================================================
 struct RecompArgs {
   const char* X;
-  const char* W;
+  const char* W;  // vocabulary row v0 of the weight (the block's first row)
   int64_t ldx_b, ldw_b;
   int32_t H, V;
+  uint32_t x_range, w_range, g_range;  // bytes addressable from X, W, G
   const int32_t* row_index;  // offset to the block's first valid row
   const int32_t* row_label;
   const float* lse;
@@ -330,7 +337,7 @@ __device__ __forceinline__ void recompute_epilogue(const f32x4_t (&acc)[8][NFN],
   }
 }
 
-template <typename T>
+template <typename T, bool kKTail>
 MT_GEMM_KERNEL void recompute_kernel(RecompArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   uint32_t tm, tn;
@@ -345,15 +352,21 @@ MT_GEMM_KERNEL void recompute_kernel(RecompArgs a) {
     rr = rr < a.Cn ? rr : a.Cn - 1;
     return a.X + (int64_t)a.row_index[rr] * a.ldx_b;
   });
-  const int32_t vrow0 = a.v0 + (int32_t)tn * 256;
+  const int32_t vloc0 = (int32_t)tn * 256;  // rows from the block's first (W's row 0)
   DirectLoader lb;
   lb.init([&](uint32_t r) __attribute__((always_inline)) {
-    int32_t v = vrow0 + (int32_t)r;
-    v = v < a.V ? v : a.V - 1;
+    int32_t v = vloc0 + (int32_t)r;
+    v = v < a.cv ? v : a.cv - 1;  // rows past the block repeat its last one
     return a.W + (int64_t)v * a.ldw_b;
   });
   f32x4_t acc[8][8];
-  mainloop<T>(lds, acc, la, lb, a.H / Elt<T>::kBK, fo);
+  const int KT = (a.H + Elt<T>::kBK - 1) / Elt<T>::kBK;
+  const uint32_t c_lim = (uint32_t)(a.H - (KT - 1) * Elt<T>::kBK) / Elt<T>::kPerChunk;
+  if constexpr (kKTail) {
+    la.set_tail(c_lim);
+    lb.set_tail(c_lim);
+  }
+  mainloop<T, kKTail>(lds, acc, la, lb, KT, fo, c_lim);
   if (a.softcap > 0.f) recompute_epilogue<T, 8, true>(acc, a, ec, row0, (int32_t)tn * 256);
   else recompute_epilogue<T, 8, false>(acc, a, ec, row0, (int32_t)tn * 256);
 }
@@ -366,8 +379,9 @@ enum DxMode : int32_t { kDxStore = 0, kDxAdd = 1, kDxAddEmit = 2, kDxEmit = 3 };
 struct DxArgs {
   const char* G;
   int64_t ldg_b;
-  const char* W;
+  const char* W;  // vocabulary row v0 of the weight (the block's first row)
   int64_t ldw_b;
+  uint32_t g_range, w_range;  // bytes addressable from G, W
   int32_t V, v0, kv;  // K = vocabulary entries v0 .. v0 + kv
   int32_t H, Cn;
   float* accbuf;  // fp32 [>= Cn][ld_acc]
@@ -420,8 +434,7 @@ MT_GEMM_KERNEL void dx_kernel(DxArgs a) {
   la.init([&](uint32_t r) __attribute__((always_inline)) { return a.G + (int64_t)(row0 + (int32_t)r) * a.ldg_b; });
   const int32_t h0 = (int32_t)tn * 256;
   TransLoader<T> lb;
-  lb.init(a.W + (int64_t)a.v0 * a.ldw_b + (int64_t)h0 * Elt<T>::kBytes, a.ldw_b, a.V - a.v0,
-          a.H - h0);
+  lb.init(a.W + (int64_t)h0 * Elt<T>::kBytes, a.ldw_b, a.V - a.v0, a.H - h0);
   f32x4_t acc[8][8];
   const int KT = (a.kv + Elt<T>::kBK - 1) / Elt<T>::kBK;
   mainloop<T>(lds, acc, la, lb, KT, fo);
@@ -438,6 +451,7 @@ struct DwArgs {
   int32_t g_cols;  // columns of G that exist
   const char* XcT;  // [H][K] gathered + transposed X rows of the block
   int64_t ldxt_b;
+  uint32_t g_range, xt_range;  // bytes addressable from G, XcT
   int32_t kt_rows;  // K extent (valid rows of the block)
   int32_t H, cv, v0;
   float* dW;

@@ -71,7 +71,10 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
                                                   float (&d)[8], const int32_t (&lbl)[8],
                                                   const int32_t (&rglob)[8], int32_t vrow0,
                                                   const EpiCoordsBf& ec, const FwdArgs& a) {
-  const int32_t ncol0 = vrow0 + ec.col(0);
+  // vrow0: the tile's first column from W's row 0; labels and S columns are
+  // global vocabulary indices (a.vcol0 + local)
+  const int32_t lcol0 = vrow0 + ec.col(0);
+  const int32_t ncol0 = a.vcol0 + lcol0;
   int32_t rel[8];
   bool hit = false;
 #pragma unroll
@@ -89,15 +92,16 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
   // columns, 8 (2 (q & 1) + (q >> 1)) + 32 p, for one 16-byte store: half the
   // store instructions, each writing 64 contiguous bytes per row instead of
   // 32 (the store pipeline's cost goes with instructions x rows touched).
-  const rsrc_t srs = make_rsrc(kStoreS ? static_cast<const void*>(a.S) : a.xy, kWholeRange);
+  const rsrc_t srs = make_rsrc(kStoreS ? static_cast<const void*>(a.S) : a.xy,
+                               kStoreS ? a.s_range : 0u);
   const uint32_t q = ec.lane >> 4;
-  const uint32_t scol = (uint32_t)vrow0 + ec.wn * 128u + 8u * (2u * (q & 1u) + (q >> 1));
+  const uint32_t scol = (uint32_t)(a.vcol0 + vrow0) + ec.wn * 128u + 8u * (2u * (q & 1u) + (q >> 1));
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     // vocabulary columns of this lane below V, re-formed per fragment row
     // through an empty asm so that the 32 compares are not hoisted out of
     // the row loop (their masks spilled from the scalar registers)
-    int32_t lim = a.V - ncol0;
+    int32_t lim = a.V - lcol0;
     if (kTail) asm volatile("" : "+v"(lim));
     float v[8][4];
     uint32_t slo[8], shi[8];
@@ -160,26 +164,33 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
 
 // kTail: V is not a multiple of 256, so the last vocabulary tile masks its
 // columns past V (without it the epilogue skips that select per logit).
-template <bool kCap, bool kStoreS, bool kTail>
+// kKTail: H is not a multiple of 64, so the last K stage is partial.
+template <bool kCap, bool kStoreS, bool kTail, bool kKTail>
 MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
   const TileSeq seq((uint32_t)(a.tiles_m * a.vt_total));
   const EpiCoordsBf ec0;
+  const int KT = (a.H + kBKBf - 1) / kBKBf;
+  const uint32_t c_lim = (uint32_t)(a.H - (KT - 1) * kBKBf) / 8u;
   KcOp A, B;
   A.init_frag(ec0.wm * 128);
   B.init_frag(ec0.wn * 128);
-  mainloop_bf16<false>(
-      lds, A, B, a.H / kBKBf, seq.count(),
+  if constexpr (kKTail) {
+    A.set_tail(c_lim);
+    B.set_tail(c_lim);
+  }
+  mainloop_bf16<false, kKTail>(
+      lds, A, B, KT, seq.count(),
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tv;
         grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, kFwdGroupBf, tm, tv);
         const int32_t row0 = (int32_t)tm * 256, vrow0 = (int32_t)tv * 256;
-        A.set_rows(make_rsrc(a.X, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+        A.set_rows(make_rsrc(a.X, a.x_range), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t rr = row0 + (int32_t)r;
           rr = rr < a.N ? rr : a.N - 1;
           return (uint32_t)a.row_index[rr] * (uint32_t)a.ldx_b;
         });
-        B.set_rows(make_rsrc(a.W, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+        B.set_rows(make_rsrc(a.W, a.w_range), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t v = vrow0 + (int32_t)r;
           v = v < a.V ? v : a.V - 1;
           return (uint32_t)v * (uint32_t)a.ldw_b;
@@ -200,10 +211,11 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
           d[fm] = 0.f;
         }
         fwd_epilogue_bf16<kCap, kStoreS, kTail>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
-        fwd_final_merge(scratch, m2, d, rglob, tv, ec, a);
+        fwd_final_merge(scratch, m2, d, rglob, (uint32_t)a.vcol0 / 256u + tv, ec, a);
         // the merge's LDS is the ring slot refilled in the next phase 1
         __syncthreads();
-      });
+      },
+      ZeroInit(), c_lim);
 }
 
 // Backward recompute epilogue of the bf16 kernel, one fragment row at a
@@ -234,7 +246,7 @@ __device__ __forceinline__ void recompute_epilogue_bf16(const f32x4_t (&acc)[8][
     hit |= lane_holds<8>(rel[fm]);
   }
   const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
-  const rsrc_t grs = make_rsrc(a.G, kWholeRange);
+  const rsrc_t grs = make_rsrc(a.G, a.g_range);
   const uint32_t q = ec.lane >> 4;
   const uint32_t gcol = (uint32_t)col0 + ec.wn * 128u + 8u * (2u * (q & 1u) + (q >> 1));
 #pragma unroll
@@ -289,28 +301,35 @@ __device__ __forceinline__ void recompute_epilogue_bf16(const f32x4_t (&acc)[8][
 // vocabulary entries); the epilogue writes G.  kTail: the block's vocabulary
 // width cv is not a multiple of 256 (only the last block, and only when V is
 // not), so its last tile masks the columns past cv.
-template <bool kCap, bool kTail>
+template <bool kCap, bool kTail, bool kKTail>
 MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
   const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
   const EpiCoordsBf ec0;
+  const int KT = (a.H + kBKBf - 1) / kBKBf;
+  const uint32_t c_lim = (uint32_t)(a.H - (KT - 1) * kBKBf) / 8u;
   KcOp A, B;
   A.init_frag(ec0.wm * 128);
   B.init_frag(ec0.wn * 128);
-  mainloop_bf16<false>(
-      lds, A, B, a.H / kBKBf, seq.count(),
+  if constexpr (kKTail) {
+    A.set_tail(c_lim);
+    B.set_tail(c_lim);
+  }
+  mainloop_bf16<false, kKTail>(
+      lds, A, B, KT, seq.count(),
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
-        const int32_t row0 = (int32_t)tm * 256, vrow0 = a.v0 + (int32_t)tn * 256;
-        A.set_rows(make_rsrc(a.X, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+        // W points at the block's first vocabulary row (v0)
+        const int32_t row0 = (int32_t)tm * 256, vloc0 = (int32_t)tn * 256;
+        A.set_rows(make_rsrc(a.X, a.x_range), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t rr = row0 + (int32_t)r;
           rr = rr < a.Cn ? rr : a.Cn - 1;
           return (uint32_t)a.row_index[rr] * (uint32_t)a.ldx_b;
         });
-        B.set_rows(make_rsrc(a.W, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
-          int32_t v = vrow0 + (int32_t)r;
-          v = v < a.V ? v : a.V - 1;
+        B.set_rows(make_rsrc(a.W, a.w_range), [&](uint32_t r) __attribute__((always_inline)) {
+          int32_t v = vloc0 + (int32_t)r;
+          v = v < a.cv ? v : a.cv - 1;  // rows past the block repeat its last one
           return (uint32_t)v * (uint32_t)a.ldw_b;
         });
       },
@@ -320,7 +339,8 @@ MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t row0 = (int32_t)tm * 256, col0 = (int32_t)tn * 256;
         recompute_epilogue_bf16<kCap, kTail>(acc, a, ec, row0, col0);
-      });
+      },
+      ZeroInit(), c_lim);
 }
 
 // dX tile epilogue of the bf16 kernels (one mode of dx_epilogue per
@@ -385,11 +405,12 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t row0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
-        A.set_rows(make_rsrc(a.G, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+        A.set_rows(make_rsrc(a.G, a.g_range), [&](uint32_t r) __attribute__((always_inline)) {
           return (uint32_t)(row0 + (int32_t)r) * (uint32_t)a.ldg_b;
         });
-        B.init(make_rsrc(a.W, kWholeRange), (uint32_t)a.v0 * (uint32_t)a.ldw_b + (uint32_t)h0 * 2u,
-               (uint32_t)a.ldw_b, a.V - a.v0, a.H - h0, ec0.wn * 128);
+        // W points at the block's first vocabulary row (v0)
+        B.init(make_rsrc(a.W, a.w_range), (uint32_t)h0 * 2u, (uint32_t)a.ldw_b, a.V - a.v0,
+               a.H - h0, ec0.wn * 128);
       },
       [&](int k, f32x4_t(&acc)[8][8], char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
@@ -397,6 +418,12 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         dx_epilogue_bf16<kMode>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
       });
+}
+
+// Bytes of a whole 256 x 256 dW tile's rows from its base: 255 row pitches
+// plus one row of 256 values.
+__device__ __forceinline__ uint32_t dw_tile_range(const DwArgs& a) {
+  return (uint32_t)(255u * (uint32_t)a.lddw + 256u) * 4u;
 }
 
 // dW tiles accumulate in place: a tile's accumulators start from the fp32
@@ -411,8 +438,9 @@ __device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& 
   if (load && m0 + 256 <= a.cv && h0 + 256 <= a.H) {
     // whole tile inside dW (all but the edge tiles): unconditional buffer
     // loads off the tile's base, one lane offset for all 64 (fragment row fm
-    // adds a scalar offset, fragment column fn an immediate)
-    const rsrc_t r = make_rsrc(base, kWholeRange);
+    // adds a scalar offset, fragment column fn an immediate); the resource
+    // ends with the tile's last row
+    const rsrc_t r = make_rsrc(base, dw_tile_range(a));
     const uint32_t voff = ((uint32_t)ec.row(0) * (uint32_t)a.lddw + (uint32_t)ec.col(0)) * 4u;
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm)
@@ -444,7 +472,7 @@ __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const D
                                              const EpiCoordsBf& ec, int32_t m0, int32_t h0) {
   float* base = a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0;
   if (m0 + 256 <= a.cv && h0 + 256 <= a.H) {
-    const rsrc_t r = make_rsrc(base, kWholeRange);
+    const rsrc_t r = make_rsrc(base, dw_tile_range(a));
     const uint32_t voff = ((uint32_t)ec.row(0) * (uint32_t)a.lddw + (uint32_t)ec.col(0)) * 4u;
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm) {
@@ -485,9 +513,9 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
         uint32_t tm, tn;
         grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t m0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
-        A.init(make_rsrc(a.G, kWholeRange), (uint32_t)m0 * 2u, (uint32_t)a.ldg_b, a.g_rows,
+        A.init(make_rsrc(a.G, a.g_range), (uint32_t)m0 * 2u, (uint32_t)a.ldg_b, a.g_rows,
                a.g_cols - m0, ec0.wm * 128);
-        B.set_rows(make_rsrc(a.XcT, kWholeRange), [&](uint32_t r) __attribute__((always_inline)) {
+        B.set_rows(make_rsrc(a.XcT, a.xt_range), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t h = h0 + (int32_t)r;
           h = h < a.H ? h : a.H - 1;
           return (uint32_t)h * (uint32_t)a.ldxt_b;

@@ -189,7 +189,7 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         ctx.path = "general"
         if dt == MT_DTYPE_BF16 and n > 0 and (grad_scale is not None or allow_unit):
             C, ws_bytes, pays = fused_plan(T, n, H, V)
-            if _use_fused(pays):
+            if C > 0 and _use_fused(pays):  # C = 0: the fused path cannot run this shape
                 ctx.path = "fused" if grad_scale is not None else "fused_unit"
         ctx.dw_accumulator = dw_accumulator
         if ctx.path != "general":
@@ -487,6 +487,20 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     cap = 0.0 if softcap is None else float(softcap)
     if cap < 0:
         raise ValueError("softcap must be positive (or None)")
+    # whole 16-byte chunks along H: zero columns appended (F.pad, whose
+    # backward slices the gradients back) contribute nothing to the logits
+    H = lm_head_weight.shape[-1]
+    hmul = 16 // max(lm_head_weight.element_size(), 1)
+    if H % hmul and lm_head_weight.dtype in (torch.bfloat16, torch.float32):
+        if dw_accumulator is not None:
+            raise ValueError(f"dw_accumulator needs H a multiple of {hmul} (H={H}): the weight "
+                             "gradient is formed at a zero-padded width")
+        Hp = -(-H // hmul) * hmul
+        return fused_linear_cross_entropy(
+            torch.nn.functional.pad(hidden_states, (0, Hp - H)),
+            torch.nn.functional.pad(lm_head_weight, (0, Hp - H)), target,
+            ignore_index=ignore_index, softcap=softcap, shift_labels=shift_labels,
+            grad_scale=grad_scale)
     recording = torch.is_grad_enabled() and (hidden_states.requires_grad
                                              or lm_head_weight.requires_grad)
     if not recording:
@@ -499,9 +513,32 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
     if shift_labels and target.dim() >= 2 and target.shape[0] > 1:
         target = torch.nn.functional.pad(target, (0, 1), value=int(ignore_index))[..., 1:]
         shift_labels = False
+    # bf16 rows are addressed with 32-bit offsets: X beyond one buffer's
+    # reach (mt_flce_max_buffer_bytes) runs over row ranges; the lm_head
+    # gradient of every range accumulates (autograd, or dw_accumulator)
+    T = target.numel()
+    if hidden_states.dtype == torch.bfloat16 and T > 0:
+        limit = int(load().mt_flce_max_buffer_bytes())
+        pitch = -(-H // 8) * 8 * 2
+        rows = max(1, limit // pitch)
+        if T > rows:
+            hid = hidden_states.reshape(T, H)
+            tgt = target.reshape(T)
+            if shift_labels:
+                tgt = torch.nn.functional.pad(tgt, (0, 1), value=int(ignore_index))[1:]
+            gs = grad_scale
+            parts = []
+            for t0 in range(0, T, rows):
+                t1 = min(T, t0 + rows)
+                g = gs[t0:t1] if isinstance(gs, torch.Tensor) and gs.numel() == T else gs
+                parts.append(_FusedLinearCrossEntropyNone.apply(
+                    hid[t0:t1], lm_head_weight, tgt[t0:t1], int(ignore_index), cap, False,
+                    dw_accumulator, g, allow_unit))
+            return torch.cat(parts).view(hidden_states.shape[:-1])
     return _FusedLinearCrossEntropyNone.apply(hidden_states, lm_head_weight, target,
                                               int(ignore_index), cap, bool(shift_labels),
                                               dw_accumulator, grad_scale, allow_unit)
+
 
 
 class _CrossEntropyNone(torch.autograd.Function):

@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_double, c_int, c_int64, c_void_p
 
 import numpy as np
@@ -12,11 +13,16 @@ _lib = None
 
 
 def lib() -> ctypes.CDLL:
+    """The C restatement; MT_ORACLE_LIB names another build of it (the
+    sanitised one of oracle/build.py, for tests/test_oracle_asan.py)."""
     global _lib
     if _lib is None:
-        if not LIB.exists():
-            build()
-        L = ctypes.CDLL(str(LIB))
+        path = os.environ.get("MT_ORACLE_LIB")
+        if not path:
+            if not LIB.exists():
+                build()
+            path = str(LIB)
+        L = ctypes.CDLL(path)
         L.ref_prepare.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p]
         L.ref_forward.argtypes = [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_double,
                                   c_void_p, c_void_p, c_int64, c_void_p, c_void_p]

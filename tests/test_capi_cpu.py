@@ -80,7 +80,7 @@ def call_forward(**kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(dtype=7), 1),            # unknown dtype
-    (dict(H=96, ldx=96, ldw=96), 3),  # H not a multiple of 64 (bf16)
+    (dict(H=100, ldx=104, ldw=104), 3),  # H not whole 16-byte chunks (bf16: multiple of 8)
     (dict(ldx=32), 1),             # ldx < H
     (dict(ldx=68), 1),             # row pitch not a multiple of 16 bytes
     (dict(X=18), 1),               # misaligned X
@@ -176,3 +176,24 @@ def test_fused_planner_prefers_the_faster_path():
     c, ws, pays = ctypes.c_int64(), ctypes.c_size_t(), ctypes.c_int()
     assert lib.mt_flce_fused_plan(100, 50, 64, 100, 0, 0, ctypes.byref(c), ctypes.byref(ws),
                                   ctypes.byref(pays)) == 3  # fp32: unsupported
+
+
+def test_buffer_reach_hook(monkeypatch):
+    """MT_FLCE_MAX_BUFFER_BYTES lowers the reach of one bf16 buffer: X beyond it
+    is rejected (the host layer splits rows), 256 weight rows beyond it too,
+    and the fused path rejects a weight beyond it (no kernel is launched)."""
+    lib = _lib.load()
+    assert lib.mt_flce_max_buffer_bytes() == 0xFFFFFFFF
+    monkeypatch.setenv("MT_FLCE_MAX_BUFFER_BYTES", "4096")
+    assert lib.mt_flce_max_buffer_bytes() == 4096
+    # X of 8 rows x 64 bf16 = 1 KiB fits; 64 rows = 8 KiB does not
+    assert call_forward(T=64, n=4) == 3
+    assert "row ranges" in lib.mt_flce_last_error().decode()
+    # fused: W of 100 x 64 bf16 = 12.8 KB beyond 4 KiB
+    assert lib.mt_flce_fused(16, 16, 8, 64, 100, 64, 64, 1, 0.0, 16, 16, 4, 16, 0, 16, 16, 16, 64,
+                             16, 64, 0, 256, 16, 1 << 30, None) == 3
+    assert "one buffer" in lib.mt_flce_last_error().decode()
+    monkeypatch.setenv("MT_FLCE_MAX_BUFFER_BYTES", "1000")
+    # 256 weight rows of 128 bytes exceed 1000 bytes
+    assert call_forward(T=4, n=2) == 3
+    assert "256 of them" in lib.mt_flce_last_error().decode()
