@@ -483,10 +483,10 @@ int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t 
     // vocabulary blocks of at most one buffer's reach; each writes the
     // partials of its own tiles, the finalize merges them all
     static void (*const kerns[2][2][2])(FwdArgs) = {
-        {{fwd_bf16_kernel<false, false, false, false>, fwd_bf16_kernel<false, false, false, true>},
-         {fwd_bf16_kernel<false, false, true, false>, fwd_bf16_kernel<false, false, true, true>}},
-        {{fwd_bf16_kernel<true, false, false, false>, fwd_bf16_kernel<true, false, false, true>},
-         {fwd_bf16_kernel<true, false, true, false>, fwd_bf16_kernel<true, false, true, true>}}};
+        {{fwd_bf16_kernel<false, kStoreNone, false, false>, fwd_bf16_kernel<false, kStoreNone, false, true>},
+         {fwd_bf16_kernel<false, kStoreNone, true, false>, fwd_bf16_kernel<false, kStoreNone, true, true>}},
+        {{fwd_bf16_kernel<true, kStoreNone, false, false>, fwd_bf16_kernel<true, kStoreNone, false, true>},
+         {fwd_bf16_kernel<true, kStoreNone, true, false>, fwd_bf16_kernel<true, kStoreNone, true, true>}}};
     const int64_t vb = vocab_block_rows(V, ldw);
     for (int64_t v0 = 0; v0 < V; v0 += vb) {
       const int64_t vn = std::min(vb, V - v0);
@@ -508,7 +508,7 @@ int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t 
     MT_TRY(check_launch("fwd_kernel"));
   }
   hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(n_valid, 4)), dim3(256), 0, stream,
-                     a.part, a.xy, a.N, a.splits, row_index, loss, lse);
+                     a.part, a.xy, a.N, a.splits, row_index, loss, lse, static_cast<int32_t*>(nullptr));
   return check_launch("fwd_finalize_kernel");
 }
 
@@ -659,10 +659,17 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
 }
 
 // ------------------------------------------------------------------ fused
-// Fused forward + backward (bf16): per chunk of C valid rows, the logits
-// S [C, Vpad] are written once (bf16), turned into G in place once the rows'
-// lse is known, and consumed by dX = G W (complete, K = V) and
-// dW (+)= G^T X_chunk.  6 H V N flops, no recompute.
+// Fused forward + backward (bf16): per chunk of C valid rows, the forward
+// writes E = exp(z) (times the softcap derivative) [C, Vpad] in bf16 once;
+// with the rows' lse known, G = s E - onehot g dz for the per-row factor
+// s = g exp(-lse), so dX = s (E W) (complete, K = V; s in dX's epilogue) and
+// dW (+)= E^T (s X_chunk) (s folded into the gathered X^T), after a one-
+// element-per-row fix-up of the label column.  6 H V N flops, no recompute,
+// no pass over E between the forward and the products.  A chunk with a row
+// whose largest logit lies outside [kGuardLo, kGuardHi] (E's bf16 range
+// would lose the small terms) is recomputed with the logits stored instead
+// and G formed from them in place (s = 1): the guard is raised on the
+// device and the two extra launches return at once when it is not.
 struct FusedPlan {
   int64_t C = 0;
   size_t ws = 0;
@@ -674,7 +681,8 @@ size_t fused_ws(int64_t C, int64_t H, int64_t V) {
   if (C == 0) return 0;
   const int64_t vt = cdiv(V, 256);
   return align_up((size_t)C * vocab_pad(V) * 2) + align_up((size_t)vt * C * 2 * sizeof(float)) +
-         align_up((size_t)C * sizeof(float)) + align_up((size_t)H * C * 2);
+         align_up((size_t)C * sizeof(float)) + align_up((size_t)H * C * 2) +
+         align_up((size_t)C * sizeof(float)) + align_up(sizeof(int32_t));
 }
 
 FusedPlan plan_fused(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) {
@@ -721,15 +729,13 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
   float* xy = reinterpret_cast<float*>(reinterpret_cast<char*>(part) +
                                        align_up((size_t)vt * C * 2 * sizeof(float)));
   char* XcT = reinterpret_cast<char*>(xy) + align_up((size_t)C * sizeof(float));
+  float* scale = reinterpret_cast<float*>(XcT + align_up((size_t)H * C * 2));
+  int32_t* guard = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(scale) +
+                                              align_up((size_t)C * sizeof(float)));
   const int64_t lds_b = Vp * 2, ldxt_b = C * 2;
   for (int64_t c0 = 0; c0 < N; c0 += C) {
     const int64_t cn = std::min(C, N - c0);
     const int64_t tm = cdiv(cn, 256), cn_pad = tm * 256;
-    hipLaunchKernelGGL(gather_t_kernel<__bf16>, dim3((uint32_t)(cn_pad / 64), (uint32_t)cdiv(H, 64)),
-                       dim3(256), 0, stream, static_cast<const char*>(X), ldx * 2, row_index + c0,
-                       (int32_t)cn, (int32_t)H, XcT, ldxt_b);
-    MT_TRY(check_launch("gather_t_kernel"));
-
     FwdArgs a;
     a.X = static_cast<const char*>(X);
     a.W = static_cast<const char*>(W);
@@ -753,26 +759,49 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
     a.xy = xy;
     a.S = S;
     a.lds_b = lds_b;
-    static void (*const kerns[2][2][2])(FwdArgs) = {
-        {{fwd_bf16_kernel<false, true, false, false>, fwd_bf16_kernel<false, true, false, true>},
-         {fwd_bf16_kernel<false, true, true, false>, fwd_bf16_kernel<false, true, true, true>}},
-        {{fwd_bf16_kernel<true, true, false, false>, fwd_bf16_kernel<true, true, false, true>},
-         {fwd_bf16_kernel<true, true, true, false>, fwd_bf16_kernel<true, true, true, true>}}};
-    void (*kern)(FwdArgs) = kerns[softcap > 0.f][V % 256 != 0][H % kBKBf != 0];
-    const int pf = prof_begin("fwd_bf16_kernel<store_s>", 2.0 * H * (double)V * cn, 0, stream);
-    hipLaunchKernelGGL(kern, dim3(persistent_grid(tm * vt)), dim3(kThreadsBf), 0, stream, a);
+    a.guard_reset = guard;
+    static void (*const kerns_e[2][2][2])(FwdArgs) = {
+        {{fwd_bf16_kernel<false, kStoreExp, false, false>, fwd_bf16_kernel<false, kStoreExp, false, true>},
+         {fwd_bf16_kernel<false, kStoreExp, true, false>, fwd_bf16_kernel<false, kStoreExp, true, true>}},
+        {{fwd_bf16_kernel<true, kStoreExp, false, false>, fwd_bf16_kernel<true, kStoreExp, false, true>},
+         {fwd_bf16_kernel<true, kStoreExp, true, false>, fwd_bf16_kernel<true, kStoreExp, true, true>}}};
+    static void (*const kerns_s[2][2][2])(FwdArgs) = {
+        {{fwd_bf16_kernel<false, kStoreLogits, false, false>,
+          fwd_bf16_kernel<false, kStoreLogits, false, true>},
+         {fwd_bf16_kernel<false, kStoreLogits, true, false>,
+          fwd_bf16_kernel<false, kStoreLogits, true, true>}},
+        {{fwd_bf16_kernel<true, kStoreLogits, false, false>,
+          fwd_bf16_kernel<true, kStoreLogits, false, true>},
+         {fwd_bf16_kernel<true, kStoreLogits, true, false>,
+          fwd_bf16_kernel<true, kStoreLogits, true, true>}}};
+    const int ci = softcap > 0.f, ti = V % 256 != 0, ki = H % kBKBf != 0;
+    const dim3 fgrid(persistent_grid(tm * vt));
+    const int pf = prof_begin("fwd_bf16_kernel<store_e>", 2.0 * H * (double)V * cn, 0, stream);
+    hipLaunchKernelGGL(kerns_e[ci][ti][ki], fgrid, dim3(kThreadsBf), 0, stream, a);
     prof_end(pf, stream);
     MT_TRY(check_launch("fwd_bf16_kernel"));
     hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(cn, 4)), dim3(256), 0, stream,
-                       part, xy, (int32_t)cn, (int32_t)vt, row_index + c0, loss, lse + c0);
+                       part, xy, (int32_t)cn, (int32_t)vt, row_index + c0, loss, lse + c0, guard);
     MT_TRY(check_launch("fwd_finalize_kernel"));
-    const int ps = prof_begin("softmax_grad_kernel", 0, 2.0 * 2.0 * (double)cn_pad * Vp, stream);
+    // the guarded recomputation: logits stored, G formed in place (both
+    // return at once unless the guard was raised)
+    a.guard_reset = nullptr;
+    a.run_if = guard;
+    hipLaunchKernelGGL(kerns_s[ci][ti][ki], fgrid, dim3(kThreadsBf), 0, stream, a);
+    MT_TRY(check_launch("fwd_bf16_kernel"));
     hipLaunchKernelGGL(softcap > 0.f ? softmax_grad_kernel<true> : softmax_grad_kernel<false>,
                        dim3((uint32_t)cn_pad), dim3(256), 0, stream, S, lds_b,
                        (int32_t)Vp, (int32_t)cn, (int32_t)V, lse + c0, grad, gstride,
-                       row_index + c0, row_label + c0, softcap);
-    prof_end(ps, stream);
+                       row_index + c0, row_label + c0, softcap, guard);
     MT_TRY(check_launch("softmax_grad_kernel"));
+    hipLaunchKernelGGL(fused_row_scale_kernel, dim3((uint32_t)(cn_pad / 256)), dim3(256), 0, stream,
+                       (int32_t)cn, (int32_t)cn_pad, lse + c0, xy, grad, gstride, row_index + c0,
+                       row_label + c0, guard, softcap, S, lds_b, scale);
+    MT_TRY(check_launch("fused_row_scale_kernel"));
+    hipLaunchKernelGGL(gather_t_kernel<__bf16>, dim3((uint32_t)(cn_pad / 64), (uint32_t)cdiv(H, 64)),
+                       dim3(256), 0, stream, static_cast<const char*>(X), ldx * 2, row_index + c0,
+                       (int32_t)cn, (int32_t)H, XcT, ldxt_b, static_cast<const float*>(scale));
+    MT_TRY(check_launch("gather_t_kernel"));
 
     DxArgs x;
     x.G = S;
@@ -794,6 +823,7 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
     x.row_index = row_index + c0;
     x.tiles_m = (int32_t)tm;
     x.tiles_n = (int32_t)cdiv(H, 256);
+    x.row_scale = scale;
     DwArgs w;
     w.G = S;
     w.ldg_b = lds_b;

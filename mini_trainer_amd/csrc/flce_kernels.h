@@ -67,8 +67,10 @@ struct FwdArgs {
   int32_t tiles_m, splits, vt_total, vt_per_split;
   float* part;  // [N][splits][2] = (max in log2 units, scaled sum)
   float* xy;    // [N] label logit
-  char* S;      // bf16 logits [>= tiles_m * 256][lds_b / 2] (fused path only)
+  char* S;      // bf16 logits or exponentials [>= tiles_m * 256][lds_b / 2] (fused path only)
   int64_t lds_b;
+  const int32_t* run_if = nullptr;  // non-null: the kernel does nothing unless *run_if != 0
+  int32_t* guard_reset = nullptr;   // non-null: set to 0 by the launch (read only after it)
 };
 
 // Columns at or beyond V are masked with a select (no separate tail variant:
@@ -233,10 +235,17 @@ MT_GEMM_KERNEL void fwd_kernel(FwdArgs a) {
 // lse and loss of each valid row from its `splits` (max, sum) partials: one
 // wave per row, lanes merge strided partials, then a fixed shuffle tree
 // (deterministic order).
+// guard (non-null): set to 1 when some row's largest logit lies outside
+// [kGuardLo, kGuardHi], the range in which the fused path keeps exp(logit)
+// itself in bf16 (see fused_row_scale_kernel): at a row maximum of -48 the
+// terms within 39 of it (relative weight e^-39 and more) stay normal numbers
+// (e^-87 is about the smallest), and at +48, lse <= 48 + ln V keeps the row
+// factor g exp(-lse) a normal fp32 number for g down to 1e-10 at V = 2^20.
+constexpr float kGuardLo = -48.f, kGuardHi = 48.f;
 __global__ __launch_bounds__(256) void fwd_finalize_kernel(const float* part, const float* xy,
                                                            int32_t N, int32_t splits,
                                                            const int32_t* row_index, float* loss,
-                                                           float* lse) {
+                                                           float* lse, int32_t* guard) {
   const int32_t r = (int32_t)(blockIdx.x * 4 + (threadIdx.x >> 6));
   if (r >= N) return;  // uniform per wave
   const int lane = (int)(threadIdx.x & 63u);
@@ -249,7 +258,45 @@ __global__ __launch_bounds__(256) void fwd_finalize_kernel(const float* part, co
     const float L = (m + fast_log2(d)) * kLn2;
     lse[r] = L;
     loss[row_index[r]] = L - xy[r];
+    const float mx = m * kLn2;
+    if (guard && !(mx >= kGuardLo && mx <= kGuardHi)) atomicOr(guard, 1);
   }
+}
+
+// Fused path, per row chunk, after the forward stored E = exp(z) (z the
+// bf16-rounded, soft-capped logit; times the softcap derivative 1 - (z/cap)^2)
+// instead of the logits: G = g (softmax - onehot) dz = s E - onehot g dz with
+// the per-row factor s = g exp(-lse).  dX = G W and dW = G^T X then take s as
+// a row scale of dX and of the gathered X^T (gather_t_kernel), and this
+// kernel replaces the label's element by (exp(z_y) - exp(lse)) dz_y, formed
+// in fp32 from the label logit (no cancellation against the rounded E).  When
+// the guard is set the chunk holds G itself (the logits were stored and
+// turned into G by softmax_grad_kernel): s = 1 and no element is touched.
+// Rows cn .. cn_pad get s = 0.  One thread per row.
+__global__ __launch_bounds__(256) void fused_row_scale_kernel(
+    int32_t cn, int32_t cn_pad, const float* lse, const float* xy, const float* grad,
+    int64_t gstride, const int32_t* row_index, const int32_t* row_label, const int32_t* guard,
+    float softcap, char* E, int64_t lde_b, float* scale) {
+  const int32_t t = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (t >= cn_pad) return;
+  if (t >= cn) {
+    scale[t] = 0.f;
+    return;
+  }
+  if (*guard != 0) {
+    scale[t] = 1.f;
+    return;
+  }
+  const float L = lse[t], z = xy[t];
+  const float g = grad[(int64_t)row_index[t] * gstride];
+  float dz = 1.f;
+  if (softcap > 0.f) {
+    const float q = z / softcap;
+    dz = fmaf(-q, q, 1.f);
+  }
+  const float e = (fast_exp2(z * kLog2e) - fast_exp2(L * kLog2e)) * dz;
+  reinterpret_cast<__bf16*>(E + (int64_t)t * lde_b)[row_label[t]] = (__bf16)e;
+  scale[t] = g * fast_exp2(-L * kLog2e);
 }
 
 // ===========================================================================
@@ -391,6 +438,7 @@ struct DxArgs {
   int64_t lddx_b;
   const int32_t* row_index;  // offset to the block's first valid row
   int32_t tiles_m, tiles_n;
+  const float* row_scale = nullptr;  // non-null (bf16 kDxEmit): dX row r times row_scale[r]
 };
 
 template <typename T, int NFN, int WC>
@@ -509,10 +557,14 @@ MT_GEMM_KERNEL void dw_kernel(DwArgs a) {
 
 // XcT[h][t] = X[row_index[t]][h] for t < Cn, 0 for Cn <= t < t_pad.
 // 64 x 64 element tiles; 16-byte loads along h, 16-byte stores along t.
+// scale (non-null, bf16 only): row t is multiplied by scale[t] in fp32 and
+// rounded to bf16 (the fused path's per-row factor of G, see
+// fused_row_scale_kernel).
 template <typename T>
 __global__ __launch_bounds__(256) void gather_t_kernel(const char* X, int64_t ldx_b,
                                                        const int32_t* row_index, int32_t Cn,
-                                                       int32_t H, char* XcT, int64_t ldxt_b) {
+                                                       int32_t H, char* XcT, int64_t ldxt_b,
+                                                       const float* scale = nullptr) {
   constexpr int E = Elt<T>::kBytes;
   constexpr int PER = 16 / E;  // elements per 16-byte vector
   __shared__ T tile[64][64 + 1];
@@ -525,6 +577,15 @@ __global__ __launch_bounds__(256) void gather_t_kernel(const char* X, int64_t ld
     if (t < Cn && hb + hc < H)
       val = *reinterpret_cast<const u32x4_t*>(X + (int64_t)row_index[t] * ldx_b +
                                               (int64_t)(hb + hc) * E);
+    if constexpr (sizeof(T) == 2) {
+      if (scale && t < Cn) {
+        const float sc = scale[t];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          val[j] = pack_bf16x2(__builtin_bit_cast(float, val[j] << 16) * sc,
+                               __builtin_bit_cast(float, val[j] & 0xffff0000u) * sc);
+      }
+    }
     const T* e = reinterpret_cast<const T*>(&val);
 #pragma unroll
     for (int j = 0; j < PER; ++j) tile[tr][hc + j] = e[j];

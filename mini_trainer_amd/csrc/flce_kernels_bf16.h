@@ -51,9 +51,13 @@ struct TileSeq {
 // part[vocab tile][row];
 // the lane that holds a row's label logit writes it to xy[row].  Nothing is
 // carried in registers from one tile to the next.
-// With kStoreS the tile's bf16-rounded logits (before the softcap) are also
-// written to S, row = compacted row of the chunk, column = vocabulary index:
-// the fused path forms G from them in place once the row's lse is known.
+// kStore = kStoreLogits: the tile's bf16-rounded logits (before the softcap)
+// are also written to S, row = compacted row of the chunk, column =
+// vocabulary index, and the fused path forms G from them in place once the
+// row's lse is known.  kStore = kStoreExp: S receives E = exp(z) (1 - (z /
+// cap)^2) instead, z the soft-capped logit (fwd_epilogue_exp_bf16): G is
+// then s E with a per-row factor s applied downstream (see
+// fused_row_scale_kernel), which saves the pass over S that forms G.
 // Row tiles per group of the forward's tile walk: W (the larger operand) is
 // streamed once per group, so wider groups cut its re-reads (8: 2% faster
 // than 4 at config 3; 16 is no better and costs L2 hits).
@@ -62,11 +66,12 @@ constexpr uint32_t kFwdGroupBf = 8;
 // Forward tile epilogue of the bf16 kernels, one fragment row fm at a time
 // (a scheduling fence after each keeps a single row group's values in
 // registers; the unrolled whole-tile form spilled): the lane's 32 logits of
-// the row are rounded to bf16 once, stored to S (kStoreS, before the
-// softcap), soft-capped, masked past V, merged into the row's running
-// (max, sum) and scanned for the label (same arithmetic as
+// the row are rounded to bf16 once, stored to S (kStore = kStoreLogits,
+// before the softcap), soft-capped, masked past V, merged into the row's
+// running (max, sum) and scanned for the label (same arithmetic as
 // fwd_tile_epilogue).
-template <bool kCap, bool kStoreS, bool kTail>
+enum FwdStore : int { kStoreNone = 0, kStoreLogits = 1, kStoreExp = 2 };
+template <bool kCap, int kStore, bool kTail>
 __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], float (&m2)[8],
                                                   float (&d)[8], const int32_t (&lbl)[8],
                                                   const int32_t (&rglob)[8], int32_t vrow0,
@@ -92,6 +97,7 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
   // columns, 8 (2 (q & 1) + (q >> 1)) + 32 p, for one 16-byte store: half the
   // store instructions, each writing 64 contiguous bytes per row instead of
   // 32 (the store pipeline's cost goes with instructions x rows touched).
+  constexpr bool kStoreS = kStore == kStoreLogits;
   const rsrc_t srs = make_rsrc(kStoreS ? static_cast<const void*>(a.S) : a.xy,
                                kStoreS ? a.s_range : 0u);
   const uint32_t q = ec.lane >> 4;
@@ -162,12 +168,135 @@ __device__ __forceinline__ void fwd_epilogue_bf16(const f32x4_t (&acc)[8][8], fl
   }
 }
 
+// Forward tile epilogue with kStore = kStoreExp, two passes per fragment row
+// over the row's bf16-rounded logits, held packed in 16 registers rather
+// than as 32 floats.  Pass 1 finds the lane's row maximum of the
+// soft-capped, masked logits; pass 2 re-forms each logit x, adds
+// exp2(x log2e - max) to the row's sum and stores E = exp2(x log2e)
+// (1 - (x / cap)^2) through the same paired 16-byte stores as the logits,
+// half a row per fenced group.  E takes a
+// second exponential rather than the sum's term times exp2(max): that extra
+// per-row factor, live across the half rows, pushed the register allocator
+// into spilling the main loop's DMA offsets (a scratch reload and a full
+// vmcnt wait in every K stage), as did the float form of the logits.
+// Columns past V give E = 0; rows past N repeat row N - 1's values (the
+// gather clamps the row index) and meet zero rows of the gathered X^T.  The
+// label's logit is scanned in the (rare) branch of the wave that holds it.
+template <bool kCap, bool kTail>
+__device__ __forceinline__ void fwd_epilogue_exp_bf16(const f32x4_t (&acc)[8][8], float (&m2)[8],
+                                                      float (&d)[8], const int32_t (&lbl)[8],
+                                                      const int32_t (&rglob)[8], int32_t vrow0,
+                                                      const EpiCoordsBf& ec, const FwdArgs& a) {
+  const int32_t lcol0 = vrow0 + ec.col(0);
+  const int32_t ncol0 = a.vcol0 + lcol0;
+  int32_t rel[8];
+  bool hit = false;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    rel[fm] = lbl[fm] - ncol0;
+    hit |= lane_holds<8>(rel[fm]);
+  }
+  const bool any_hit = __builtin_amdgcn_ballot_w64(hit) != 0;
+  const float cap = a.softcap, inv_cap = kCap ? 1.0f / a.softcap : 0.f;
+  const rsrc_t srs = make_rsrc(a.S, a.s_range);
+  const uint32_t q = ec.lane >> 4;
+  const uint32_t scol = (uint32_t)(a.vcol0 + vrow0) + ec.wn * 128u + 8u * (2u * (q & 1u) + (q >> 1));
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    int32_t lim = a.V - lcol0;
+    if (kTail) asm volatile("" : "+v"(lim));
+    // logit r of fragment fn from the packed pair, soft-capped and masked;
+    // dz = the softcap's derivative
+    uint32_t slo[8], shi[8];
+    auto logit = [&](int fn, int r, float& dz) __attribute__((always_inline)) {
+      const uint32_t w = r < 2 ? slo[fn] : shi[fn];
+      float x = __builtin_bit_cast(float, (r & 1) ? (w & 0xffff0000u) : (w << 16));
+      dz = 1.f;
+      if (kCap) {
+        const float t = tanh_approx(x * inv_cap);
+        x = cap * t;
+        dz = fmaf(-t, t, 1.f);
+      }
+      if (kTail) x = fn * 16 + r < lim ? x : -INFINITY;
+      return x;
+    };
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) {
+      slo[fn] = pack_bf16x2(acc[fm][fn][0], acc[fm][fn][1]);
+      shi[fn] = pack_bf16x2(acc[fm][fn][2], acc[fm][fn][3]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float dz;
+        tmax = fmaxf(tmax, logit(fn, r, dz));
+      }
+    }
+    if (any_hit) {
+      const int rl = rel[fm];
+      if (lane_holds<8>(rl) && rglob[fm] < a.N) {
+        float hitv = 0.f;
+#pragma unroll
+        for (int fn = 0; fn < 8; ++fn)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float dz;
+            hitv = (rl == fn * 16 + r) ? logit(fn, r, dz) : hitv;
+          }
+        a.xy[rglob[fm]] = hitv;
+      }
+    }
+    const float mn = fmaxf(m2[fm], tmax * kLog2e);
+    const uint32_t soff = (uint32_t)rglob[fm] * (uint32_t)a.lds_b + scol * 2u;
+    float sum = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      uint32_t plo[4], phi[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int fn = 4 * hh + j;
+        float e[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float dz;
+          const float x = logit(fn, r, dz);
+          const float t = fast_exp2(fmaf(x, kLog2e, -mn));
+          sum += t;
+          const float ex = fast_exp2(x * kLog2e);
+          e[r] = kCap ? ex * dz : ex;
+        }
+        plo[j] = pack_bf16x2(e[0], e[1]);
+        phi[j] = pack_bf16x2(e[2], e[3]);
+      }
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const auto l2 = __builtin_amdgcn_permlane16_swap(plo[2 * pp], plo[2 * pp + 1], false, false);
+        const auto h2 = __builtin_amdgcn_permlane16_swap(phi[2 * pp], phi[2 * pp + 1], false, false);
+        u32x4_t o;
+        o[0] = l2[0];
+        o[1] = h2[0];
+        o[2] = l2[1];
+        o[3] = h2[1];
+        __builtin_amdgcn_raw_buffer_store_b128(o, srs, soff + (uint32_t)(2 * hh + pp) * 64u, 0, 0);
+      }
+      sched_fence();
+    }
+    d[fm] = fmaf(d[fm], fast_exp2(m2[fm] - mn), sum);
+    m2[fm] = mn;
+    sched_fence();
+  }
+}
+
 // kTail: V is not a multiple of 256, so the last vocabulary tile masks its
 // columns past V (without it the epilogue skips that select per logit).
 // kKTail: H is not a multiple of 64, so the last K stage is partial.
-template <bool kCap, bool kStoreS, bool kTail, bool kKTail>
+// run_if (non-null): the launch does nothing unless *run_if != 0 (the fused
+// path's recomputation of a chunk whose exponentials are out of range);
+// guard_reset (non-null): set to 0 (its readers run after this launch).
+template <bool kCap, int kStore, bool kTail, bool kKTail>
 MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  if (a.run_if && *a.run_if == 0) return;
+  if (a.guard_reset && blockIdx.x == 0 && threadIdx.x == 0) *a.guard_reset = 0;
   const TileSeq seq((uint32_t)(a.tiles_m * a.vt_total));
   const EpiCoordsBf ec0;
   const int KT = (a.H + kBKBf - 1) / kBKBf;
@@ -210,7 +339,10 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
           m2[fm] = kNegBig;
           d[fm] = 0.f;
         }
-        fwd_epilogue_bf16<kCap, kStoreS, kTail>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
+        if constexpr (kStore == kStoreExp)
+          fwd_epilogue_exp_bf16<kCap, kTail>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
+        else
+          fwd_epilogue_bf16<kCap, kStore, kTail>(acc, m2, d, lbl, rglob, (int32_t)tv * 256, ec, a);
         fwd_final_merge(scratch, m2, d, rglob, (uint32_t)a.vcol0 / 256u + tv, ec, a);
         // the merge's LDS is the ring slot refilled in the next phase 1
         __syncthreads();
@@ -358,6 +490,7 @@ __device__ __forceinline__ void dx_epilogue_bf16(const f32x4_t (&acc)[8][8], con
     float* arow = a.accbuf + (int64_t)(rv ? rowl : 0) * a.ld_acc;
     char* xrow = kMode >= kDxAddEmit ? a.dX + (int64_t)a.row_index[rv ? rowl : 0] * a.lddx_b
                                      : nullptr;
+    const float sc = kMode == kDxEmit && a.row_scale ? a.row_scale[rv ? rowl : 0] : 1.f;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
 #pragma unroll
@@ -371,6 +504,7 @@ __device__ __forceinline__ void dx_epilogue_bf16(const f32x4_t (&acc)[8][8], con
           if (kMode <= kDxAdd) {
             *reinterpret_cast<f32x4_t*>(arow + h) = v;
           } else {
+            if (kMode == kDxEmit) v *= sc;
             u32x2_t o;
             o[0] = pack_bf16x2(v[0], v[1]);
             o[1] = pack_bf16x2(v[2], v[3]);
@@ -535,10 +669,12 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
       });
 }
 
-// Fused path: G = g_t (softmax(cap(S_t)) - onehot(y_t)) (1 - tanh^2), in place
-// over one chunk of the bf16 logits S written by fwd_bf16_kernel<*, true>.  One
-// workgroup per row; rows >= cn and columns >= V become 0.  HBM-bound: one
-// 16-byte read and one 16-byte write per 8 elements.
+// Fused path, chunks whose exponentials would leave bf16's range: G = g_t
+// (softmax(cap(S_t)) - onehot(y_t)) (1 - tanh^2), in place over one chunk of
+// the bf16 logits S written by fwd_bf16_kernel<*, kStoreLogits>; nothing
+// unless *run_if != 0 (run_if non-null).  One workgroup per row; rows >= cn
+// and columns >= V become 0.  HBM-bound: one 16-byte read and one 16-byte
+// write per 8 elements.
 template <bool kCap>
 __global__ __launch_bounds__(256) void softmax_grad_kernel(char* S, int64_t lds_b, int32_t cols,
                                                            int32_t cn, int32_t V,
@@ -546,7 +682,9 @@ __global__ __launch_bounds__(256) void softmax_grad_kernel(char* S, int64_t lds_
                                                            int64_t gstride,
                                                            const int32_t* row_index,
                                                            const int32_t* row_label,
-                                                           float softcap) {
+                                                           float softcap,
+                                                           const int32_t* run_if) {
+  if (run_if && *run_if == 0) return;
   const int32_t row = blockIdx.x;
   const bool rv = row < cn;
   const float lse2 = rv ? lse[row] * kLog2e : 0.f;
