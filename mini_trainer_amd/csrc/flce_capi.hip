@@ -296,9 +296,17 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream) {
   prof_end(px, stream);
   MT_TRY(check_launch("dx_bf16_kernel"));
   const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
-  const int pw = prof_begin("dw_bf16_kernel", fw, 0, side->stream);
-  hipLaunchKernelGGL(dw_bf16_kernel, dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
-                     dim3(kThreadsBf), 0, side->stream, w);
+  const int pw = prof_begin(w.queue ? "dw_bf16_kernel<queue>" : "dw_bf16_kernel", fw, 0, side->stream);
+  if (w.queue) {
+    // persistent over the work queue: one workgroup per CU (a multiple of
+    // the 8 XCDs), each tile >= 2 K stages (dw_bf16_kernel<true>)
+    hipLaunchKernelGGL(dw_bf16_kernel<true>, dim3((uint32_t)device_cus()), dim3(kThreadsBf), 0,
+                       side->stream, w);
+  } else {
+    hipLaunchKernelGGL(dw_bf16_kernel<false>,
+                       dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
+                       dim3(kThreadsBf), 0, side->stream, w);
+  }
   prof_end(pw, side->stream);
   MT_TRY(check_launch("dw_bf16_kernel"));
   MT_TRY(hipEventRecord(side->join, side->stream) == hipSuccess
@@ -645,7 +653,7 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       } else {
         if constexpr (sizeof(T) == 2) {
           const int pw = prof_begin("dw_bf16_kernel", dw_flops(w), 0, stream);
-          hipLaunchKernelGGL(dw_bf16_kernel, dim3(persistent_grid(w.tiles_m * w.tiles_n)),
+          hipLaunchKernelGGL(dw_bf16_kernel<false>, dim3(persistent_grid(w.tiles_m * w.tiles_n)),
                              dim3(kThreadsBf), 0, stream, w);
           prof_end(pw, stream);
         } else
@@ -682,7 +690,7 @@ size_t fused_ws(int64_t C, int64_t H, int64_t V) {
   const int64_t vt = cdiv(V, 256);
   return align_up((size_t)C * vocab_pad(V) * 2) + align_up((size_t)vt * C * 2 * sizeof(float)) +
          align_up((size_t)C * sizeof(float)) + align_up((size_t)H * C * 2) +
-         align_up((size_t)C * sizeof(float)) + align_up(sizeof(int32_t));
+         align_up((size_t)C * sizeof(float)) + align_up(sizeof(int32_t) + kQueueWords * 4);
 }
 
 FusedPlan plan_fused(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) {
@@ -732,6 +740,7 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
   float* scale = reinterpret_cast<float*>(XcT + align_up((size_t)H * C * 2));
   int32_t* guard = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(scale) +
                                               align_up((size_t)C * sizeof(float)));
+  uint32_t* queue = reinterpret_cast<uint32_t*>(guard + 1);
   const int64_t lds_b = Vp * 2, ldxt_b = C * 2;
   for (int64_t c0 = 0; c0 < N; c0 += C) {
     const int64_t cn = std::min(C, N - c0);
@@ -794,9 +803,10 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
                        (int32_t)Vp, (int32_t)cn, (int32_t)V, lse + c0, grad, gstride,
                        row_index + c0, row_label + c0, softcap, guard);
     MT_TRY(check_launch("softmax_grad_kernel"));
+    // (also clears dW's work queue: dW runs after the fork below)
     hipLaunchKernelGGL(fused_row_scale_kernel, dim3((uint32_t)(cn_pad / 256)), dim3(256), 0, stream,
                        (int32_t)cn, (int32_t)cn_pad, lse + c0, xy, grad, gstride, row_index + c0,
-                       row_label + c0, guard, softcap, S, lds_b, scale);
+                       row_label + c0, guard, softcap, S, lds_b, scale, queue, (int32_t)kQueueWords);
     MT_TRY(check_launch("fused_row_scale_kernel"));
     hipLaunchKernelGGL(gather_t_kernel<__bf16>, dim3((uint32_t)(cn_pad / 64), (uint32_t)cdiv(H, 64)),
                        dim3(256), 0, stream, static_cast<const char*>(X), ldx * 2, row_index + c0,
@@ -842,6 +852,12 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
     w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
     w.tiles_m = (int32_t)vt;
     w.tiles_n = (int32_t)cdiv(H, 256);
+    // the work queue pays where the tiles outnumber the CUs several times
+    // and each has at least two K stages
+    // (one workgroup per CU covers the 8 XCD shares only for a multiple of 8 CUs)
+    if ((int64_t)w.tiles_m * w.tiles_n >= 4 * device_cus() && device_cus() % kQueueWords == 0 &&
+        cn > kBKBf)
+      w.queue = queue;
     // S and XcT are rewritten by the next chunk only after the join
     MT_TRY(launch_dx_dw_bf16(x, w, stream));
   }

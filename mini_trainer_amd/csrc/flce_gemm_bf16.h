@@ -324,19 +324,23 @@ __device__ __forceinline__ void wait_vm8() {
 // kKTail (both operands KcOp, K contiguous in their rows): the last K stage
 // holds only c_lim of its 8 chunks below K; its DMA keeps to the rows' K
 // extent and its fragments are masked (KcOp::issue_one_k, mask_tail).
-template <bool kThreeA, bool kKTail = false, class A, class B, class Retarget, class Epi,
-          class Init = ZeroInit>
-__device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int ntiles,
-                                              Retarget retarget, Epi epilogue, Init init = Init(),
-                                              uint32_t c_lim = 8) {
-  if (KT <= 0 || ntiles <= 0) return;
+// more(t): does tile t exist?  It is asked in increasing order of t, at most
+// one tile ahead of the one being multiplied when KT >= 2 (two ahead when
+// KT == 1) -- a tile stream whose length is found as it runs (a work queue)
+// answers from what it has fetched so far.
+template <bool kThreeA, bool kKTail = false, class A, class B, class More, class Retarget,
+          class Epi, class Init = ZeroInit>
+__device__ __forceinline__ void mainloop_bf16_seq(char* lds, A& a, B& b, int KT, More more,
+                                                  Retarget retarget, Epi epilogue,
+                                                  Init init = Init(), uint32_t c_lim = 8) {
+  if (KT <= 0 || !more(0)) return;
   // (tile2, kt2) = coordinates of stage g + 2, the next stage to be loaded;
   // they stop at the last stage of the last tile
   int tile2 = 0, kt2 = 0;
   auto advance = [&]() __attribute__((always_inline)) {
     if (kt2 + 1 < KT) {
       ++kt2;
-    } else if (tile2 + 1 < ntiles) {
+    } else if (more(tile2 + 1)) {
       kt2 = 0;
       ++tile2;
       retarget(tile2);
@@ -386,7 +390,7 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
   tie_frags<A>(fa0);
   tie_frags<B>(fb0);
   int g = 0, g3 = 0;  // stage being multiplied, g % 3
-  for (int tile = 0; tile < ntiles; ++tile) {
+  for (int tile = 0; more(tile); ++tile) {
     f32x4_t acc[8][8];
     init(tile, acc);
     for (int kt = 0; kt < KT; ++kt, ++g, g3 = (g3 == 2 ? 0 : g3 + 1)) {
@@ -466,7 +470,7 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
     // them again here (stage g is resident until phase 2 of stage g refills
     // the two-slot operand's other buffer) keeps their 64 registers free
     // during the epilogue.
-    if (tile + 1 < ntiles) {
+    if (more(tile + 1)) {
       // (the memory clobber keeps these reads from being hoisted into the
       // epilogue, where their registers would be live again)
       lgkm_wait0();
@@ -483,6 +487,17 @@ __device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int
     }
   }
   wait_vm0();
+}
+
+// The same over a fixed number of tiles.
+template <bool kThreeA, bool kKTail = false, class A, class B, class Retarget, class Epi,
+          class Init = ZeroInit>
+__device__ __forceinline__ void mainloop_bf16(char* lds, A& a, B& b, int KT, int ntiles,
+                                              Retarget retarget, Epi epilogue, Init init = Init(),
+                                              uint32_t c_lim = 8) {
+  mainloop_bf16_seq<kThreeA, kKTail>(
+      lds, a, b, KT, [ntiles](int t) __attribute__((always_inline)) { return t < ntiles; },
+      retarget, epilogue, init, c_lim);
 }
 
 }  // namespace mtf

@@ -272,12 +272,14 @@ __global__ __launch_bounds__(256) void fwd_finalize_kernel(const float* part, co
 // in fp32 from the label logit (no cancellation against the rounded E).  When
 // the guard is set the chunk holds G itself (the logits were stored and
 // turned into G by softmax_grad_kernel): s = 1 and no element is touched.
-// Rows cn .. cn_pad get s = 0.  One thread per row.
+// Rows cn .. cn_pad get s = 0.  One thread per row; the first n_zero threads
+// also clear zero_words (the dW work queue of the chunk).
 __global__ __launch_bounds__(256) void fused_row_scale_kernel(
     int32_t cn, int32_t cn_pad, const float* lse, const float* xy, const float* grad,
     int64_t gstride, const int32_t* row_index, const int32_t* row_label, const int32_t* guard,
-    float softcap, char* E, int64_t lde_b, float* scale) {
+    float softcap, char* E, int64_t lde_b, float* scale, uint32_t* zero_words, int32_t n_zero) {
   const int32_t t = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (t < n_zero) zero_words[t] = 0u;
   if (t >= cn_pad) return;
   if (t >= cn) {
     scale[t] = 0.f;
@@ -492,6 +494,7 @@ MT_GEMM_KERNEL void dx_kernel(DxArgs a) {
 // ===========================================================================
 // Backward, step 3: dW[v0 : v0 + cv] (+)= G^T . X_block
 // ===========================================================================
+constexpr int kQueueWords = 8;
 struct DwArgs {
   const char* G;  // [K = tokens][vocab], row pitch ldg_b
   int64_t ldg_b;
@@ -506,6 +509,9 @@ struct DwArgs {
   int64_t lddw;
   int32_t accumulate;
   int32_t tiles_m, tiles_n;
+  // non-null: persistent schedule over a work queue (dw_bf16_kernel<true>):
+  // kQueueWords counters, zero at launch, one per XCD's share of the tiles
+  uint32_t* queue = nullptr;
 };
 
 template <int NFN, int WC>

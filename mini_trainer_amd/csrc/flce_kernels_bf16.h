@@ -602,21 +602,48 @@ __device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& 
   }
 }
 
+// Whole tiles leave through LDS: a store instruction straight from the
+// accumulators covers 16 rows x 64 bytes (each lane holds 4 consecutive
+// columns of one row), and the memory pipeline takes such scattered half
+// lines at a quarter of its rate (16.8k cycles per tile against 5.2k for
+// the same bytes in whole rows, measured).  Per fragment row fm each wave
+// writes its 16 x 128 fp32 block (8 KiB) into its own quarter of
+// `scratch` (the epilogue's free ring slot, 32 KiB), reads it back two rows
+// of 512 contiguous bytes per instruction and stores those.  The 16-byte
+// chunk c of row i sits at i * 512 + ((c ^ i) & 31) * 16, so that any 8
+// consecutive lanes of a write or a read touch 8 different 16-byte bank
+// groups.  Each wave uses only its own 8 KiB (no barrier; LDS operations of
+// one wave complete in order).
 __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const DwArgs& a,
-                                             const EpiCoordsBf& ec, int32_t m0, int32_t h0) {
+                                             const EpiCoordsBf& ec, int32_t m0, int32_t h0,
+                                             char* scratch) {
   float* base = a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0;
   if (m0 + 256 <= a.cv && h0 + 256 <= a.H) {
     const rsrc_t r = make_rsrc(base, dw_tile_range(a));
-    const uint32_t voff = ((uint32_t)ec.row(0) * (uint32_t)a.lddw + (uint32_t)ec.col(0)) * 4u;
+    char* R = scratch + (ec.wm * 2u + ec.wn) * 8192u;
+    const uint32_t i = ec.lane & 15u, q = ec.lane >> 4;
+    const uint32_t rr = ec.lane >> 5, c = ec.lane & 31u;
+    // global offset of (row wm * 128 + rr, column wn * 128 + 4 c); fragment
+    // row fm and read j add 16 fm + 2 j rows
+    const uint32_t voff = ((ec.wm * 128u + rr) * (uint32_t)a.lddw + ec.wn * 128u + 4u * c) * 4u;
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm) {
 #pragma unroll
       for (int fn = 0; fn < 8; ++fn)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[fm][fn]), r,
-                                               voff + (uint32_t)fn * 64u,
-                                               (uint32_t)(fm * 16) * (uint32_t)a.lddw * 4u, 0);
+        lds_write16(R, i * 512u + ((((uint32_t)fn * 4u + q) ^ i) & 31u) * 16u,
+                    __builtin_bit_cast(u32x4_t, acc[fm][fn]));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t row = 2u * (uint32_t)j + rr;
+        const u32x4_t v = lds_read16(R, row * 512u + ((c ^ row) & 31u) * 16u);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            v, r, voff, (uint32_t)(fm * 16 + 2 * j) * (uint32_t)a.lddw * 4u, 0);
+      }
       sched_fence();
     }
+    // the slot is refilled by the next phase 1's DMA: every wave's reads first
+    lgkm_wait0();
+    __builtin_amdgcn_s_barrier();
     return;
   }
 #pragma unroll
@@ -632,20 +659,100 @@ __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const D
   }
 }
 
+// Work queue of the persistent dW schedule.  The logical tiles are split
+// into 8 contiguous shares, one per XCD (workgroup b runs on XCD b mod 8, as
+// in xcd_remap), and the workgroups of an XCD take the tiles of its share in
+// the order they ask for them (one atomic per tile on the share's counter):
+// workgroups that start late -- on CUs that dX holds when dW is launched
+// beside it -- simply take fewer tiles.  Wave 0 asks two tiles ahead (the
+// main loop re-points its DMA at tile t + 1 while it multiplies tile t); the
+// answer reaches the other waves through LDS in the tile's epilogue.
+struct DwQueue {
+  uint32_t* ctr;       // this XCD's counter
+  uint32_t lo, hi;     // this XCD's share [lo, hi) of the logical tiles
+  uint32_t cur, nxt;   // logical ids of tiles base, base + 1 (>= hi: none)
+  int base;            // main-loop index of `cur`
+  uint32_t asked;      // wave 0, lane 0: the id of tile base + 2, being fetched
+  uint32_t pending;    // the same, read out (meaningful in wave 0)
+
+  __device__ __forceinline__ uint32_t fetch() const {
+    return lo + __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // first two tiles, broadcast through LDS (before the ring uses it)
+  __device__ __forceinline__ void start(const DwArgs& a, uint32_t total, char* lds) {
+    const uint32_t x = blockIdx.x & 7u;
+    ctr = a.queue + x;
+    lo = (uint32_t)((uint64_t)total * x / 8u);
+    hi = (uint32_t)((uint64_t)total * (x + 1u) / 8u);
+    base = 0;
+    uint32_t* box = reinterpret_cast<uint32_t*>(lds);
+    if (threadIdx.x == 0) {
+      const uint32_t t0 = lo + __hip_atomic_fetch_add(ctr, 2u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+      box[0] = t0;
+      box[1] = t0 + 1u;
+    }
+    lgkm_wait0();
+    __builtin_amdgcn_s_barrier();
+    cur = __builtin_amdgcn_readfirstlane(box[0]);
+    nxt = __builtin_amdgcn_readfirstlane(box[1]);
+    lgkm_wait0();
+    __builtin_amdgcn_s_barrier();
+  }
+  __device__ __forceinline__ uint32_t id(int t) const { return t == base ? cur : nxt; }
+  __device__ __forceinline__ bool has(int t) const { return id(t) < hi; }
+  // init of tile `base`, before its accumulator loads: ask for tile
+  // base + 2 (only while tiles remain) ...
+  __device__ __forceinline__ void ask() {
+    if (threadIdx.x == 0 && nxt < hi) asked = fetch();
+  }
+  // ... and after them: the answer into a scalar register (its wait then
+  // falls inside the loads' own latency rather than in the epilogue, where
+  // waiting on it would also wait for the ring's DMA of the next tile)
+  __device__ __forceinline__ void settle() { pending = __builtin_amdgcn_readfirstlane(asked); }
+  // epilogue of tile `base`: tile base + 2's id to every wave, then advance
+  __device__ __forceinline__ void rotate(char* scratch) {
+    uint32_t* box = reinterpret_cast<uint32_t*>(scratch);
+    if (threadIdx.x == 0) box[0] = nxt < hi ? pending : hi;
+    lgkm_wait0();
+    __builtin_amdgcn_s_barrier();
+    const uint32_t n2 = __builtin_amdgcn_readfirstlane(box[0]);
+    lgkm_wait0();
+    __builtin_amdgcn_s_barrier();
+    cur = nxt;
+    nxt = n2;
+    ++base;
+  }
+};
+
 // Backward step 3: A = G read K-major (256 vocabulary columns, K = tokens),
-// B = X^T rows of the block (256 hidden rows).
+// B = X^T rows of the block (256 hidden rows).  kQueue: persistent over the
+// work queue above (grid = one workgroup per CU, K >= 2 stages); otherwise
+// one workgroup per tile or a static persistent schedule (TileSeq).
+template <bool kQueue>
 MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
-  const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
+  const uint32_t total = (uint32_t)(a.tiles_m * a.tiles_n);
+  const TileSeq seq(total);
+  DwQueue q;
+  if constexpr (kQueue) q.start(a, total, lds);
   const EpiCoordsBf ec0;
   TrOp A;
   KcOp B;
   B.init_frag(ec0.wn * 128);
-  mainloop_bf16<true>(
-      lds, A, B, (a.kt_rows + kBKBf - 1) / kBKBf, seq.count(),
+  auto logical = [&](int k) __attribute__((always_inline)) {
+    if constexpr (kQueue) return q.id(k);
+    else return seq.logical(k);
+  };
+  mainloop_bf16_seq<true>(
+      lds, A, B, (a.kt_rows + kBKBf - 1) / kBKBf,
+      [&](int k) __attribute__((always_inline)) {
+        if constexpr (kQueue) return q.has(k);
+        else return k < seq.count();
+      },
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tn;
-        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        grouped_tile(logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t m0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
         A.init(make_rsrc(a.G, a.g_range), (uint32_t)m0 * 2u, (uint32_t)a.ldg_b, a.g_rows,
                a.g_cols - m0, ec0.wm * 128);
@@ -655,17 +762,20 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
           return (uint32_t)h * (uint32_t)a.ldxt_b;
         });
       },
-      [&](int k, f32x4_t(&acc)[8][8], char*) __attribute__((always_inline)) {
+      [&](int k, f32x4_t(&acc)[8][8], char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
-        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
-        dw_store_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
+        grouped_tile(logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        if constexpr (kQueue) q.rotate(scratch);
+        dw_store_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch);
       },
       [&](int k, f32x4_t(&acc)[8][8]) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
-        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        grouped_tile(logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        if constexpr (kQueue) q.ask();
         dw_load_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0);
+        if constexpr (kQueue) q.settle();
       });
 }
 

@@ -120,6 +120,34 @@ def test_fused_out_of_range_logits_recompute_their_chunk(gpu, monkeypatch, shift
     assert torch.equal(l2.cpu(), loss)
 
 
+def test_fused_dw_work_queue_with_tails(gpu, monkeypatch):
+    # 257 x 5 = 1285 dW tiles per chunk, at least 4 per CU: dW runs
+    # persistent over its work queue; a vocabulary tail (V = 65600) and a
+    # hidden tail (H = 1056: the fifth column of tiles 32 wide), 256-row
+    # chunks.  Reference: the torch path on the GPU in fp32.
+    from mini_trainer_amd.flce import profile_enable, profile_report
+    from oracle.torch_path import torch_path
+    monkeypatch.setenv(BACKWARD_BUDGET_ENV, "1")
+    T, H, V = 700, 1056, 65600
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=51)
+    n = int((y != -100).sum())
+    assert fused_plan(T, n, H, V)[0] == 256
+    profile_enable(True)
+    try:
+        loss, dX, dW = run_fused(gpu, X, W, y, 1.0 / n)
+    finally:
+        profile_enable(False)
+    assert profile_report()["dw_bf16_kernel<queue>"]["launches"] == -(-n // 256)  # one per chunk
+    g = torch.full((T,), 1.0 / n, device=gpu)
+    rl, rdX, rdW = torch_path(X.to(gpu), W.to(gpu), y.to(gpu), grad=g, upcast=True)
+    valid = y != -100
+    assert torch.equal(loss[~valid], torch.zeros(int((~valid).sum())))
+    err = ((loss[valid] - rl.cpu()[valid]).abs() / rl.cpu()[valid].abs()).max().item()
+    assert err <= 2e-3, err
+    assert rel_fro(dX.float(), rdX.cpu().float()) <= GRAD_RFRO
+    assert rel_fro(dW, rdW.cpu()) <= GRAD_RFRO
+
+
 def test_fused_accumulates_and_all_masked(gpu):
     X, W, y = make_case(300, 128, 700, torch.bfloat16, seed=9)
     X2, _, y2 = make_case(200, 128, 700, torch.bfloat16, seed=10)
