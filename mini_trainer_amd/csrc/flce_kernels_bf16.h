@@ -664,33 +664,48 @@ __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const D
 // in xcd_remap), and the workgroups of an XCD take the tiles of its share in
 // the order they ask for them (one atomic per tile on the share's counter):
 // workgroups that start late -- on CUs that dX holds when dW is launched
-// beside it -- simply take fewer tiles.  Wave 0 asks two tiles ahead (the
-// main loop re-points its DMA at tile t + 1 while it multiplies tile t); the
-// answer reaches the other waves through LDS in the tile's epilogue.
+// beside it -- simply take fewer tiles.  A workgroup whose share is used up
+// goes on to the next XCD's share, and so on round the eight: without that,
+// the XCDs that dX leaves earlier or that run faster finished their shares
+// ~0.8 ms before the last one at config 3 (a mean of 300 us idle per CU
+// per chunk, measured).  Wave 0 asks two tiles ahead (the main loop
+// re-points its DMA at tile t + 1 while it multiplies tile t); the answer
+// reaches the other waves through LDS in the tile's epilogue.
 struct DwQueue {
-  uint32_t* ctr;       // this XCD's counter
-  uint32_t lo, hi;     // this XCD's share [lo, hi) of the logical tiles
-  uint32_t cur, nxt;   // logical ids of tiles base, base + 1 (>= hi: none)
+  uint32_t* ctrs;      // the 8 counters
+  uint32_t total;      // logical tiles
+  uint32_t x, steps;   // share being drawn from; shares found used up
+  uint32_t cur, nxt;   // logical ids of tiles base, base + 1 (>= total: none)
   int base;            // main-loop index of `cur`
   uint32_t asked;      // wave 0, lane 0: the id of tile base + 2, being fetched
   uint32_t pending;    // the same, read out (meaningful in wave 0)
 
-  __device__ __forceinline__ uint32_t fetch() const {
-    return lo + __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __device__ __forceinline__ static uint32_t share_lo(uint32_t total, uint32_t s) {
+    return (uint32_t)((uint64_t)total * s / 8u);
+  }
+  // next tile for this workgroup (wave 0, lane 0 only), total when none is left
+  __device__ __forceinline__ uint32_t fetch() {
+    while (steps < 8u) {
+      const uint32_t r = __hip_atomic_fetch_add(ctrs + x, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t t = share_lo(total, x) + r;
+      if (t < share_lo(total, x + 1u)) return t;
+      x = (x + 1u) & 7u;
+      ++steps;
+    }
+    return total;
   }
   // first two tiles, broadcast through LDS (before the ring uses it)
-  __device__ __forceinline__ void start(const DwArgs& a, uint32_t total, char* lds) {
-    const uint32_t x = blockIdx.x & 7u;
-    ctr = a.queue + x;
-    lo = (uint32_t)((uint64_t)total * x / 8u);
-    hi = (uint32_t)((uint64_t)total * (x + 1u) / 8u);
+  __device__ __forceinline__ void start(const DwArgs& a, uint32_t total_, char* lds) {
+    ctrs = a.queue;
+    total = total_;
+    x = blockIdx.x & 7u;
+    steps = 0;
     base = 0;
     uint32_t* box = reinterpret_cast<uint32_t*>(lds);
     if (threadIdx.x == 0) {
-      const uint32_t t0 = lo + __hip_atomic_fetch_add(ctr, 2u, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-      box[0] = t0;
-      box[1] = t0 + 1u;
+      box[0] = fetch();
+      box[1] = fetch();
     }
     lgkm_wait0();
     __builtin_amdgcn_s_barrier();
@@ -700,11 +715,11 @@ struct DwQueue {
     __builtin_amdgcn_s_barrier();
   }
   __device__ __forceinline__ uint32_t id(int t) const { return t == base ? cur : nxt; }
-  __device__ __forceinline__ bool has(int t) const { return id(t) < hi; }
+  __device__ __forceinline__ bool has(int t) const { return id(t) < total; }
   // init of tile `base`, before its accumulator loads: ask for tile
   // base + 2 (only while tiles remain) ...
   __device__ __forceinline__ void ask() {
-    if (threadIdx.x == 0 && nxt < hi) asked = fetch();
+    if (threadIdx.x == 0 && nxt < total) asked = fetch();
   }
   // ... and after them: the answer into a scalar register (its wait then
   // falls inside the loads' own latency rather than in the epilogue, where
@@ -713,7 +728,7 @@ struct DwQueue {
   // epilogue of tile `base`: tile base + 2's id to every wave, then advance
   __device__ __forceinline__ void rotate(char* scratch) {
     uint32_t* box = reinterpret_cast<uint32_t*>(scratch);
-    if (threadIdx.x == 0) box[0] = nxt < hi ? pending : hi;
+    if (threadIdx.x == 0) box[0] = nxt < total ? pending : total;
     lgkm_wait0();
     __builtin_amdgcn_s_barrier();
     const uint32_t n2 = __builtin_amdgcn_readfirstlane(box[0]);
