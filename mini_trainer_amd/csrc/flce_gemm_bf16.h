@@ -113,8 +113,10 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 // Raw buffer resource over `bytes` bytes from `base` (stride 0, dword 3 =
 // the gfx9 raw-buffer format word).  Operand loads go through buffer
 // instructions so that a lane's address is a 32-bit offset (one VGPR instead
-// of two) and the K advance of a stage is a scalar offset; every access is
-// kept in range by the callers, the resource bound only backs that up.
+// of two) and the K advance of a stage is a scalar offset.  Operand DMA is
+// kept in range by the callers, the bound only backs that up; the dW tile
+// accesses use it: a lane outside the tile gets an offset past the bound,
+// whose load returns 0 and whose store is dropped.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
@@ -328,8 +330,11 @@ __device__ __forceinline__ void wait_vm8() {
 // one tile ahead of the one being multiplied when KT >= 2 (two ahead when
 // KT == 1) -- a tile stream whose length is found as it runs (a work queue)
 // answers from what it has fetched so far.
-template <bool kThreeA, bool kKTail = false, class A, class B, class More, class Retarget,
-          class Epi, class Init = ZeroInit>
+// kCarry: one accumulator array for all tiles; init runs for tile 0 only and
+// the epilogue of tile t leaves tile t + 1's starting values in it (dW: its
+// stores of tile t interleaved with the loads of tile t + 1).
+template <bool kThreeA, bool kKTail = false, bool kCarry = false, class A, class B, class More,
+          class Retarget, class Epi, class Init = ZeroInit>
 __device__ __forceinline__ void mainloop_bf16_seq(char* lds, A& a, B& b, int KT, More more,
                                                   Retarget retarget, Epi epilogue,
                                                   Init init = Init(), uint32_t c_lim = 8) {
@@ -390,9 +395,11 @@ __device__ __forceinline__ void mainloop_bf16_seq(char* lds, A& a, B& b, int KT,
   tie_frags<A>(fa0);
   tie_frags<B>(fb0);
   int g = 0, g3 = 0;  // stage being multiplied, g % 3
+  f32x4_t acc_carried[8][8];
   for (int tile = 0; more(tile); ++tile) {
-    f32x4_t acc[8][8];
-    init(tile, acc);
+    f32x4_t acc_own[8][8];
+    f32x4_t(&acc)[8][8] = kCarry ? acc_carried : acc_own;
+    if (!kCarry || tile == 0) init(tile, acc);
     for (int kt = 0; kt < KT; ++kt, ++g, g3 = (g3 == 2 ? 0 : g3 + 1)) {
       advance();
       if constexpr (kKTail) {

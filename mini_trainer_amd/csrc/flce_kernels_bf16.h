@@ -554,109 +554,118 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
       });
 }
 
-// Bytes of a whole 256 x 256 dW tile's rows from its base: 255 row pitches
-// plus one row of 256 values.
-__device__ __forceinline__ uint32_t dw_tile_range(const DwArgs& a) {
-  return (uint32_t)(255u * (uint32_t)a.lddw + 256u) * 4u;
-}
-
 // dW tiles accumulate in place: a tile's accumulators start from the fp32
 // values already in dW (when the kernel accumulates) -- 64 loads per lane in
 // flight together, straight into the accumulator registers -- and the
-// epilogue only stores.  Rows past cv and columns past H start at zero and
-// are not stored.
-__device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& a,
-                                            const EpiCoordsBf& ec, int32_t m0, int32_t h0,
+// epilogue only stores.  Every tile, whole or at the edge (rows past cv,
+// columns past H), takes the same branch-free code: one buffer resource per
+// tile that ends at its last element, and a lane whose element lies outside
+// the tile gets an offset past that end (loads return 0, stores are
+// dropped).  The whole offset is in the per-lane register (no scalar part),
+// which is what the range check covers.
+constexpr uint32_t kDwOut = 0x80000000u;  // beyond any tile resource (< 2 GiB)
+
+struct DwTile {
+  rsrc_t r;
+  uint32_t rows, cols;  // valid extent (<= 256 each)
+};
+__device__ __forceinline__ DwTile dw_tile(const DwArgs& a, int32_t m0, int32_t h0) {
+  DwTile t;
+  t.rows = (uint32_t)min(256, a.cv - m0);
+  t.cols = (uint32_t)min(256, a.H - h0);
+  t.r = make_rsrc(a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0,
+                  ((t.rows - 1u) * (uint32_t)a.lddw + t.cols) * 4u);
+  return t;
+}
+
+// Accumulators of tile (m0, h0) from dW (or zero), fragment row fm of the
+// wave (its fragments' 16 rows x 4 columns per lane).
+__device__ __forceinline__ void dw_load_row(f32x4_t (&accrow)[8], const DwArgs& a,
+                                            const EpiCoordsBf& ec, const DwTile& t, int fm,
                                             bool load) {
-  const float* base = a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0;
-  if (load && m0 + 256 <= a.cv && h0 + 256 <= a.H) {
-    // whole tile inside dW (all but the edge tiles): unconditional buffer
-    // loads off the tile's base, one lane offset for all 64 (fragment row fm
-    // adds a scalar offset, fragment column fn an immediate); the resource
-    // ends with the tile's last row
-    const rsrc_t r = make_rsrc(base, dw_tile_range(a));
-    const uint32_t voff = ((uint32_t)ec.row(0) * (uint32_t)a.lddw + (uint32_t)ec.col(0)) * 4u;
+  const uint32_t row = (uint32_t)ec.row(fm);
 #pragma unroll
-    for (int fm = 0; fm < 8; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < 8; ++fn)
-        acc[fm][fn] = __builtin_bit_cast(
-            f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff + (uint32_t)fn * 64u,
-                                                           (uint32_t)(fm * 16) * (uint32_t)a.lddw * 4u, 0));
-    return;
-  }
-#pragma unroll
-  for (int fm = 0; fm < 8; ++fm) {
-    const int32_t vl = m0 + ec.row(fm);
-#pragma unroll
-    for (int fn = 0; fn < 8; ++fn) {
-      const int32_t h = h0 + ec.col(fn);
-      f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      if (load && vl < a.cv && h < a.H)
-        v = *reinterpret_cast<const f32x4_t*>(base + (int64_t)ec.row(fm) * a.lddw + ec.col(fn));
-      acc[fm][fn] = v;
-    }
-    // one fragment row at a time (uniform point: the conditional loads above
-    // would otherwise all be hoisted and need 256 registers at once)
-    sched_fence();
+  for (int fn = 0; fn < 8; ++fn) {
+    const uint32_t col = (uint32_t)ec.col(fn);
+    const uint32_t off = row < t.rows && col < t.cols ? (row * (uint32_t)a.lddw + col) * 4u : kDwOut;
+    accrow[fn] = load ? __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(t.r, off, 0, 0))
+                      : f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 }
 
-// Whole tiles leave through LDS: a store instruction straight from the
+__device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& a,
+                                            const EpiCoordsBf& ec, int32_t m0, int32_t h0,
+                                            bool load) {
+  const DwTile t = dw_tile(a, m0, h0);
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) dw_load_row(acc[fm], a, ec, t, fm, load);
+}
+
+// Stores leave through LDS: a store instruction straight from the
 // accumulators covers 16 rows x 64 bytes (each lane holds 4 consecutive
 // columns of one row), and the memory pipeline takes such scattered half
 // lines at a quarter of its rate (16.8k cycles per tile against 5.2k for
 // the same bytes in whole rows, measured).  Per fragment row fm each wave
-// writes its 16 x 128 fp32 block (8 KiB) into its own quarter of
-// `scratch` (the epilogue's free ring slot, 32 KiB), reads it back two rows
-// of 512 contiguous bytes per instruction and stores those.  The 16-byte
-// chunk c of row i sits at i * 512 + ((c ^ i) & 31) * 16, so that any 8
-// consecutive lanes of a write or a read touch 8 different 16-byte bank
-// groups.  Each wave uses only its own 8 KiB (no barrier; LDS operations of
-// one wave complete in order).
+// writes its 16 x 128 fp32 block (8 KiB) into its own quarter of `scratch`
+// (the epilogue's free ring slot, 32 KiB), reads it back two rows of 512
+// contiguous bytes per instruction and stores those.  The 16-byte chunk c
+// of row i sits at i * 512 + ((c ^ i) & 31) * 16, so that any 8 consecutive
+// lanes of a write or a read touch 8 different 16-byte bank groups.  Each
+// wave uses only its own 8 KiB (LDS operations of one wave complete in
+// order); the barrier at the end keeps the next phase's DMA into the slot
+// behind every wave's reads.
+__device__ __forceinline__ void dw_store_row(const f32x4_t (&accrow)[8], const DwArgs& a,
+                                             const EpiCoordsBf& ec, const DwTile& t, int fm,
+                                             char* R) {
+  const uint32_t i = ec.lane & 15u, q = ec.lane >> 4;
+  const uint32_t rr = ec.lane >> 5, c = ec.lane & 31u;
+#pragma unroll
+  for (int fn = 0; fn < 8; ++fn)
+    lds_write16(R, i * 512u + ((((uint32_t)fn * 4u + q) ^ i) & 31u) * 16u,
+                __builtin_bit_cast(u32x4_t, accrow[fn]));
+  const uint32_t col = ec.wn * 128u + 4u * c;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t lrow = 2u * (uint32_t)j + rr;
+    const uint32_t row = ec.wm * 128u + (uint32_t)fm * 16u + lrow;
+    const u32x4_t v = lds_read16(R, lrow * 512u + ((c ^ lrow) & 31u) * 16u);
+    const uint32_t off = row < t.rows && col < t.cols ? (row * (uint32_t)a.lddw + col) * 4u : kDwOut;
+    __builtin_amdgcn_raw_buffer_store_b128(v, t.r, off, 0, 0);
+  }
+}
+
 __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const DwArgs& a,
                                              const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                              char* scratch) {
-  float* base = a.dW + (int64_t)(a.v0 + m0) * a.lddw + h0;
-  if (m0 + 256 <= a.cv && h0 + 256 <= a.H) {
-    const rsrc_t r = make_rsrc(base, dw_tile_range(a));
-    char* R = scratch + (ec.wm * 2u + ec.wn) * 8192u;
-    const uint32_t i = ec.lane & 15u, q = ec.lane >> 4;
-    const uint32_t rr = ec.lane >> 5, c = ec.lane & 31u;
-    // global offset of (row wm * 128 + rr, column wn * 128 + 4 c); fragment
-    // row fm and read j add 16 fm + 2 j rows
-    const uint32_t voff = ((ec.wm * 128u + rr) * (uint32_t)a.lddw + ec.wn * 128u + 4u * c) * 4u;
-#pragma unroll
-    for (int fm = 0; fm < 8; ++fm) {
-#pragma unroll
-      for (int fn = 0; fn < 8; ++fn)
-        lds_write16(R, i * 512u + ((((uint32_t)fn * 4u + q) ^ i) & 31u) * 16u,
-                    __builtin_bit_cast(u32x4_t, acc[fm][fn]));
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t row = 2u * (uint32_t)j + rr;
-        const u32x4_t v = lds_read16(R, row * 512u + ((c ^ row) & 31u) * 16u);
-        __builtin_amdgcn_raw_buffer_store_b128(
-            v, r, voff, (uint32_t)(fm * 16 + 2 * j) * (uint32_t)a.lddw * 4u, 0);
-      }
-      sched_fence();
-    }
-    // the slot is refilled by the next phase 1's DMA: every wave's reads first
-    lgkm_wait0();
-    __builtin_amdgcn_s_barrier();
-    return;
-  }
+  const DwTile t = dw_tile(a, m0, h0);
+  char* R = scratch + (ec.wm * 2u + ec.wn) * 8192u;
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
-    const int32_t vl = m0 + ec.row(fm);
-#pragma unroll
-    for (int fn = 0; fn < 8; ++fn) {
-      const int32_t h = h0 + ec.col(fn);
-      if (vl < a.cv && h < a.H)
-        *reinterpret_cast<f32x4_t*>(base + (int64_t)ec.row(fm) * a.lddw + ec.col(fn)) = acc[fm][fn];
-    }
+    dw_store_row(acc[fm], a, ec, t, fm, R);
     sched_fence();
   }
+  lgkm_wait0();
+  __builtin_amdgcn_s_barrier();
+}
+
+// Epilogue of a dW tile when the workgroup has a next tile (nm0, nh0): the
+// stores of this tile interleaved, fragment row by fragment row, with the
+// loads of the next tile's starting values into the same accumulators, so
+// that the loads' latency runs beside the remaining stores instead of
+// before the next tile's first multiplication.
+__device__ __forceinline__ void dw_store_then_load(f32x4_t (&acc)[8][8], const DwArgs& a,
+                                                   const EpiCoordsBf& ec, int32_t m0, int32_t h0,
+                                                   char* scratch, int32_t nm0, int32_t nh0) {
+  const DwTile t = dw_tile(a, m0, h0), nt = dw_tile(a, nm0, nh0);
+  char* R = scratch + (ec.wm * 2u + ec.wn) * 8192u;
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    dw_store_row(acc[fm], a, ec, t, fm, R);
+    dw_load_row(acc[fm], a, ec, nt, fm, a.accumulate != 0);
+    sched_fence();
+  }
+  lgkm_wait0();
+  __builtin_amdgcn_s_barrier();
 }
 
 // Work queue of the persistent dW schedule.  The logical tiles are split
@@ -677,8 +686,7 @@ struct DwQueue {
   uint32_t x, steps;   // share being drawn from; shares found used up
   uint32_t cur, nxt;   // logical ids of tiles base, base + 1 (>= total: none)
   int base;            // main-loop index of `cur`
-  uint32_t asked;      // wave 0, lane 0: the id of tile base + 2, being fetched
-  uint32_t pending;    // the same, read out (meaningful in wave 0)
+  uint32_t asked;      // wave 0, lane 0: the id of tile base + 2
 
   __device__ __forceinline__ static uint32_t share_lo(uint32_t total, uint32_t s) {
     return (uint32_t)((uint64_t)total * s / 8u);
@@ -716,19 +724,16 @@ struct DwQueue {
   }
   __device__ __forceinline__ uint32_t id(int t) const { return t == base ? cur : nxt; }
   __device__ __forceinline__ bool has(int t) const { return id(t) < total; }
-  // init of tile `base`, before its accumulator loads: ask for tile
-  // base + 2 (only while tiles remain) ...
+  // ask for tile base + 2 (only while tiles remain): at tile 0's init, then
+  // in every epilogue after rotate(), so that the atomic's round trip runs
+  // beside the epilogue's stores and the next tile's multiplications
   __device__ __forceinline__ void ask() {
     if (threadIdx.x == 0 && nxt < total) asked = fetch();
   }
-  // ... and after them: the answer into a scalar register (its wait then
-  // falls inside the loads' own latency rather than in the epilogue, where
-  // waiting on it would also wait for the ring's DMA of the next tile)
-  __device__ __forceinline__ void settle() { pending = __builtin_amdgcn_readfirstlane(asked); }
   // epilogue of tile `base`: tile base + 2's id to every wave, then advance
   __device__ __forceinline__ void rotate(char* scratch) {
     uint32_t* box = reinterpret_cast<uint32_t*>(scratch);
-    if (threadIdx.x == 0) box[0] = nxt < total ? pending : total;
+    if (threadIdx.x == 0) box[0] = nxt < total ? asked : total;
     lgkm_wait0();
     __builtin_amdgcn_s_barrier();
     const uint32_t n2 = __builtin_amdgcn_readfirstlane(box[0]);
@@ -759,7 +764,7 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
     if constexpr (kQueue) return q.id(k);
     else return seq.logical(k);
   };
-  mainloop_bf16_seq<true>(
+  mainloop_bf16_seq<true, false, true>(
       lds, A, B, (a.kt_rows + kBKBf - 1) / kBKBf,
       [&](int k) __attribute__((always_inline)) {
         if constexpr (kQueue) return q.has(k);
@@ -777,20 +782,35 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
           return (uint32_t)h * (uint32_t)a.ldxt_b;
         });
       },
+      // epilogue: this tile's stores, the next tile's starting values
       [&](int k, f32x4_t(&acc)[8][8], char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
-        if constexpr (kQueue) q.rotate(scratch);
-        dw_store_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch);
+        bool next;
+        if constexpr (kQueue) {
+          q.rotate(scratch);
+          next = q.has(k + 1);
+          q.ask();
+        } else {
+          next = k + 1 < seq.count();
+        }
+        if (next) {
+          uint32_t ntm, ntn;
+          grouped_tile(logical(k + 1), a.tiles_m, a.tiles_n, 4, ntm, ntn);
+          dw_store_then_load(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch,
+                             (int32_t)ntm * 256, (int32_t)ntn * 256);
+        } else {
+          dw_store_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch);
+        }
       },
+      // init: the first tile's starting values
       [&](int k, f32x4_t(&acc)[8][8]) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
         grouped_tile(logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         if constexpr (kQueue) q.ask();
         dw_load_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0);
-        if constexpr (kQueue) q.settle();
       });
 }
 
