@@ -184,9 +184,10 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H,
 
 /*
  * Fused forward + backward plan (bf16 only): the largest chunk of valid rows
- * (multiple of 256) whose workspace -- the chunk's bf16 logits [chunk,
- * round_up(V, 256)], the (max, sum) partials, the label logits and the chunk's
- * X^T -- fits budget_bytes (0 = default: 5% of T*V*2), then evened out over
+ * (multiple of 256) whose workspace -- the chunk's bf16 exponentials [chunk,
+ * round_up(V, 256)], the (max, sum) partials, the label logits, the chunk's
+ * X^T, its row factors and a few counters -- fits budget_bytes (0 = default:
+ * 5% of T*V*2), then evened out over
  * the chunks.  Writes the chunk size, the workspace size and *pays = 1 if
  * a cost model expects the fused path to beat the general one
  * (mt_flce_forward + mt_flce_backward) under the same budget, else 0: small

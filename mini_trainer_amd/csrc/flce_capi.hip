@@ -362,7 +362,8 @@ size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es) {
   size_t g = align_up((size_t)C * Cv * es);
   size_t acc = Cv < V ? align_up((size_t)C * H * sizeof(float)) : 0;
   size_t xt = align_up((size_t)H * C * es);
-  return g + acc + xt;
+  size_t queue = es == 2 ? align_up(kQueueWords * sizeof(uint32_t)) : 0;  // dW work queue
+  return g + acc + xt + queue;
 }
 
 // ----------------------------------------------------------------- costs
@@ -534,6 +535,7 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
   float* accbuf = nv > 1 ? reinterpret_cast<float*>(ws + align_up((size_t)C * Cv * es)) : nullptr;
   char* XcT = ws + align_up((size_t)C * Cv * es) +
               (nv > 1 ? align_up((size_t)C * H * sizeof(float)) : 0);
+  uint32_t* queue = reinterpret_cast<uint32_t*>(XcT + align_up((size_t)H * C * es));
   const int64_t ldg_b = Cv * es, ldxt_b = C * es;
 
   for (int64_t c0 = 0; c0 < N; c0 += C) {
@@ -571,6 +573,7 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       r.ldg_b = ldg_b;
       r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
+      if constexpr (sizeof(T) == 2) r.zero_words = queue;
       if constexpr (sizeof(T) == 2) {
         static void (*const kerns[2][2][2])(RecompArgs) = {
             {{recompute_bf16_kernel<false, false, false>, recompute_bf16_kernel<false, false, true>},
@@ -618,6 +621,10 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       // tests reach the one-after-the-other form)
       const int64_t cus = grid_cap() > 0 ? std::min(grid_cap(), device_cus()) : device_cus();
       const bool beside = sizeof(T) == 2 && (int64_t)x.tiles_m * x.tiles_n < cus;
+      // dW beside dX over the work queue (as on the fused path), which the
+      // recompute launch just before the fork clears
+      const bool use_queue = beside && cdiv(cv, 256) * cdiv(H, 256) >= 4 * device_cus() &&
+                             device_cus() % kQueueWords == 0 && cn > kBKBf;
       if (!beside) {
         if constexpr (sizeof(T) == 2) {
           const int px = prof_begin(dx_name(x.mode), dx_flops(x), 0, stream);
@@ -647,6 +654,7 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
       w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
       w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
+      if (use_queue) w.queue = queue;
       if (beside) {
         // the next block's recompute (G) and gather (X^T) follow the join
         MT_TRY(launch_dx_dw_bf16(x, w, stream));

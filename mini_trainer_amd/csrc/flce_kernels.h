@@ -321,6 +321,7 @@ struct RecompArgs {
   char* G;         // [tiles_m * 256][>= tiles_n * 256], row pitch ldg_b
   int64_t ldg_b;
   int32_t tiles_m, tiles_n;
+  uint32_t* zero_words = nullptr;  // cleared by the launch (dW's work queue, read after it)
 };
 
 template <typename T>

@@ -436,6 +436,8 @@ __device__ __forceinline__ void recompute_epilogue_bf16(const f32x4_t (&acc)[8][
 template <bool kCap, bool kTail, bool kKTail>
 MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  if (a.zero_words && blockIdx.x == 0 && threadIdx.x < (uint32_t)kQueueWords)
+    a.zero_words[threadIdx.x] = 0u;
   const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
   const EpiCoordsBf ec0;
   const int KT = (a.H + kBKBf - 1) / kBKBf;

@@ -132,8 +132,10 @@ def test_backward_plan_fits_budget(key):
     assert C % 256 == 0 and Cv % 256 == 0 and C >= 256 and Cv >= 256
     assert ws <= 0.05 * cfg.T * cfg.V * es
     # the workspace formula: G block + fp32 dX accumulator (if V is split) + X^T block
+    # + (bf16) the 8 counters of dW's work queue
     al = lambda b: (b + 255) // 256 * 256  # noqa: E731
-    expect = al(C * Cv * es) + (al(C * cfg.H * 4) if Cv < cfg.V else 0) + al(cfg.H * C * es)
+    expect = (al(C * Cv * es) + (al(C * cfg.H * 4) if Cv < cfg.V else 0) + al(cfg.H * C * es) +
+              (al(8 * 4) if es == 2 else 0))
     assert ws == expect
 
 
