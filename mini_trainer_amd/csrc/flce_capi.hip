@@ -270,8 +270,24 @@ inline const char* dx_name(int mode) {
 inline void launch_dx_bf16(const DxArgs& x, hipStream_t stream) {
   static void (*const kern[4])(DxArgs) = {dx_bf16_kernel<kDxStore>, dx_bf16_kernel<kDxAdd>,
                                           dx_bf16_kernel<kDxAddEmit>, dx_bf16_kernel<kDxEmit>};
-  hipLaunchKernelGGL(kern[x.mode & 3], dim3((uint32_t)(x.tiles_m * x.tiles_n)), dim3(kThreadsBf),
-                     0, stream, x);
+  hipLaunchKernelGGL(kern[x.mode & 3], dim3((uint32_t)(x.tiles_m * x.tiles_n * x.nsplit)),
+                     dim3(kThreadsBf), 0, stream, x);
+}
+
+// The sum of a K-split dX's slices, scaled and written as bf16 dX rows.
+struct DxReduce {
+  const float* part = nullptr;
+  int64_t stride = 0, ld = 0;
+  int32_t nsplit = 1, cn = 0, H = 0;
+  const float* scale = nullptr;
+  const int32_t* row_index = nullptr;
+  char* dX = nullptr;
+  int64_t lddx_b = 0;
+};
+inline void launch_dx_reduce(const DxReduce& r, hipStream_t stream) {
+  hipLaunchKernelGGL(dx_split_reduce_kernel, dim3((uint32_t)cdiv(r.H, 1024), (uint32_t)r.cn),
+                     dim3(256), 0, stream, r.part, r.stride, r.nsplit, r.ld, r.cn, r.H, r.scale,
+                     r.row_index, r.dX, r.lddx_b);
 }
 
 // dX and dW of one block side by side: dX (tiles_m x tiles_n workgroups,
@@ -279,8 +295,10 @@ inline void launch_dx_bf16(const DxArgs& x, hipStream_t stream) {
 // dW (one workgroup per tile) on the library's side stream, forked from and
 // joined back to the caller's stream with events, so dW's workgroups take
 // the CUs dX leaves free and then the rest.  Both only read G and the X^T
-// block; whatever rewrites them is enqueued after the join.
-int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream) {
+// block; whatever rewrites them is enqueued after the join.  red (K-split
+// dX): its reduction follows dX on the caller's stream, beside dW.
+int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
+                      const DxReduce* red = nullptr) {
   SideStream* side = nullptr;
   MT_TRY(side_stream(&side));
   std::lock_guard<std::mutex> lock(side->use);
@@ -291,8 +309,9 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream) {
   MT_TRY(hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess
              ? MT_OK
              : fail(MT_ERR_HIP, "hipStreamWaitEvent"));
-  const int px = prof_begin(dx_name(x.mode), fx, 0, stream);
+  const int px = prof_begin(red ? "dx_bf16_kernel<split>" : dx_name(x.mode), fx, 0, stream);
   launch_dx_bf16(x, stream);
+  if (red) launch_dx_reduce(*red, stream);
   prof_end(px, stream);
   MT_TRY(check_launch("dx_bf16_kernel"));
   const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
@@ -367,18 +386,34 @@ size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es) {
 }
 
 // ----------------------------------------------------------------- costs
-// Modelled seconds of `tiles` output tiles (256 x 256) of depth k on the
-// persistent grid.  Whole rounds run at the busy per-CU rate; the CUs a
-// partial round leaves idle are charged 30% of a busy one: under the chip's
-// power limit the others clock up while they idle.
-constexpr double kCuRate = 4.5e12;  // sustained bf16 flop/s of one busy CU
+// Modelled seconds, calibrated on MI355X at configs 2-5 (same-box step
+// times against the model's: within ~10%, and it ranks fused against general
+// right at all four).  A 256 x 256 tile of depth k costs k + 160 K-entries
+// of one busy CU (160: its epilogue); a dW tile that adds into dW costs 640
+// more (the fp32 tile stored and the next one loaded).  Whole rounds run at
+// the busy rate; the CUs a partial round leaves idle are charged 30% of a
+// busy one: under the chip's power limit the others clock up while they
+// idle.
+constexpr double kCuRate = 5.6e12;  // sustained bf16 flop/s of one busy CU
 constexpr double kLaunch = 8e-6, kBw = 5e12;
+constexpr int64_t kEpiK = 160, kDwRmwK = 640;
 
-double gemm_time(int64_t tiles, int64_t k) {
+double tile_time(int64_t k, int64_t extra = 0) {
+  return 2.0 * 256 * 256 * (double)(round_up(k, 64) + kEpiK + extra) / kCuRate;
+}
+
+double gemm_time(int64_t tiles, int64_t k, int64_t extra = 0) {
   if (tiles <= 0) return 0.0;
-  const double tile_time = 2.0 * 256 * 256 * (double)round_up(k, 64) / kCuRate;
   const double full = (double)tiles / kCUs, rounds = std::ceil(full);
-  return (full + 0.3 * (rounds - full)) * tile_time + kLaunch;
+  return (full + 0.3 * (rounds - full)) * tile_time(k, extra) + kLaunch;
+}
+
+// dX (dx_items tiles of depth dx_k, one per CU) beside dW (dw_tiles of depth
+// dw_k over the work queue): the CU time of both spread over the chip, but
+// never shorter than one dX tile.
+double phase_time(int64_t dx_items, int64_t dx_k, int64_t dw_tiles, int64_t dw_k) {
+  const double cu = dx_items * tile_time(dx_k) + dw_tiles * tile_time(dw_k, kDwRmwK);
+  return std::max(cu / kCUs, tile_time(dx_k)) + 2 * kLaunch;
 }
 
 // Modelled seconds for one backward with blocks of C x Cv.
@@ -390,9 +425,12 @@ double backward_cost(int64_t N, int64_t H, int64_t V, int64_t C, int64_t Cv, int
     const int64_t nv = cdiv(V, Cv), tm = cdiv(cn, 256), th = cdiv(H, 256);
     for (int64_t v0 = 0; v0 < V; v0 += Cv) {
       const int64_t cv = std::min(Cv, V - v0), tv = cdiv(cv, 256);
-      t += gemm_time(tm * tv, H) + gemm_time(tm * th, cv) + gemm_time(tv * th, cn);
+      t += gemm_time(tm * tv, H);
+      if (tm * th < kCUs)
+        t += phase_time(tm * th, cv, tv * th, cn);  // dW beside dX
+      else
+        t += gemm_time(tm * th, cv) + gemm_time(tv * th, cn, kDwRmwK);
     }
-    bytes += (double)V * H * 8;                              // dW read-modify-write
     if (nv > 1) bytes += (double)(2 * nv - 2) * cn * H * 4;  // dX accumulator
     t += kLaunch;
   }
@@ -404,17 +442,28 @@ double forward_cost(int64_t N, int64_t H, int64_t V) {
   return gemm_time(cdiv(N, 256) * cdiv(V, 256), H);
 }
 
+// K slices of a fused chunk's dX (fused_split, below)
+struct DxSplit {
+  int64_t S = 1, kslice = 0;
+};
+DxSplit fused_split(int64_t C, int64_t H, int64_t V);
+
 // Modelled seconds of the fused forward + backward with row chunks of C.
+// A chunk of fewer than 4 row tiles streams the weight from HBM for every
+// row tile (few tiles per W block share it in L2): its forward is also
+// bounded by that traffic.
 double fused_cost(int64_t N, int64_t H, int64_t V, int64_t C) {
-  const int64_t vt = cdiv(V, 256), th = cdiv(H, 256), Vp = round_up(V, 256);
-  double t = 0, bytes = 0;
+  const int64_t vt = cdiv(V, 256), th = cdiv(H, 256);
+  const DxSplit sp = fused_split(C, H, V);
+  double t = 0;
   for (int64_t c0 = 0; c0 < N; c0 += C) {
     const int64_t cn = std::min(C, N - c0), tm = cdiv(cn, 256);
-    t += gemm_time(tm * vt, H) + gemm_time(tm * th, V) + gemm_time(vt * th, cn);
-    t += (double)cn * Vp * 2 * 2 / kBw + 4 * kLaunch;  // G formed in place: read + write
-    bytes += (double)V * H * 8 + (double)cn * Vp * 2;  // dW read-modify-write, S stores
+    t += std::max(gemm_time(tm * vt, H), (double)V * H * 2 * 4.0 / std::min<int64_t>(tm, 4) / kBw);
+    t += phase_time(tm * th * sp.S, sp.S > 1 ? sp.kslice : V, vt * th, cn);
+    if (sp.S > 1) t += (double)(sp.S * cn * H * 4 + cn * H * 2) / kBw;  // slice reduction
+    t += 4 * kLaunch;
   }
-  return t + 0.5 * bytes / kBw;
+  return t;
 }
 
 struct BwdPlan {
@@ -693,12 +742,31 @@ struct FusedPlan {
 
 inline int64_t vocab_pad(int64_t V) { return round_up(V, 256); }
 
+// K slices of a fused chunk's dX: dX has only cdiv(C, 256) x cdiv(H, 256)
+// tiles, each contracting the whole vocabulary; with fewer tiles than half
+// the CUs, dX alone would outlast dW beside it, so each tile is split over
+// the vocabulary into enough slices to give dX about half the CUs (at most
+// 8), summed by dx_split_reduce_kernel from fp32 planes of C x H.
+// Slices are whole 64-entry K stages and none is empty.
+DxSplit fused_split(int64_t C, int64_t H, int64_t V) {
+  DxSplit d;
+  const int64_t tiles = cdiv(C, 256) * cdiv(H, 256), cus = device_cus();
+  if (2 * tiles >= cus) return d;
+  const int64_t want = std::min<int64_t>({8, cdiv(cus, 2 * tiles), cdiv(V, 64)});
+  if (want <= 1) return d;
+  d.kslice = round_up(cdiv(V, want), 64);
+  d.S = cdiv(V, d.kslice);
+  if (d.S <= 1) d = DxSplit();
+  return d;
+}
+
 size_t fused_ws(int64_t C, int64_t H, int64_t V) {
   if (C == 0) return 0;
-  const int64_t vt = cdiv(V, 256);
+  const int64_t vt = cdiv(V, 256), S = fused_split(C, H, V).S;
   return align_up((size_t)C * vocab_pad(V) * 2) + align_up((size_t)vt * C * 2 * sizeof(float)) +
          align_up((size_t)C * sizeof(float)) + align_up((size_t)H * C * 2) +
-         align_up((size_t)C * sizeof(float)) + align_up(sizeof(int32_t) + kQueueWords * 4);
+         align_up((size_t)C * sizeof(float)) + align_up(sizeof(int32_t) + kQueueWords * 4) +
+         (S > 1 ? align_up((size_t)S * C * H * sizeof(float)) : 0);
 }
 
 FusedPlan plan_fused(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) {
@@ -749,6 +817,10 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
   int32_t* guard = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(scale) +
                                               align_up((size_t)C * sizeof(float)));
   uint32_t* queue = reinterpret_cast<uint32_t*>(guard + 1);
+  const DxSplit split = fused_split(C, H, V);
+  const int64_t nsplit = split.S;
+  float* dx_part = reinterpret_cast<float*>(reinterpret_cast<char*>(guard) +
+                                            align_up(sizeof(int32_t) + kQueueWords * 4));
   const int64_t lds_b = Vp * 2, ldxt_b = C * 2;
   for (int64_t c0 = 0; c0 < N; c0 += C) {
     const int64_t cn = std::min(C, N - c0);
@@ -842,6 +914,26 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
     x.tiles_m = (int32_t)tm;
     x.tiles_n = (int32_t)cdiv(H, 256);
     x.row_scale = scale;
+    DxReduce red;
+    if (nsplit > 1) {
+      // K slices into fp32 planes of C x H, summed and scaled into dX after
+      x.mode = kDxStore;
+      x.accbuf = dx_part;
+      x.ld_acc = H;
+      x.nsplit = (int32_t)nsplit;
+      x.kslice = (int32_t)split.kslice;
+      x.split_stride = C * H;
+      red.part = dx_part;
+      red.stride = C * H;
+      red.ld = H;
+      red.nsplit = (int32_t)nsplit;
+      red.cn = (int32_t)cn;
+      red.H = (int32_t)H;
+      red.scale = scale;
+      red.row_index = row_index + c0;
+      red.dX = static_cast<char*>(dX);
+      red.lddx_b = lddx * 2;
+    }
     DwArgs w;
     w.G = S;
     w.ldg_b = lds_b;
@@ -867,7 +959,7 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
         cn > kBKBf)
       w.queue = queue;
     // S and XcT are rewritten by the next chunk only after the join
-    MT_TRY(launch_dx_dw_bf16(x, w, stream));
+    MT_TRY(launch_dx_dw_bf16(x, w, stream, nsplit > 1 ? &red : nullptr));
   }
   return MT_OK;
 }

@@ -442,7 +442,33 @@ struct DxArgs {
   const int32_t* row_index;  // offset to the block's first valid row
   int32_t tiles_m, tiles_n;
   const float* row_scale = nullptr;  // non-null (bf16 kDxEmit): dX row r times row_scale[r]
+  // split over K (bf16): nsplit slices of kslice vocabulary entries, slice z
+  // stored (kDxStore) at accbuf + z * split_stride; the grid is
+  // tiles_m * tiles_n * nsplit (dx_split_reduce_kernel sums the slices)
+  int32_t nsplit = 1, kslice = 0;
+  int64_t split_stride = 0;
 };
+
+// dX of a K-split fused chunk: row t < cn, columns h .. h + 3 of the sum of
+// the nsplit fp32 slices (in slice order), times scale[t], to bf16 at dX row
+// row_index[t].  One thread per 4 columns.
+__global__ __launch_bounds__(256) void dx_split_reduce_kernel(const float* part, int64_t stride,
+                                                              int32_t nsplit, int64_t ld, int32_t cn,
+                                                              int32_t H, const float* scale,
+                                                              const int32_t* row_index, char* dX,
+                                                              int64_t lddx_b) {
+  const int32_t t = (int32_t)blockIdx.y;
+  const int32_t h = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (t >= cn || h >= H) return;
+  const float* p = part + (int64_t)t * ld + h;
+  f32x4_t v = *reinterpret_cast<const f32x4_t*>(p);
+  for (int32_t z = 1; z < nsplit; ++z) v += *reinterpret_cast<const f32x4_t*>(p + z * stride);
+  v *= scale[t];
+  u32x2_t o;
+  o[0] = pack_bf16x2(v[0], v[1]);
+  o[1] = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<u32x2_t*>(dX + (int64_t)row_index[t] * lddx_b + (int64_t)h * 2) = o;
+}
 
 template <typename T, int NFN, int WC>
 __device__ __forceinline__ void dx_epilogue(const f32x4_t (&acc)[8][NFN], const DxArgs& a,

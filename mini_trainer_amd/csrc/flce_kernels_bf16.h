@@ -530,28 +530,46 @@ __device__ __forceinline__ void dx_epilogue_bf16(const f32x4_t (&acc)[8][8], con
 template <int kMode>
 MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
-  const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
+  // K split (nsplit > 1): workgroup b takes slice b % nsplit of tile b / nsplit:
+  // the slice's first vocabulary entry becomes K = 0 of E and of W, and its
+  // fp32 result goes to its own plane of accbuf
+  uint32_t b = blockIdx.x, nb = gridDim.x;
+  if (a.nsplit > 1) {
+    const uint32_t z = b % (uint32_t)a.nsplit;
+    b /= (uint32_t)a.nsplit;
+    nb /= (uint32_t)a.nsplit;
+    const int32_t k0 = (int32_t)z * a.kslice;
+    a.G += (int64_t)k0 * 2;
+    a.g_range -= (uint32_t)k0 * 2u;
+    a.W += (int64_t)k0 * a.ldw_b;
+    a.w_range -= (uint32_t)k0 * (uint32_t)a.ldw_b;
+    a.v0 += k0;
+    a.kv = min(a.kslice, a.kv - k0);
+    a.accbuf += (int64_t)z * a.split_stride;
+  }
+  const uint32_t tile = xcd_remap(b, nb);
+  const int ntiles = tile < (uint32_t)(a.tiles_m * a.tiles_n) ? 1 : 0;
   const EpiCoordsBf ec0;
   KcOp A;
   TrOp B;
   A.init_frag(ec0.wm * 128);
   mainloop_bf16<false>(
-      lds, A, B, (a.kv + kBKBf - 1) / kBKBf, seq.count() > 0 ? 1 : 0,
-      [&](int k) __attribute__((always_inline)) {
+      lds, A, B, (a.kv + kBKBf - 1) / kBKBf, ntiles,
+      [&](int) __attribute__((always_inline)) {
         uint32_t tm, tn;
-        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        grouped_tile(tile, a.tiles_m, a.tiles_n, 4, tm, tn);
         const int32_t row0 = (int32_t)tm * 256, h0 = (int32_t)tn * 256;
         A.set_rows(make_rsrc(a.G, a.g_range), [&](uint32_t r) __attribute__((always_inline)) {
           return (uint32_t)(row0 + (int32_t)r) * (uint32_t)a.ldg_b;
         });
-        // W points at the block's first vocabulary row (v0)
+        // W points at the block's (or slice's) first vocabulary row (v0)
         B.init(make_rsrc(a.W, a.w_range), (uint32_t)h0 * 2u, (uint32_t)a.ldw_b, a.V - a.v0,
                a.H - h0, ec0.wn * 128);
       },
-      [&](int k, f32x4_t(&acc)[8][8], char* scratch) __attribute__((always_inline)) {
+      [&](int, f32x4_t(&acc)[8][8], char*) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tn;
-        grouped_tile(seq.logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
+        grouped_tile(tile, a.tiles_m, a.tiles_n, 4, tm, tn);
         dx_epilogue_bf16<kMode>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
       });
 }
