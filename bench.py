@@ -17,7 +17,8 @@ Prints ONE JSON line (driver contract) with, in addition:
                 dW GEMMs of each fused chunk: 2*C*V*H flops each, fork to
                 join), timed live with the library's per-launch HIP events on
                 the streams the kernels run on, against the bf16 dense peak;
-                `kernels` lists every kernel of the step the same way;
+                `kernels` lists every kernel of the step the same way (with
+                the GEMMs' calibrated counter bytes per dispatch);
                 traffic = HBM bytes per launch from the committed rocprofv3
                 FETCH_SIZE / WRITE_SIZE summary (profiles/)
   cpu_baseline  the reference torch path (oracle/torch_path.py) on the host
@@ -137,19 +138,34 @@ def torch_gpu_path(data, W, scale: float, steps: int = 2):
             "path": "F.linear -> .float() -> F.cross_entropy(reduction='none') -> backward (torch on the GPU)"}
 
 
-def measured_traffic(key: int, unit: str):
-    """HBM bytes per launch of the roofline unit, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload (calibrated
-    against a 1 GiB device copy), or None when no summary covers it."""
+def traffic_summary(key: int):
+    """The committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this
+    workload (bytes calibrated against a 1 GiB device copy), or None."""
     path = os.path.join(ROOT, "profiles", f"flce_cfg{key}_traffic.json")
     try:
         with open(path) as f:
-            t = json.load(f)
+            return json.load(f)
     except (OSError, ValueError):
         return None
-    if t.get("unit") != unit:
+
+
+def measured_traffic(key: int, unit: str):
+    """HBM bytes per launch of the roofline unit from that summary, or None
+    when no summary covers it."""
+    t = traffic_summary(key)
+    if not t or t.get("unit") != unit:
         return None
     return t.get("traffic_bytes")
+
+
+def add_counter_bytes(kernels: dict, key: int) -> None:
+    """Per-dispatch read / written bytes of the summary's kernels (same
+    names as the event report) beside their event timings."""
+    t = traffic_summary(key) or {}
+    for name, b in t.get("per_kernel", {}).items():
+        if name in kernels:
+            kernels[name]["counter_read_GB_per_launch"] = b["read_bytes"] / 1e9
+            kernels[name]["counter_write_GB_per_launch"] = b["write_bytes"] / 1e9
 
 
 def copy_calibration():
@@ -428,6 +444,7 @@ def main():
     roof, kernels = roofline_of(report, peak_flops, args.steps)
     if roof is not None:
         roof["traffic"] = measured_traffic(cfg.key, roof["kernel"])
+    add_counter_bytes(kernels, cfg.key)
     log(f"profiled step: {ms_prof:.2f} ms; roofline unit {roof and roof['kernel']}")
 
     north = {
