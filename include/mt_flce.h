@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define MT_FLCE_ABI_VERSION 3
+#define MT_FLCE_ABI_VERSION 4
 
 typedef struct ihipStream_t* mt_stream_t; /* == hipStream_t */
 
@@ -220,6 +220,51 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
                   float* loss, float* lse, void* dX, int64_t lddx, float* dW,
                   int64_t lddw, int accumulate_dW, int64_t chunk_rows,
                   void* workspace, size_t workspace_bytes, mt_stream_t stream);
+
+/*
+ * Bytes of the tiled fp32 weight gradient that mt_flce_fused_tiles forms
+ * (0 for sizes out of range): a pad of 256 * round_up(H, 256) bf16 elements,
+ * then ceil(V/256) x ceil(H/256) tiles of 256 x 256 fp32 in the order the
+ * dW GEMM holds them.  At least V * H * 4, so the same allocation also
+ * serves as a row-major fp32 [V, H] (mt_flce_backward's recompute for a
+ * per-token gradient).  No counterpart in the reference.
+ */
+size_t mt_flce_dw_tiles_bytes(int64_t V, int64_t H);
+
+/*
+ * mt_flce_fused with dW formed as tiles (layout of mt_flce_dw_tiles_bytes)
+ * instead of rows: every load and store of the dW GEMM's accumulators is one
+ * contiguous KiB, without the transpose a row-major tile edge needs.  Same
+ * arithmetic, so mt_flce_narrow_tiles of the result equals mt_flce_fused +
+ * mt_flce_scale_grads bit for bit.  dW is never accumulated into (a
+ * dw_accumulator stays on mt_flce_fused).  Replaces the same reference
+ * interface as mt_flce_fused (none_reduction_losses.py:16-23 -> LIGER's
+ * fused_linear_cross_entropy_forward, whose grad_weight is the tensor here).
+ */
+int mt_flce_fused_tiles(const void* X, const void* W, int64_t T, int64_t H,
+                        int64_t V, int64_t ldx, int64_t ldw, int dtype,
+                        float softcap, const int32_t* row_index,
+                        const int32_t* row_label, int64_t n_valid,
+                        const float* grad_loss, int64_t grad_stride, float* loss,
+                        float* lse, void* dX, int64_t lddx, float* dW_tiles,
+                        size_t dw_tiles_bytes, int64_t chunk_rows,
+                        void* workspace, size_t workspace_bytes,
+                        mt_stream_t stream);
+
+/*
+ * scale * tiled dW -> bf16 rows [V, H] of pitch ldo (the weight gradient in
+ * the weight's dtype); the tiled counterpart of mt_flce_scale_grads's dW
+ * part (LIGER's fused_linear_cross_entropy_backward: grad_weight times
+ * grad_output[0]).  dW_out is either a separate buffer or dW_tiles itself
+ * (ldo <= round_up(H, 256)): in place, row r lands at element r * ldo from
+ * the base, and the tile rows are narrowed in launches {0}, {1}, [2, 4),
+ * [4, 8), ... so that none is overwritten before it is read.  bf16 only,
+ * H % 8 == 0; rounds to nearest even.  scale fp32 [1] on the device.
+ */
+int mt_flce_narrow_tiles(const float* scale, const float* dW_tiles,
+                         size_t dw_tiles_bytes, int64_t V, int64_t H,
+                         void* dW_out, int64_t ldo, int dtype_out,
+                         mt_stream_t stream);
 
 /*
  * Per-sample sums over a packed batch (no counterpart in the reference, which

@@ -319,11 +319,11 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
   if (w.queue) {
     // persistent over the work queue: one workgroup per CU (a multiple of
     // the 8 XCDs), each tile >= 2 K stages (dw_bf16_kernel<true>)
-    hipLaunchKernelGGL(dw_bf16_kernel<true>, dim3((uint32_t)device_cus()), dim3(kThreadsBf), 0,
-                       side->stream, w);
+    void (*kern)(DwArgs) = w.tiled ? dw_bf16_kernel<true, true> : dw_bf16_kernel<true, false>;
+    hipLaunchKernelGGL(kern, dim3((uint32_t)device_cus()), dim3(kThreadsBf), 0, side->stream, w);
   } else {
-    hipLaunchKernelGGL(dw_bf16_kernel<false>,
-                       dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
+    void (*kern)(DwArgs) = w.tiled ? dw_bf16_kernel<false, true> : dw_bf16_kernel<false, false>;
+    hipLaunchKernelGGL(kern, dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
                        dim3(kThreadsBf), 0, side->stream, w);
   }
   prof_end(pw, side->stream);
@@ -710,7 +710,8 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       } else {
         if constexpr (sizeof(T) == 2) {
           const int pw = prof_begin("dw_bf16_kernel", dw_flops(w), 0, stream);
-          hipLaunchKernelGGL(dw_bf16_kernel<false>, dim3(persistent_grid(w.tiles_m * w.tiles_n)),
+          void (*kern)(DwArgs) = dw_bf16_kernel<false, false>;
+          hipLaunchKernelGGL(kern, dim3(persistent_grid(w.tiles_m * w.tiles_n)),
                              dim3(kThreadsBf), 0, stream, w);
           prof_end(pw, stream);
         } else
@@ -760,6 +761,17 @@ DxSplit fused_split(int64_t C, int64_t H, int64_t V) {
   return d;
 }
 
+// Tiled fp32 dW: 256 x 256 tiles (the grid padded to whole tiles), each
+// 256 KiB in the accumulators' own order, row-major over the tile grid,
+// after a leading pad of half a tile row (256 * Hp bf16 elements): the
+// bf16 rows narrowed out of tile row r then end at or before tile row r / 2
+// starts, so tile rows narrowed in launches {0}, {1}, [2, 4), [4, 8), ...
+// only overwrite tiles an earlier launch has read.
+int64_t dw_tiles_pad(int64_t H) { return 128 * round_up(H, 256); }  // floats
+size_t dw_tiles_bytes(int64_t V, int64_t H) {
+  return (size_t)dw_tiles_pad(H) * 4 + (size_t)cdiv(V, 256) * cdiv(H, 256) * 65536 * 4;
+}
+
 size_t fused_ws(int64_t C, int64_t H, int64_t V) {
   if (C == 0) return 0;
   const int64_t vt = cdiv(V, 256), S = fused_split(C, H, V).S;
@@ -805,8 +817,8 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
                  int64_t ldw,
                  float softcap, const int32_t* row_index, const int32_t* row_label, int64_t N,
                  const float* grad, int64_t gstride, float* loss, float* lse, void* dX,
-                 int64_t lddx, float* dW, int64_t lddw, int accumulate, int64_t C, char* ws,
-                 hipStream_t stream) {
+                 int64_t lddx, float* dW, int64_t lddw, int accumulate, bool tiled, int64_t C,
+                 char* ws, hipStream_t stream) {
   const int64_t Vp = vocab_pad(V), vt = cdiv(V, 256);
   char* S = ws;
   float* part = reinterpret_cast<float*>(ws + align_up((size_t)C * Vp * 2));
@@ -952,6 +964,11 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
     w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
     w.tiles_m = (int32_t)vt;
     w.tiles_n = (int32_t)cdiv(H, 256);
+    if (tiled) {
+      w.tiled = 1;
+      w.tile_pad = dw_tiles_pad(H);
+      w.lddw = 0;
+    }
     // the work queue pays where the tiles outnumber the CUs several times
     // and each has at least two K stages
     // (one workgroup per CU covers the 8 XCD shares only for a multiple of 8 CUs)
@@ -1216,12 +1233,18 @@ int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dty
   return MT_OK;
 }
 
-int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
-                  int64_t ldw, int dtype, float softcap, const int32_t* row_index,
-                  const int32_t* row_label, int64_t n_valid, const float* grad_loss,
-                  int64_t grad_stride, float* loss, float* lse, void* dX, int64_t lddx, float* dW,
-                  int64_t lddw, int accumulate_dW, int64_t chunk_rows, void* workspace,
-                  size_t workspace_bytes, mt_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// mt_flce_fused (row-major dW, lddw > 0) and mt_flce_fused_tiles (tiled dW
+// of dw_tiles_bytes, lddw == 0, never accumulated into).
+int fused_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                int64_t ldw, int dtype, float softcap, const int32_t* row_index,
+                const int32_t* row_label, int64_t n_valid, const float* grad_loss,
+                int64_t grad_stride, float* loss, float* lse, void* dX, int64_t lddx, float* dW,
+                int64_t lddw, int accumulate_dW, bool tiled, int64_t chunk_rows, void* workspace,
+                size_t workspace_bytes, mt_stream_t stream) {
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "the fused path is bf16 only (dtype %d)", dtype);
   MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
@@ -1231,7 +1254,7 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
                 "MT_FLCE_MAX_BUFFER_BYTES); use mt_flce_forward + mt_flce_backward");
   if (n_valid < 0 || n_valid > T)
     return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
-  if (lddx < H || lddw < H)
+  if (lddx < H || (!tiled && lddw < H))
     return fail(MT_ERR_INVALID_ARGUMENT, "lddx=%lld / lddw=%lld must be >= H", (long long)lddx, (long long)lddw);
   if ((lddx * 2) % 16 != 0 || (lddw * 4) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "dX / dW row pitches must be multiples of 16 bytes");
@@ -1267,7 +1290,12 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
     MT_TRY(check_launch("zero_rows_kernel"));
   }
   if (n_valid == 0) {
-    if (!accumulate_dW) {
+    if (tiled) {  // every tile, as 1 KiB rows
+      const int64_t rows = cdiv(V, 256) * cdiv(H, 256) * 256;
+      hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(rows, 8192)), dim3(256),
+                         0, s, dW + dw_tiles_pad(H), rows, (int64_t)256, (int64_t)256);
+      MT_TRY(check_launch("zero_matrix_f32_kernel"));
+    } else if (!accumulate_dW) {
       hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
                          s, dW, V, H, lddw);
       MT_TRY(check_launch("zero_matrix_f32_kernel"));
@@ -1275,8 +1303,42 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
     return MT_OK;
   }
   return launch_fused(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, grad_loss,
-                      grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, chunk_rows,
+                      grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, tiled, chunk_rows,
                       static_cast<char*>(workspace), s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                  int64_t ldw, int dtype, float softcap, const int32_t* row_index,
+                  const int32_t* row_label, int64_t n_valid, const float* grad_loss,
+                  int64_t grad_stride, float* loss, float* lse, void* dX, int64_t lddx, float* dW,
+                  int64_t lddw, int accumulate_dW, int64_t chunk_rows, void* workspace,
+                  size_t workspace_bytes, mt_stream_t stream) {
+  return fused_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid,
+                     grad_loss, grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, false,
+                     chunk_rows, workspace, workspace_bytes, stream);
+}
+
+size_t mt_flce_dw_tiles_bytes(int64_t V, int64_t H) {
+  if (V <= 0 || H <= 0 || V > INT32_MAX || H > INT32_MAX) return 0;
+  return dw_tiles_bytes(V, H);
+}
+
+int mt_flce_fused_tiles(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                        int64_t ldw, int dtype, float softcap, const int32_t* row_index,
+                        const int32_t* row_label, int64_t n_valid, const float* grad_loss,
+                        int64_t grad_stride, float* loss, float* lse, void* dX, int64_t lddx,
+                        float* dW_tiles, size_t dw_tiles_bytes_, int64_t chunk_rows,
+                        void* workspace, size_t workspace_bytes, mt_stream_t stream) {
+  if (H > 0 && V > 0 && dw_tiles_bytes_ < dw_tiles_bytes(V, H))
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles %zu bytes < mt_flce_dw_tiles_bytes = %zu",
+                dw_tiles_bytes_, dw_tiles_bytes(V, H));
+  return fused_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid,
+                     grad_loss, grad_stride, loss, lse, dX, lddx, dW_tiles, 0, 0, true, chunk_rows,
+                     workspace, workspace_bytes, stream);
 }
 
 int mt_segment_sum(const float* loss, const int64_t* target, int64_t T, int64_t ignore_index,
@@ -1381,6 +1443,47 @@ int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H, int6
     prof_end(p, s);
     MT_TRY(check_launch("scale_rows_kernel"));
   }
+  return MT_OK;
+}
+
+int mt_flce_narrow_tiles(const float* scale, const float* dW_tiles, size_t dw_tiles_bytes_,
+                         int64_t V, int64_t H, void* dW_out, int64_t ldo, int dtype_out,
+                         mt_stream_t stream) {
+  if (dtype_out != MT_DTYPE_BF16)
+    return fail(MT_ERR_UNSUPPORTED, "tiled dW narrows to bf16 only (dtype_out %d)", dtype_out);
+  if (V <= 0 || H <= 0 || V > INT32_MAX || H > INT32_MAX)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes H=%lld V=%lld", (long long)H, (long long)V);
+  if (H % 8 != 0) return fail(MT_ERR_UNSUPPORTED, "tiled dW narrowing needs H %% 8 == 0 (H=%lld)", (long long)H);
+  if (!scale || !dW_tiles || !dW_out) return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (dw_tiles_bytes_ < dw_tiles_bytes(V, H))
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles %zu bytes < mt_flce_dw_tiles_bytes = %zu",
+                dw_tiles_bytes_, dw_tiles_bytes(V, H));
+  if (ldo < H || ldo > (int64_t)1 << 22 || (ldo * 2) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "ldo=%lld: needs H <= ldo <= 2^22, 16-byte row pitch", (long long)ldo);
+  if ((reinterpret_cast<uintptr_t>(dW_tiles) | reinterpret_cast<uintptr_t>(dW_out)) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles and dW_out must be 16-byte aligned");
+  const int64_t tn = cdiv(H, 256), vt = cdiv(V, 256);
+  const char *t0 = static_cast<const char*>(static_cast<const void*>(dW_tiles)),
+             *t1 = t0 + dw_tiles_bytes(V, H);
+  const char *o0 = static_cast<const char*>(dW_out), *o1 = o0 + ((V - 1) * ldo + H) * 2;
+  const bool inplace = o0 == t0;
+  if (inplace && ldo > tn * 256)
+    return fail(MT_ERR_INVALID_ARGUMENT, "in-place narrowing needs ldo <= round_up(H, 256)");
+  if (!inplace && o0 < t1 && t0 < o1)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_out partially overlaps dW_tiles");
+  hipStream_t s = (hipStream_t)stream;
+  const float* tiles = dW_tiles + dw_tiles_pad(H);
+  const int p = prof_begin("narrow_tiles_kernel<dW>", 0, (double)V * H * 6, s);
+  // in place: tile rows {0}, {1}, [2, 4), ... one launch each (the bf16
+  // rows of tile row r end where tile row r / 2 starts); else one launch
+  for (int64_t lo = 0, hi = inplace ? 1 : vt; lo < vt; lo = hi, hi = std::max<int64_t>(2 * lo, lo + 1)) {
+    const int64_t r1 = std::min(hi, vt);
+    hipLaunchKernelGGL(narrow_tiles_kernel, dim3((uint32_t)((r1 - lo) * tn)), dim3(kThreadsBf), 0, s,
+                       scale, tiles, (int32_t)lo, (int32_t)tn, (int32_t)V, (int32_t)H,
+                       static_cast<char*>(dW_out), ldo * 2);
+    MT_TRY(check_launch("narrow_tiles_kernel"));
+  }
+  prof_end(p, s);
   return MT_OK;
 }
 

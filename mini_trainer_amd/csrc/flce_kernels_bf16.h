@@ -598,6 +598,18 @@ __device__ __forceinline__ DwTile dw_tile(const DwArgs& a, int32_t m0, int32_t h
   return t;
 }
 
+// Tiled dW (DwArgs::tiled): a tile's 256 KiB are contiguous and ordered by
+// wave, fragment and lane, so every load and store of the accumulators is
+// one contiguous KiB per instruction -- no transpose, no bounds (the tile
+// grid is padded; rows past V and columns past H are never read back).
+__device__ __forceinline__ rsrc_t dw_tiled_rsrc(const DwArgs& a, int32_t m0, int32_t h0) {
+  const int64_t tile = (int64_t)(m0 / 256) * a.tiles_n + h0 / 256;
+  return make_rsrc(a.dW + a.tile_pad + tile * 65536, 262144u);
+}
+__device__ __forceinline__ uint32_t dw_tiled_off(const EpiCoordsBf& ec, int fm, int fn) {
+  return ((((ec.wm * 2u + ec.wn) * 64u + (uint32_t)fm * 8u + (uint32_t)fn) * 64u) + ec.lane) * 16u;
+}
+
 // Accumulators of tile (m0, h0) from dW (or zero), fragment row fm of the
 // wave (its fragments' 16 rows x 4 columns per lane).
 __device__ __forceinline__ void dw_load_row(f32x4_t (&accrow)[8], const DwArgs& a,
@@ -613,9 +625,21 @@ __device__ __forceinline__ void dw_load_row(f32x4_t (&accrow)[8], const DwArgs& 
   }
 }
 
+template <bool kTiled>
 __device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& a,
                                             const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                             bool load) {
+  if constexpr (kTiled) {
+    const rsrc_t r = dw_tiled_rsrc(a, m0, h0);
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn)
+        acc[fm][fn] = load ? __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          r, dw_tiled_off(ec, fm, fn), 0, 0))
+                           : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    return;
+  }
   const DwTile t = dw_tile(a, m0, h0);
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) dw_load_row(acc[fm], a, ec, t, fm, load);
@@ -654,9 +678,22 @@ __device__ __forceinline__ void dw_store_row(const f32x4_t (&accrow)[8], const D
   }
 }
 
+template <bool kTiled>
 __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const DwArgs& a,
                                              const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                              char* scratch) {
+  if constexpr (kTiled) {
+    const rsrc_t r = dw_tiled_rsrc(a, m0, h0);
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[fm][fn]), r,
+                                               dw_tiled_off(ec, fm, fn), 0, 0);
+      sched_fence();
+    }
+    return;
+  }
   const DwTile t = dw_tile(a, m0, h0);
   char* R = scratch + (ec.wm * 2u + ec.wn) * 8192u;
 #pragma unroll
@@ -673,9 +710,28 @@ __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const D
 // loads of the next tile's starting values into the same accumulators, so
 // that the loads' latency runs beside the remaining stores instead of
 // before the next tile's first multiplication.
+template <bool kTiled>
 __device__ __forceinline__ void dw_store_then_load(f32x4_t (&acc)[8][8], const DwArgs& a,
                                                    const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                                    char* scratch, int32_t nm0, int32_t nh0) {
+  if constexpr (kTiled) {
+    const rsrc_t r = dw_tiled_rsrc(a, m0, h0), nr = dw_tiled_rsrc(a, nm0, nh0);
+    const bool load = a.accumulate != 0;
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[fm][fn]), r,
+                                               dw_tiled_off(ec, fm, fn), 0, 0);
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn)
+        acc[fm][fn] = load ? __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          nr, dw_tiled_off(ec, fm, fn), 0, 0))
+                           : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      sched_fence();
+    }
+    return;
+  }
   const DwTile t = dw_tile(a, m0, h0), nt = dw_tile(a, nm0, nh0);
   char* R = scratch + (ec.wm * 2u + ec.wn) * 8192u;
 #pragma unroll
@@ -769,7 +825,7 @@ struct DwQueue {
 // B = X^T rows of the block (256 hidden rows).  kQueue: persistent over the
 // work queue above (grid = one workgroup per CU, K >= 2 stages); otherwise
 // one workgroup per tile or a static persistent schedule (TileSeq).
-template <bool kQueue>
+template <bool kQueue, bool kTiled>
 MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
   const uint32_t total = (uint32_t)(a.tiles_m * a.tiles_n);
@@ -818,10 +874,10 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
         if (next) {
           uint32_t ntm, ntn;
           grouped_tile(logical(k + 1), a.tiles_m, a.tiles_n, 4, ntm, ntn);
-          dw_store_then_load(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch,
-                             (int32_t)ntm * 256, (int32_t)ntn * 256);
+          dw_store_then_load<kTiled>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch,
+                                     (int32_t)ntm * 256, (int32_t)ntn * 256);
         } else {
-          dw_store_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch);
+          dw_store_acc<kTiled>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch);
         }
       },
       // init: the first tile's starting values
@@ -830,8 +886,66 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
         uint32_t tm, tn;
         grouped_tile(logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         if constexpr (kQueue) q.ask();
-        dw_load_acc(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0);
+        dw_load_acc<kTiled>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0);
       });
+}
+
+// Tiled fp32 dW (dw_bf16_kernel<*, true>) times *scale, narrowed to bf16 rows
+// of pitch ldo_b bytes at `out` (V rows, H columns, H a multiple of 8): one
+// workgroup per tile of tile rows tr0, tr0 + 1, ... (gridDim.x / tiles_n of
+// them).  Each lane reads its fragment pairs (fn = 2p, 2p + 1) as contiguous
+// KiB and, after one v_permlane16_swap per dword (the pairing the forward
+// uses for its chunk of exponentials), writes 8 consecutive columns.  The
+// output resource of a tile ends at its last element; lanes outside the
+// tile (rows past V, columns past H) get an offset past that end.
+__global__ __launch_bounds__(256) void narrow_tiles_kernel(const float* scale, const float* tiles,
+                                                           int32_t tr0, int32_t tiles_n, int32_t V,
+                                                           int32_t H, char* out, int64_t ldo_b) {
+  const int32_t tile = tr0 * tiles_n + (int32_t)blockIdx.x;
+  const int32_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
+  const uint32_t rows = (uint32_t)min(256, V - tm * 256), cols = (uint32_t)min(256, H - tn * 256);
+  const float sc = *scale;
+  const EpiCoordsBf ec;
+  const rsrc_t src = make_rsrc(tiles + (int64_t)tile * 65536, 262144u);
+  const rsrc_t dst = make_rsrc(out + (int64_t)tm * 256 * ldo_b + (int64_t)tn * 512,
+                               (rows - 1u) * (uint32_t)ldo_b + cols * 2u);
+  const uint32_t q = ec.lane >> 4;
+  const uint32_t scol = ec.wn * 128u + 8u * (2u * (q & 1u) + (q >> 1));
+  // the next fragment row's loads go out before this row's stores: loads and
+  // stores share one in-order counter, so a load issued after a store would
+  // wait for that store too
+  f32x4_t cur[8], nxt[8];
+#pragma unroll
+  for (int fn = 0; fn < 8; ++fn)
+    cur[fn] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src, dw_tiled_off(ec, 0, fn), 0, 0));
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const uint32_t row = (uint32_t)ec.row(fm);
+    if (fm < 7) {
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn)
+        nxt[fn] = __builtin_bit_cast(
+            f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src, dw_tiled_off(ec, fm + 1, fn), 0, 0));
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const f32x4_t v0 = cur[2 * p], v1 = cur[2 * p + 1];
+      const auto l2 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(v0[0] * sc, v0[1] * sc),
+                                                       pack_bf16x2(v1[0] * sc, v1[1] * sc), false, false);
+      const auto h2 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(v0[2] * sc, v0[3] * sc),
+                                                       pack_bf16x2(v1[2] * sc, v1[3] * sc), false, false);
+      u32x4_t o;
+      o[0] = l2[0];
+      o[1] = h2[0];
+      o[2] = l2[1];
+      o[3] = h2[1];
+      const uint32_t col = scol + 32u * (uint32_t)p;
+      const uint32_t off = row < rows && col < cols ? row * (uint32_t)ldo_b + col * 2u : kDwOut;
+      __builtin_amdgcn_raw_buffer_store_b128(o, dst, off, 0, 0);
+    }
+#pragma unroll
+    for (int fn = 0; fn < 8; ++fn) cur[fn] = nxt[fn];
+  }
 }
 
 // Fused path, chunks whose exponentials would leave bf16's range: G = g_t

@@ -163,18 +163,23 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
     fused       grad_scale promised the upstream gradient at the forward and
                 the planner expects the fused path to pay (bf16,
                 mt_flce_fused_plan): the forward also forms dX and dW for it
-                (mt_flce_fused); the backward checks the gradient it receives
-                against the promise and hands the stored gradients to autograd.
+                (mt_flce_fused into dw_accumulator, else mt_flce_fused_tiles:
+                dW as 256 x 256 fp32 tiles); the backward checks the gradient
+                it receives against the promise and hands the stored
+                gradients to autograd (tiles narrowed by mt_flce_narrow_tiles).
     fused_unit  no promise, no dw_accumulator, bf16, the planner expects the
                 fused path to pay: the forward forms dX and dW for a unit
                 upstream gradient -- the structure of the reference's fused
                 loss (none_reduction_losses.py:16-23 -> Liger's
                 fused_linear_cross_entropy_forward), which train.py:97-104
-                drives unchanged.  The backward multiplies them by the upstream
-                gradient when it is one scalar for every token (stride 0, what
-                sum() / mean() and train.py's scaling give; mt_flce_scale_grads
-                reads it on the device), and otherwise recomputes with the
-                saved lse (mt_flce_backward), exact for any per-token gradient.
+                drives unchanged (mt_flce_fused_tiles).  The backward
+                multiplies them by the upstream gradient when it is one scalar
+                for every token (stride 0, what sum() / mean() and train.py's
+                scaling give; mt_flce_scale_grads for dX and
+                mt_flce_narrow_tiles for dW read it on the device), and
+                otherwise recomputes with the saved lse (mt_flce_backward into
+                the tiles' allocation as a row-major fp32 [V, H]), exact for
+                any per-token gradient.
     """
 
     @staticmethod
@@ -198,16 +203,24 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
             else:
                 g, gstride = torch.ones(1, dtype=torch.float32, device=dev), 0
             dX = torch.empty((T, H), dtype=X.dtype, device=dev)
-            if dw_accumulator is not None:
-                dW, accumulate = dw_accumulator, 1
-            else:
-                dW, accumulate = torch.empty((V, H), dtype=torch.float32, device=dev), 0
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-            check(lib.mt_flce_fused(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
-                                    float(softcap), _p(row_index), _p(row_label), n, _p(g),
-                                    gstride, _p(loss), _p(lse), _p(dX), dX.stride(0), _p(dW),
-                                    dW.stride(0), accumulate, C, _p(ws), ws_bytes, _stream(dev)),
-                  "mt_flce_fused")
+            if dw_accumulator is not None:
+                dW = dw_accumulator
+                check(lib.mt_flce_fused(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
+                                        float(softcap), _p(row_index), _p(row_label), n, _p(g),
+                                        gstride, _p(loss), _p(lse), _p(dX), dX.stride(0), _p(dW),
+                                        dW.stride(0), 1, C, _p(ws), ws_bytes, _stream(dev)),
+                      "mt_flce_fused")
+            else:
+                # dW as 256 x 256 tiles (mt_flce_dw_tiles_bytes), narrowed into
+                # the weight's dtype at the start of the same allocation later
+                tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+                dW = torch.empty(tb // 4, dtype=torch.float32, device=dev)
+                check(lib.mt_flce_fused_tiles(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0),
+                                              dt, float(softcap), _p(row_index), _p(row_label),
+                                              n, _p(g), gstride, _p(loss), _p(lse), _p(dX),
+                                              dX.stride(0), _p(dW), tb, C, _p(ws), ws_bytes,
+                                              _stream(dev)), "mt_flce_fused_tiles")
             del ws
             if ctx.path == "fused":
                 ctx.save_for_backward(row_index, g)
@@ -215,6 +228,7 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
                 ctx.save_for_backward(X, W, row_index, row_label, lse)
             ctx.meta = (n, gstride, hidden.shape, float(softcap), dt)
             ctx.w_dtype = weight.dtype
+            ctx.w_shape = (V, H)
             ctx.dX = dX
             ctx.dW = None if dw_accumulator is not None else dW
             ctx.fused_consumed = False
@@ -292,8 +306,10 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         ctx.dX = ctx.dW = None
         ctx.fused_consumed = True
         grad_x = dX.view(hshape) if ctx.needs_input_grad[0] else None
-        grad_w = (_weight_grad_in_dtype(dW, ctx.w_dtype)
-                  if ctx.needs_input_grad[1] and dW is not None else None)
+        grad_w = None
+        if ctx.needs_input_grad[1] and dW is not None:
+            one = torch.ones(1, dtype=torch.float32, device=dW.device)
+            grad_w = _tiles_in_dtype(dW, ctx.w_shape, one)
         return (grad_x, grad_w) + (None,) * 7
 
 
@@ -317,25 +333,28 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         g, gstride = _grad_vector(grad_loss, T)
         if gstride == 0:
             # one upstream scalar for every token: rescale the unit-gradient
-            # dX and dW, dW straight into the weight's dtype in place
+            # dX in place and narrow the tiled dW, times the scalar, into the
+            # weight's dtype at the start of its own allocation
             scale = g.reshape(-1)[:1]
-            check(lib.mt_flce_scale_grads(_p(scale), _p(dX) if need_x else None,
-                                          T if need_x else 0, H, dX.stride(0), dt, _p(dW),
-                                          V if need_w else 0, dW.stride(0), _p(dW), dW.stride(0),
-                                          _dtype_code(W.dtype), _stream(dev)),
-                  "mt_flce_scale_grads")
-            dW_out = _narrowed_view(dW, W.dtype)
+            if need_x:
+                check(lib.mt_flce_scale_grads(_p(scale), _p(dX), T, H, dX.stride(0), dt, None, 0,
+                                              H, None, H, _dtype_code(W.dtype), _stream(dev)),
+                      "mt_flce_scale_grads")
+            dW_out = _tiles_in_dtype(dW, (V, H), scale) if need_w else None
             del dW
         else:
             # a per-token gradient: the unit-gradient results cannot be
-            # rescaled; recompute into the same buffers
+            # rescaled; recompute into the same buffers (the tiles'
+            # allocation holds a row-major fp32 [V, H])
+            dW = dW[:V * H].view(V, H)
             C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
             check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
                                        softcap, _p(row_index), _p(row_label), n, _p(lse), _p(g),
                                        gstride, _p(dX), dX.stride(0), _p(dW), dW.stride(0), 0, C,
                                        Cv, _p(ws), ws_bytes, _stream(dev)), "mt_flce_backward")
-            dW_out = dW
+            del ws
+            dW_out = _weight_grad_in_dtype(dW, W.dtype) if need_w else None
         grad_x = dX.view(hshape) if need_x else None
         grad_w = dW_out if need_w else None
         return (grad_x, grad_w) + (None,) * 7
@@ -351,6 +370,20 @@ def _narrowed_view(dW: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     out = torch.empty(0, dtype=dtype, device=dW.device)
     # storage offsets count elements: one fp32 element is two 16-bit ones
     out.set_(dW.untyped_storage(), 2 * dW.storage_offset(), (V, H), (dW.stride(0), 1))
+    return out
+
+
+def _tiles_in_dtype(dWt: torch.Tensor, shape: Tuple[int, int],
+                    scale: torch.Tensor) -> torch.Tensor:
+    """scale * the tiled fp32 weight gradient (mt_flce_fused_tiles) as the
+    contiguous bf16 [V, H] that mt_flce_narrow_tiles writes at the start of
+    the tiles' own allocation."""
+    V, H = shape
+    check(load().mt_flce_narrow_tiles(_p(scale), _p(dWt), dWt.numel() * 4, V, H, _p(dWt), H,
+                                      MT_DTYPE_BF16, _stream(dWt.device)), "mt_flce_narrow_tiles")
+    out = torch.empty(0, dtype=torch.bfloat16, device=dWt.device)
+    # storage offsets count elements: one fp32 element is two 16-bit ones
+    out.set_(dWt.untyped_storage(), 2 * dWt.storage_offset(), (V, H), (H, 1))
     return out
 
 

@@ -123,6 +123,44 @@ def test_backward_and_misc_host_checks():
     assert lib.mt_ce_forward(None, 4, 10, 5, 1, None, -100, None, None, None, None) == 1
 
 
+def test_dw_tiles_layout_and_host_checks():
+    """Tiled dW: a pad of 256 * round_up(H, 256) bf16 elements, then whole
+    256 x 256 fp32 tiles -- never less than the row-major fp32 [V, H] the
+    same allocation also serves as.  Argument checks return before any
+    launch."""
+    lib = _lib.load()
+    for V, H in [(100, 64), (256, 256), (65600, 1056), (128256, 4096), (1, 8)]:
+        tb = lib.mt_flce_dw_tiles_bytes(V, H)
+        Hp = -(-H // 256) * 256
+        assert tb == 256 * Hp * 2 + (-(-V // 256)) * (Hp // 256) * 256 * 256 * 4
+        assert tb >= V * H * 4 and tb % 256 == 0
+    assert lib.mt_flce_dw_tiles_bytes(0, 64) == 0 and lib.mt_flce_dw_tiles_bytes(10, -1) == 0
+    tb = lib.mt_flce_dw_tiles_bytes(100, 64)
+    # fused_tiles: a tiles buffer below the layout's size
+    assert lib.mt_flce_fused_tiles(16, 16, 8, 64, 100, 64, 64, 1, 0.0, 16, 16, 4, 16, 0, 16, 16,
+                                   16, 64, 16, tb - 16, 256, 16, 1 << 30, None) == 1
+    assert "mt_flce_dw_tiles_bytes" in lib.mt_flce_last_error().decode()
+    # ... fp32 operands: the fused path is bf16 only
+    assert lib.mt_flce_fused_tiles(16, 16, 8, 64, 100, 64, 64, 0, 0.0, 16, 16, 4, 16, 0, 16, 16,
+                                   16, 64, 16, tb, 256, 16, 1 << 30, None) == 3
+
+    def narrow(**kw):
+        a = dict(scale=16, t=1 << 20, tb=tb, V=100, H=64, out=1 << 20, ldo=64, dt=1)
+        a.update(kw)
+        return lib.mt_flce_narrow_tiles(a["scale"], a["t"], a["tb"], a["V"], a["H"], a["out"],
+                                        a["ldo"], a["dt"], None)
+    assert narrow(dt=0) == 3                           # bf16 output only
+    assert narrow(H=60, ldo=64) == 3                   # H % 8
+    assert narrow(tb=tb - 1) == 1                      # buffer too small
+    assert narrow(ldo=56) == 1                         # ldo < H
+    assert narrow(ldo=264) == 1                        # in place beyond round_up(H, 256)
+    assert "in-place" in lib.mt_flce_last_error().decode()
+    assert narrow(out=(1 << 20) + 4096) == 1           # partial overlap
+    assert "overlaps" in lib.mt_flce_last_error().decode()
+    assert narrow(out=(1 << 20) + 8) == 1              # misaligned
+    assert narrow(scale=None) == 1
+
+
 @pytest.mark.parametrize("key", [1, 2, 3, 4, 5])
 def test_backward_plan_fits_budget(key):
     cfg = synth.CONFIGS[key]

@@ -11,9 +11,10 @@ reference's torch path with the north-star tolerances (loss 2e-3 relative,
 dX and dW 1e-2 relative Frobenius, ignored rows exactly +0.0 / 0), for
 world sizes that make the scale a non-power of two, for a per-token
 gradient (recompute fallback), softcap, several chunks, and the C-ABI pieces
-this path adds: the rescale kernels (bit-exact against torch's fp32 multiply
-and round-to-nearest-even), the shifted per-sample sums (against the C
-restatement) and the per-launch timing hook.
+this path adds: the tiled dW (bit for bit the row-major one, tile layout
+unscrambled in torch), the rescale kernels (bit-exact against torch's fp32
+multiply and round-to-nearest-even), the shifted per-sample sums (against
+the C restatement) and the per-launch timing hook.
 """
 from __future__ import annotations
 
@@ -25,7 +26,7 @@ import torch
 
 from mini_trainer_amd import _lib, fused_linear_cross_entropy, path_of, per_sample_loss_sums
 from mini_trainer_amd.flce import (BACKWARD_BUDGET_ENV, FUSED_ENV, PROMISE_ULPS, _p, _stream,
-                                   fused_plan, profile_enable, profile_report)
+                                   fused_plan, prepare_targets, profile_enable, profile_report)
 from mini_trainer_amd.none_reduction_losses import (
     liger_fixed_fused_linear_cross_entropy_none_reduction as drop_in)
 from oracle import ref
@@ -179,10 +180,118 @@ def test_narrow_in_place_bit_exact(gpu, V, H, ld):
     assert torch.equal(got, want)
 
 
+def _fused_abi(dev, X, W, ri, rl, n, C, wsb, tiled):
+    """One mt_flce_fused (row-major dW) or mt_flce_fused_tiles call for a
+    unit upstream gradient; returns (loss, lse, dX, dW buffer)."""
+    lib = _lib.load()
+    T, H = X.shape
+    V = W.shape[0]
+    g = torch.ones(1, device=dev)
+    loss = torch.empty(T, device=dev)
+    lse = torch.empty(max(n, 1), device=dev)
+    dX = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    if tiled:
+        tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+        dW = torch.empty(tb // 4, device=dev)
+        _lib.check(lib.mt_flce_fused_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                           _p(ri), _p(rl), n, _p(g), 0, _p(loss), _p(lse),
+                                           _p(dX), H, _p(dW), tb, C, _p(ws), wsb, _stream(dev)),
+                   "mt_flce_fused_tiles")
+    else:
+        dW = torch.empty(V, H, device=dev)
+        _lib.check(lib.mt_flce_fused(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                     _p(ri), _p(rl), n, _p(g), 0, _p(loss), _p(lse), _p(dX), H,
+                                     _p(dW), H, 0, C, _p(ws), wsb, _stream(dev)), "mt_flce_fused")
+    torch.cuda.synchronize()
+    return loss, lse[:n], dX, dW
+
+
+def _untile(buf, V, H):
+    """Row-major fp32 [V, H] from the tiled layout: a pad of 256 * Hp bf16,
+    then tile (tm, tn) at index tm * tiles_n + tn, 256 KiB each, ordered
+    (wave row wm, wave column wn, fragment row fm, fragment column fn,
+    lane / 16, lane % 16, element r) for the element at row
+    wm * 128 + fm * 16 + lane % 16, column wn * 128 + fn * 16 + 4 (lane / 16) + r."""
+    vt, tn = -(-V // 256), -(-H // 256)
+    t = buf[128 * tn * 256:].view(vt, tn, 2, 2, 8, 8, 4, 16, 4)
+    #       dims: tm tn wm wn fm fn lq li r -> rows (tm wm fm li), cols (tn wn fn lq r)
+    t = t.permute(0, 2, 4, 7, 1, 3, 5, 6, 8).reshape(vt * 256, tn * 256)
+    return t[:V, :H]
+
+
+@pytest.mark.parametrize("T,H,V,budget", [(700, 1056, 65600, 1), (513, 192, 2065, 0),
+                                          (300, 64, 256, 0)])
+def test_fused_tiles_match_rows_bit_exact(gpu, T, H, V, budget):
+    """mt_flce_fused_tiles against mt_flce_fused on the same inputs: loss,
+    lse and dX the same bits; the tiles, unscrambled, the row-major fp32 dW
+    bit for bit (tails in V and H; budget 1: 256-row chunks accumulating,
+    and at 65600 x 1056 dW over its work queue).  mt_flce_narrow_tiles in
+    place (bf16 rows at the allocation's start) and into a separate buffer
+    with a wider pitch (the columns past H untouched) against torch's fp32
+    multiply rounded to nearest even."""
+    print(f"case tiles T={T} H={H} V={V}", flush=True)
+    lib = _lib.load()
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=T + 3)
+    X, W, y = X.to(gpu), W.to(gpu), y.to(gpu)
+    ri, rl, n = prepare_targets(y, V)
+    C, wsb, _ = fused_plan(T, n, H, V, budget_bytes=budget)
+    l0, s0, x0, d0 = _fused_abi(gpu, X, W, ri, rl, n, C, wsb, tiled=False)
+    l1, s1, x1, d1 = _fused_abi(gpu, X, W, ri, rl, n, C, wsb, tiled=True)
+    assert torch.equal(l0, l1) and torch.equal(s0, s1) and torch.equal(x0, x1)
+    assert torch.equal(_untile(d1, V, H), d0)
+    scale = torch.tensor([0.37], device=gpu)
+    want = (d0 * scale).to(torch.bfloat16)
+    out = torch.full((V, H + 8), 7.0, dtype=torch.bfloat16, device=gpu)
+    tb = d1.numel() * 4
+    _lib.check(lib.mt_flce_narrow_tiles(_p(scale), _p(d1), tb, V, H, _p(out), H + 8,
+                                        _lib.MT_DTYPE_BF16, _stream(gpu)), "narrow out of place")
+    _lib.check(lib.mt_flce_narrow_tiles(_p(scale), _p(d1), tb, V, H, _p(d1), H,
+                                        _lib.MT_DTYPE_BF16, _stream(gpu)), "narrow in place")
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :H], want)
+    assert torch.equal(out[:, H:], torch.full((V, 8), 7.0, dtype=torch.bfloat16, device=gpu))
+    got = d1.view(torch.bfloat16)[: V * H].view(V, H)
+    assert torch.equal(got, want)
+
+
+def test_fused_tiles_all_masked_and_narrow_phases(gpu):
+    """No valid row: the tiles hold zeros (written over garbage).  In-place
+    narrowing over 9 tile rows (launches {0}, {1}, [2, 4), [4, 8), {8}) of a
+    random tile buffer: every row equals torch's scaled rounding of the
+    unscrambled tiles, those whose bytes the bf16 rows reuse included."""
+    lib = _lib.load()
+    T, H, V = 64, 320, 2100
+    X = torch.randn(T, H, device=gpu).to(torch.bfloat16)
+    W = torch.randn(V, H, device=gpu).to(torch.bfloat16)
+    y = torch.full((T,), -100, device=gpu)
+    ri, rl, n = prepare_targets(y, V)
+    assert n == 0
+    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    dW = torch.full((tb // 4,), float("nan"), device=gpu)
+    loss = torch.empty(T, device=gpu)
+    dX = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    _lib.check(lib.mt_flce_fused_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                       _p(ri), _p(rl), 0, None, 0, _p(loss), None, _p(dX), H,
+                                       _p(dW), tb, 0, None, 0, _stream(gpu)), "all masked")
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(_untile(dW, V, H)) == 0 and torch.count_nonzero(dX) == 0
+    assert torch.equal(loss, torch.zeros(T, device=gpu))
+    g = torch.Generator(device=gpu).manual_seed(2)
+    dW = torch.randn(tb // 4, device=gpu, generator=g)
+    scale = torch.tensor([-2.5], device=gpu)
+    want = (_untile(dW, V, H) * scale).to(torch.bfloat16)
+    _lib.check(lib.mt_flce_narrow_tiles(_p(scale), _p(dW), tb, V, H, _p(dW), H,
+                                        _lib.MT_DTYPE_BF16, _stream(gpu)), "narrow in place")
+    torch.cuda.synchronize()
+    assert torch.equal(dW.view(torch.bfloat16)[: V * H].view(V, H), want)
+
+
 def test_reference_chain_extra_memory(gpu):
     """The reference chain on the fused kernels allocates, beyond its inputs
-    and required outputs (loss, dX, the fp32 dW whose storage then holds
-    W.grad in bf16), only the fused workspace."""
+    and required outputs (loss, dX, the fp32 dW tiles whose storage then
+    holds W.grad in bf16 -- half a tile row and the tile grid's padding more
+    than V x H fp32), only the fused workspace."""
     T, H, V = 4096, 512, 32000
     X, W, y = make_case(T, H, V, torch.bfloat16, seed=51)
     n = int((y != -100).sum())
@@ -235,7 +344,7 @@ def test_profile_hook_reports_the_fused_step(gpu):
     assert path == "fused_unit"
     # (3 dX tiles: the fused dX is split over the vocabulary)
     for k in ("fwd_bf16_kernel<store_e>", "dx_bf16_kernel<split>",
-              "dw_bf16_kernel", "dx_dw_phase", "scale_rows_kernel<dX>", "narrow_rows_inplace_kernel<dW>"):
+              "dw_bf16_kernel", "dx_dw_phase", "scale_rows_kernel<dX>", "narrow_tiles_kernel<dW>"):
         assert k in rep and rep[k]["launches"] >= 1 and rep[k]["ms_total"] > 0, k
     # algorithmic work: 2 H V n for each GEMM over all chunks, their sum for the phase
     f = 2.0 * 128 * 2560 * n
