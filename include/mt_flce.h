@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define MT_FLCE_ABI_VERSION 4
+#define MT_FLCE_ABI_VERSION 5
 
 typedef struct ihipStream_t* mt_stream_t; /* == hipStream_t */
 
@@ -222,7 +222,28 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
                   void* workspace, size_t workspace_bytes, mt_stream_t stream);
 
 /*
- * Bytes of the tiled fp32 weight gradient that mt_flce_fused_tiles forms
+ * mt_flce_backward with dW formed as tiles (layout of
+ * mt_flce_dw_tiles_bytes) instead of rows, bf16 only: the same arithmetic,
+ * so mt_flce_narrow_tiles of the result equals mt_flce_backward +
+ * mt_flce_scale_grads bit for bit.  dW is never accumulated into (a
+ * dw_accumulator stays on mt_flce_backward).  Replaces the same reference
+ * interface as mt_flce_backward (the lm_head backward's dW = dS^T X,
+ * none_reduction_losses.py:35 through autograd).
+ */
+int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H,
+                           int64_t V, int64_t ldx, int64_t ldw, int dtype,
+                           float softcap, const int32_t* row_index,
+                           const int32_t* row_label, int64_t n_valid,
+                           const float* lse, const float* grad_loss,
+                           int64_t grad_stride, void* dX, int64_t lddx,
+                           float* dW_tiles, size_t dw_tiles_bytes,
+                           int64_t chunk_rows, int64_t chunk_vocab,
+                           void* workspace, size_t workspace_bytes,
+                           mt_stream_t stream);
+
+/*
+ * Bytes of the tiled fp32 weight gradient that mt_flce_fused_tiles and
+ * mt_flce_backward_tiles form
  * (0 for sizes out of range): a pad of 256 * round_up(H, 256) bf16 elements,
  * then ceil(V/256) x ceil(H/256) tiles of 256 x 256 fp32 in the order the
  * dW GEMM holds them.  At least V * H * 4, so the same allocation also

@@ -10,7 +10,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p, c_char_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmt_flce.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MT_DTYPE_F32 = 0
 MT_DTYPE_BF16 = 1
@@ -50,6 +50,10 @@ SIGNATURES = {
                               c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
                               c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int,
                               c_int64, c_void_p, c_size_t, c_void_p]),
+    "mt_flce_backward_tiles": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                       c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
+                                       c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                       c_size_t, c_int64, c_int64, c_void_p, c_size_t, c_void_p]),
     "mt_flce_dw_tiles_bytes": (c_size_t, [c_int64, c_int64]),
     "mt_flce_fused_tiles": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                     c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,

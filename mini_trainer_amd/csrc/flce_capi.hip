@@ -570,13 +570,31 @@ int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t 
   return check_launch("fwd_finalize_kernel");
 }
 
+// Tiled fp32 dW: 256 x 256 tiles (the grid padded to whole tiles), each
+// 256 KiB in the accumulators' own order, row-major over the tile grid,
+// after a leading pad of half a tile row (256 * Hp bf16 elements): the
+// bf16 rows narrowed out of tile row r then end at or before tile row r / 2
+// starts, so tile rows narrowed in launches {0}, {1}, [2, 4), [4, 8), ...
+// only overwrite tiles an earlier launch has read.
+int64_t dw_tiles_pad(int64_t H) { return 128 * round_up(H, 256); }  // floats
+size_t dw_tiles_bytes(int64_t V, int64_t H) {
+  return (size_t)dw_tiles_pad(H) * 4 + (size_t)cdiv(V, 256) * cdiv(H, 256) * 65536 * 4;
+}
+// Every tile zero (the gradient of a call without valid rows), as 1 KiB rows.
+int zero_tiles(float* tiles, int64_t V, int64_t H, hipStream_t s) {
+  const int64_t rows = cdiv(V, 256) * cdiv(H, 256) * 256;
+  hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(rows, 8192)), dim3(256), 0, s,
+                     tiles + dw_tiles_pad(H), rows, (int64_t)256, (int64_t)256);
+  return check_launch("zero_matrix_f32_kernel");
+}
+
 template <typename T>
 int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V, int64_t ldx,
                     int64_t ldw,
                     float softcap, const int32_t* row_index, const int32_t* row_label,
                     int64_t N, const float* lse, const float* grad, int64_t gstride, void* dX,
-                    int64_t lddx, float* dW, int64_t lddw, int accumulate, int64_t C, int64_t Cv,
-                    char* ws, hipStream_t stream) {
+                    int64_t lddx, float* dW, int64_t lddw, int accumulate, bool tiled, int64_t C,
+                    int64_t Cv, char* ws, hipStream_t stream) {
   constexpr int es = sizeof(T);
   const Geometry geo = geometry(es);
   const int64_t nv = cdiv(V, Cv);
@@ -703,6 +721,11 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
       w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
       w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
+      if (tiled) {  // (bf16 only; the block's tile rows start at v0 / 256)
+        w.tiled = 1;
+        w.tile_pad = dw_tiles_pad(H);
+        w.lddw = 0;
+      }
       if (use_queue) w.queue = queue;
       if (beside) {
         // the next block's recompute (G) and gather (X^T) follow the join
@@ -710,7 +733,7 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       } else {
         if constexpr (sizeof(T) == 2) {
           const int pw = prof_begin("dw_bf16_kernel", dw_flops(w), 0, stream);
-          void (*kern)(DwArgs) = dw_bf16_kernel<false, false>;
+          void (*kern)(DwArgs) = tiled ? dw_bf16_kernel<false, true> : dw_bf16_kernel<false, false>;
           hipLaunchKernelGGL(kern, dim3(persistent_grid(w.tiles_m * w.tiles_n)),
                              dim3(kThreadsBf), 0, stream, w);
           prof_end(pw, stream);
@@ -759,17 +782,6 @@ DxSplit fused_split(int64_t C, int64_t H, int64_t V) {
   d.S = cdiv(V, d.kslice);
   if (d.S <= 1) d = DxSplit();
   return d;
-}
-
-// Tiled fp32 dW: 256 x 256 tiles (the grid padded to whole tiles), each
-// 256 KiB in the accumulators' own order, row-major over the tile grid,
-// after a leading pad of half a tile row (256 * Hp bf16 elements): the
-// bf16 rows narrowed out of tile row r then end at or before tile row r / 2
-// starts, so tile rows narrowed in launches {0}, {1}, [2, 4), [4, 8), ...
-// only overwrite tiles an earlier launch has read.
-int64_t dw_tiles_pad(int64_t H) { return 128 * round_up(H, 256); }  // floats
-size_t dw_tiles_bytes(int64_t V, int64_t H) {
-  return (size_t)dw_tiles_pad(H) * 4 + (size_t)cdiv(V, 256) * cdiv(H, 256) * 65536 * 4;
 }
 
 size_t fused_ws(int64_t C, int64_t H, int64_t V) {
@@ -1154,17 +1166,23 @@ int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int 
   return MT_OK;
 }
 
-int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
-                     int64_t ldw, int dtype, float softcap, const int32_t* row_index,
-                     const int32_t* row_label, int64_t n_valid, const float* lse,
-                     const float* grad_loss, int64_t grad_stride, void* dX, int64_t lddx, float* dW,
-                     int64_t lddw, int accumulate_dW, int64_t chunk_rows, int64_t chunk_vocab,
-                     void* workspace, size_t workspace_bytes, mt_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// mt_flce_backward (row-major dW) and mt_flce_backward_tiles (tiled dW of
+// dw_tiles_bytes, bf16 only, lddw == 0, never accumulated into).
+int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                   int64_t ldw, int dtype, float softcap, const int32_t* row_index,
+                   const int32_t* row_label, int64_t n_valid, const float* lse,
+                   const float* grad_loss, int64_t grad_stride, void* dX, int64_t lddx, float* dW,
+                   int64_t lddw, int accumulate_dW, bool tiled, int64_t chunk_rows,
+                   int64_t chunk_vocab, void* workspace, size_t workspace_bytes, mt_stream_t stream) {
   MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
   const int es = esize_of(dtype);
   if (n_valid < 0 || n_valid > T)
     return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
-  if (lddx < H || lddw < H)
+  if (lddx < H || (!tiled && lddw < H))
     return fail(MT_ERR_INVALID_ARGUMENT, "lddx=%lld / lddw=%lld must be >= H", (long long)lddx, (long long)lddw);
   if ((lddx * es) % 16 != 0 || (lddw * 4) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "dX / dW row pitches must be multiples of 16 bytes");
@@ -1200,7 +1218,9 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
     MT_TRY(check_launch("zero_rows_kernel"));
   }
   if (n_valid == 0) {
-    if (!accumulate_dW) {
+    if (tiled) {
+      MT_TRY(zero_tiles(dW, V, H, s));
+    } else if (!accumulate_dW) {
       hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
                          s, dW, V, H, lddw);
       MT_TRY(check_launch("zero_matrix_f32_kernel"));
@@ -1209,11 +1229,43 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
   }
   if (dtype == MT_DTYPE_BF16)
     return launch_backward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
-                                   grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW,
+                                   grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, tiled,
                                    chunk_rows, chunk_vocab, static_cast<char*>(workspace), s);
   return launch_backward<float>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
-                                grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, chunk_rows,
-                                chunk_vocab, static_cast<char*>(workspace), s);
+                                grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, false,
+                                chunk_rows, chunk_vocab, static_cast<char*>(workspace), s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
+                     int64_t ldw, int dtype, float softcap, const int32_t* row_index,
+                     const int32_t* row_label, int64_t n_valid, const float* lse,
+                     const float* grad_loss, int64_t grad_stride, void* dX, int64_t lddx, float* dW,
+                     int64_t lddw, int accumulate_dW, int64_t chunk_rows, int64_t chunk_vocab,
+                     void* workspace, size_t workspace_bytes, mt_stream_t stream) {
+  return backward_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid, lse,
+                        grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, false, chunk_rows,
+                        chunk_vocab, workspace, workspace_bytes, stream);
+}
+
+int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
+                           int64_t ldx, int64_t ldw, int dtype, float softcap,
+                           const int32_t* row_index, const int32_t* row_label, int64_t n_valid,
+                           const float* lse, const float* grad_loss, int64_t grad_stride, void* dX,
+                           int64_t lddx, float* dW_tiles, size_t dw_tiles_bytes_,
+                           int64_t chunk_rows, int64_t chunk_vocab, void* workspace,
+                           size_t workspace_bytes, mt_stream_t stream) {
+  if (dtype != MT_DTYPE_BF16)
+    return fail(MT_ERR_UNSUPPORTED, "tiled dW is bf16 only (dtype %d)", dtype);
+  if (H > 0 && V > 0 && dw_tiles_bytes_ < dw_tiles_bytes(V, H))
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles %zu bytes < mt_flce_dw_tiles_bytes = %zu",
+                dw_tiles_bytes_, dw_tiles_bytes(V, H));
+  return backward_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid, lse,
+                        grad_loss, grad_stride, dX, lddx, dW_tiles, 0, 0, true, chunk_rows,
+                        chunk_vocab, workspace, workspace_bytes, stream);
 }
 
 int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
@@ -1290,11 +1342,8 @@ int fused_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V, i
     MT_TRY(check_launch("zero_rows_kernel"));
   }
   if (n_valid == 0) {
-    if (tiled) {  // every tile, as 1 KiB rows
-      const int64_t rows = cdiv(V, 256) * cdiv(H, 256) * 256;
-      hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(rows, 8192)), dim3(256),
-                         0, s, dW + dw_tiles_pad(H), rows, (int64_t)256, (int64_t)256);
-      MT_TRY(check_launch("zero_matrix_f32_kernel"));
+    if (tiled) {
+      MT_TRY(zero_tiles(dW, V, H, s));
     } else if (!accumulate_dW) {
       hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
                          s, dW, V, H, lddw);

@@ -539,9 +539,11 @@ struct DwArgs {
   // non-null: persistent schedule over a work queue (dw_bf16_kernel<true>):
   // kQueueWords counters, zero at launch, one per XCD's share of the tiles
   uint32_t* queue = nullptr;
-  // tiled (bf16 fused path): dW in the library's tile order instead of rows
-  // of pitch lddw: tile (tm, tn) at floats tile_pad + (tm tiles_n + tn) 65536,
-  // wave w's fragment (fm, fn) at ((w 64 + fm 8 + fn) 64 + lane) 4 within it
+  // tiled (bf16): dW in the library's tile order instead of rows of pitch
+  // lddw: tile (tm, tn) at floats tile_pad + (tm tiles_n + tn) 65536, tm
+  // counted from vocabulary row 0 (the block's tile rows start at v0 / 256,
+  // v0 a multiple of 256), wave w's fragment (fm, fn) at
+  // ((w 64 + fm 8 + fn) 64 + lane) 4 within it
   int32_t tiled = 0;
   int64_t tile_pad = 0;
 };

@@ -603,7 +603,7 @@ __device__ __forceinline__ DwTile dw_tile(const DwArgs& a, int32_t m0, int32_t h
 // one contiguous KiB per instruction -- no transpose, no bounds (the tile
 // grid is padded; rows past V and columns past H are never read back).
 __device__ __forceinline__ rsrc_t dw_tiled_rsrc(const DwArgs& a, int32_t m0, int32_t h0) {
-  const int64_t tile = (int64_t)(m0 / 256) * a.tiles_n + h0 / 256;
+  const int64_t tile = (int64_t)((a.v0 + m0) / 256) * a.tiles_n + h0 / 256;
   return make_rsrc(a.dW + a.tile_pad + tile * 65536, 262144u);
 }
 __device__ __forceinline__ uint32_t dw_tiled_off(const EpiCoordsBf& ec, int fm, int fn) {

@@ -159,7 +159,9 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
 
     general     forward keeps lse (mt_flce_forward); the backward recomputes
                 the logits for whatever upstream gradient arrives
-                (mt_flce_backward).
+                (mt_flce_backward; bf16 without dw_accumulator:
+                mt_flce_backward_tiles, dW as 256 x 256 fp32 tiles narrowed
+                by mt_flce_narrow_tiles).
     fused       grad_scale promised the upstream gradient at the forward and
                 the planner expects the fused path to pay (bf16,
                 mt_flce_fused_plan): the forward also forms dX and dW for it
@@ -262,18 +264,27 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         dev = X.device
         g, gstride = _grad_vector(grad_loss, T)
         dX = torch.empty((T, H), dtype=X.dtype, device=dev)
-        if acc is not None:
-            dW, accumulate = acc, 1
-        else:
-            dW, accumulate = torch.empty((V, H), dtype=torch.float32, device=dev), 0
         C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt, softcap,
-                                   _p(row_index), _p(row_label), n, _p(lse), _p(g), gstride,
-                                   _p(dX), dX.stride(0), _p(dW), dW.stride(0), accumulate, C, Cv,
-                                   _p(ws), ws_bytes, _stream(dev)), "mt_flce_backward")
+        if acc is None and dt == MT_DTYPE_BF16:
+            # dW as 256 x 256 fp32 tiles, narrowed into bf16 in its own allocation
+            dW = _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX,
+                                 C, Cv, ws)
+            del ws
+            grad_w = _tiles_in_dtype(dW, (V, H), torch.ones(1, device=dev)) if need_w else None
+        else:
+            if acc is not None:
+                dW, accumulate = acc, 1
+            else:
+                dW, accumulate = torch.empty((V, H), dtype=torch.float32, device=dev), 0
+            check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
+                                       softcap, _p(row_index), _p(row_label), n, _p(lse), _p(g),
+                                       gstride, _p(dX), dX.stride(0), _p(dW), dW.stride(0),
+                                       accumulate, C, Cv, _p(ws), ws_bytes, _stream(dev)),
+                  "mt_flce_backward")
+            del ws
+            grad_w = _weight_grad_in_dtype(dW, W.dtype) if (need_w and acc is None) else None
         grad_x = dX.view(hshape) if need_x else None
-        grad_w = _weight_grad_in_dtype(dW, W.dtype) if (need_w and acc is None) else None
         return (grad_x, grad_w) + none
 
     @staticmethod
@@ -344,17 +355,13 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
             del dW
         else:
             # a per-token gradient: the unit-gradient results cannot be
-            # rescaled; recompute into the same buffers (the tiles'
-            # allocation holds a row-major fp32 [V, H])
-            dW = dW[:V * H].view(V, H)
+            # rescaled; recompute into the same buffers
             C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-            check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
-                                       softcap, _p(row_index), _p(row_label), n, _p(lse), _p(g),
-                                       gstride, _p(dX), dX.stride(0), _p(dW), dW.stride(0), 0, C,
-                                       Cv, _p(ws), ws_bytes, _stream(dev)), "mt_flce_backward")
+            _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX, C, Cv,
+                            ws, dW)
             del ws
-            dW_out = _weight_grad_in_dtype(dW, W.dtype) if need_w else None
+            dW_out = _tiles_in_dtype(dW, (V, H), torch.ones(1, device=dev)) if need_w else None
         grad_x = dX.view(hshape) if need_x else None
         grad_w = dW_out if need_w else None
         return (grad_x, grad_w) + (None,) * 7
@@ -371,6 +378,23 @@ def _narrowed_view(dW: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     # storage offsets count elements: one fp32 element is two 16-bit ones
     out.set_(dW.untyped_storage(), 2 * dW.storage_offset(), (V, H), (dW.stride(0), 1))
     return out
+
+
+def _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX, C, Cv, ws,
+                    dWt: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """mt_flce_backward_tiles (bf16) into dWt, or into a new tiles buffer of
+    mt_flce_dw_tiles_bytes; returns the buffer."""
+    T, H = X.shape
+    V = W.shape[0]
+    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    if dWt is None:
+        dWt = torch.empty(tb // 4, dtype=torch.float32, device=X.device)
+    check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0),
+                                     MT_DTYPE_BF16, softcap, _p(row_index), _p(row_label), n,
+                                     _p(lse), _p(g), gstride, _p(dX), dX.stride(0), _p(dWt),
+                                     dWt.numel() * 4, C, Cv, _p(ws), ws.numel(),
+                                     _stream(X.device)), "mt_flce_backward_tiles")
+    return dWt
 
 
 def _tiles_in_dtype(dWt: torch.Tensor, shape: Tuple[int, int],

@@ -143,6 +143,15 @@ def test_dw_tiles_layout_and_host_checks():
     # ... fp32 operands: the fused path is bf16 only
     assert lib.mt_flce_fused_tiles(16, 16, 8, 64, 100, 64, 64, 0, 0.0, 16, 16, 4, 16, 0, 16, 16,
                                    16, 64, 16, tb, 256, 16, 1 << 30, None) == 3
+    # backward_tiles: fp32 unsupported, a tiles buffer below the layout's size
+    bargs = [16, 16, 8, 64, 100, 64, 64]
+    rest = [0.0, 16, 16, 4, 16, 16, 1, 16, 64, 16]
+    assert lib.mt_flce_backward_tiles(*bargs, 0, *rest, tb, 256, 256, 16, 1 << 30, None) == 3
+    assert lib.mt_flce_backward_tiles(*bargs, 1, *rest, tb - 16, 256, 256, 16, 1 << 30,
+                                      None) == 1
+    assert "mt_flce_dw_tiles_bytes" in lib.mt_flce_last_error().decode()
+    # ... chunk sizes must be positive multiples of 256
+    assert lib.mt_flce_backward_tiles(*bargs, 1, *rest, tb, 100, 256, 16, 1 << 30, None) == 1
 
     def narrow(**kw):
         a = dict(scale=16, t=1 << 20, tb=tb, V=100, H=64, out=1 << 20, ldo=64, dt=1)

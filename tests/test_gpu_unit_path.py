@@ -255,6 +255,50 @@ def test_fused_tiles_match_rows_bit_exact(gpu, T, H, V, budget):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("C,Cv,cap", [(256, 52736, None), (256, 16384, "3"), (512, 65600 + 192, None)])
+def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
+    """mt_flce_backward_tiles against mt_flce_backward on the same inputs and
+    blocks (per-token upstream gradient): dX the same bits, the tiles,
+    unscrambled, the row-major fp32 dW bit for bit.  Blocks of (C, Cv):
+    two row blocks and a vocabulary split whose first block runs dW beside dX
+    over the work queue; under a 3-CU grid cap dW runs after dX, three
+    persistent workgroups carrying tiles; one block over the whole
+    vocabulary.  V = 65600, H = 1056 (tails in both)."""
+    print(f"case backward tiles C={C} Cv={Cv} cap={cap}", flush=True)
+    if cap:
+        monkeypatch.setenv("MT_FLCE_GRID_CAP", cap)
+    lib = _lib.load()
+    T, H, V = 700, 1056, 65600
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=61)
+    X, W, y = X.to(gpu), W.to(gpu), y.to(gpu)
+    ri, rl, n = prepare_targets(y, V)
+    s = _stream(gpu)
+    loss = torch.empty(T, device=gpu)
+    lse = torch.empty(n, device=gpu)
+    fwb = int(lib.mt_flce_forward_workspace_bytes(T, n, H, V, _lib.MT_DTYPE_BF16))
+    fws = torch.empty(fwb, dtype=torch.uint8, device=gpu)
+    _lib.check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0, _p(ri),
+                                   _p(rl), n, _p(loss), _p(lse), _p(fws), fwb, s), "forward")
+    g = torch.rand(T, device=gpu, generator=torch.Generator(device=gpu).manual_seed(8)) - 0.3
+    al = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    wsb = al(C * Cv * 2) + (al(C * H * 4) if Cv < V else 0) + al(H * C * 2) + al(32)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    dX0 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    dW0 = torch.empty(V, H, device=gpu)
+    _lib.check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0, _p(ri),
+                                    _p(rl), n, _p(lse), _p(g), 1, _p(dX0), H, _p(dW0), H, 0, C, Cv,
+                                    _p(ws), wsb, s), "backward")
+    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    dX1 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    dW1 = torch.full((tb // 4,), float("nan"), device=gpu)
+    _lib.check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                          _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX1), H,
+                                          _p(dW1), tb, C, Cv, _p(ws), wsb, s), "backward_tiles")
+    torch.cuda.synchronize()
+    assert torch.equal(dX0, dX1)
+    assert torch.equal(_untile(dW1, V, H), dW0)
+
+
 def test_fused_tiles_all_masked_and_narrow_phases(gpu):
     """No valid row: the tiles hold zeros (written over garbage).  In-place
     narrowing over 9 tile rows (launches {0}, {1}, [2, 4), [4, 8), {8}) of a
