@@ -160,12 +160,18 @@ def measured_traffic(key: int, unit: str):
 
 def add_counter_bytes(kernels: dict, key: int) -> None:
     """Per-dispatch read / written bytes of the summary's kernels (same
-    names as the event report) beside their event timings."""
+    names as the event report) beside their event timings, and, where the
+    summary has them, the kernel's MFMA counters from a pass that runs each
+    dispatch alone: busy fraction per busy-CU cycle, clock, whole-chip
+    utilisation."""
     t = traffic_summary(key) or {}
     for name, b in t.get("per_kernel", {}).items():
         if name in kernels:
             kernels[name]["counter_read_GB_per_launch"] = b["read_bytes"] / 1e9
             kernels[name]["counter_write_GB_per_launch"] = b["write_bytes"] / 1e9
+            for k in ("mfma_busy", "clock_GHz", "mfma_util"):
+                if k in b:
+                    kernels[name]["counter_" + k + "_alone"] = b[k]
 
 
 def copy_calibration():
@@ -282,6 +288,11 @@ def roofline_of(report: dict, peak_flops: float, steps: int) -> tuple:
                              "frac": ach / PEAK_HBM, "bound": "hbm"}
     if "dx_dw_phase" in report:
         unit = "dx_dw_phase"
+        # dX and dW share the chip inside the phase: each one's span runs
+        # from its own start to its own end, so its frac is not its rate
+        for name in kernels:
+            if name.startswith(("dx_bf16_kernel", "dw_bf16_kernel")):
+                kernels[name]["span_inside"] = "dx_dw_phase"
     else:
         gemms = {k: v for k, v in report.items() if v["flops"] > 0}
         unit = max(gemms, key=lambda k: gemms[k]["ms_total"]) if gemms else None
