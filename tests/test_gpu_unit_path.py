@@ -221,7 +221,7 @@ def _untile(buf, V, H):
 
 
 @pytest.mark.parametrize("T,H,V,budget", [(700, 1056, 65600, 1), (513, 192, 2065, 0),
-                                          (300, 64, 256, 0)])
+                                          (300, 64, 256, 0), (200, 72, 100, 0)])
 def test_fused_tiles_match_rows_bit_exact(gpu, T, H, V, budget):
     """mt_flce_fused_tiles against mt_flce_fused on the same inputs: loss,
     lse and dX the same bits; the tiles, unscrambled, the row-major fp32 dW
@@ -229,7 +229,8 @@ def test_fused_tiles_match_rows_bit_exact(gpu, T, H, V, budget):
     and at 65600 x 1056 dW over its work queue).  mt_flce_narrow_tiles in
     place (bf16 rows at the allocation's start) and into a separate buffer
     with a wider pitch (the columns past H untouched) against torch's fp32
-    multiply rounded to nearest even."""
+    multiply rounded to nearest even.  The last case is one partial tile
+    (V < 256, H < 256) with a partial last K stage (H % 64 = 8)."""
     print(f"case tiles T={T} H={H} V={V}", flush=True)
     lib = _lib.load()
     X, W, y = make_case(T, H, V, torch.bfloat16, seed=T + 3)
