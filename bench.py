@@ -14,9 +14,9 @@ resident in HBM before timing starts.
 
 Prints ONE JSON line (driver contract) with, in addition:
   roofline      the dominant unit of the timed step (the side-by-side dX and
-                dW GEMMs of each fused chunk: 2*C*V*H flops each, fork to
-                join), timed live with the library's per-launch HIP events on
-                the streams the kernels run on, against the bf16 dense peak;
+                dW GEMMs of each fused chunk, one launch: 2*C*V*H flops
+                each), timed live with the library's per-launch HIP events on
+                the stream the kernel runs on, against the bf16 dense peak;
                 `kernels` lists every kernel of the step the same way (with
                 the GEMMs' calibrated counter bytes per dispatch);
                 traffic = HBM bytes per launch from the committed rocprofv3
@@ -172,6 +172,10 @@ def add_counter_bytes(kernels: dict, key: int) -> None:
             for k in ("mfma_busy", "clock_GHz", "mfma_util"):
                 if k in b:
                     kernels[name]["counter_" + k + "_alone"] = b[k]
+    # dX and dW of the phase as two kernels (MT_FLCE_SPLIT_PHASE=1), counted
+    # apart: their MFMA busy fractions inside the one launch the step runs
+    for name, b in t.get("split_parts", {}).items():
+        kernels.setdefault("dx_dw_phase", {}).setdefault("parts_launched_apart", {})[name] = b
 
 
 def copy_calibration():

@@ -30,11 +30,15 @@
  *     (bf16) or 4 (fp32), i.e. whole 16-byte chunks -- a partial last K
  *     stage is masked inside the kernels.  dtype selects bf16 (MFMA path) or fp32
  *     inputs; loss / lse / dW are always fp32, dX has the dtype of X.
- *   - mt_flce_fused and the bf16 mt_flce_backward run their dW GEMMs on a
+ *   - mt_flce_fused and the bf16 mt_flce_backward run dW beside dX in one
+ *     launch on the caller's stream (dX's workgroups dispatched first, dW's
+ *     on the CUs dX leaves free and then the rest).  Measurement hook:
+ *     MT_FLCE_SPLIT_PHASE=1 launches them as two kernels instead, dW on a
  *     second stream of the library's own (one per device, created on first
- *     use, default priority), beside dX, forked from and joined back to the
- *     caller's stream with events inside the call; to the caller the call
- *     stays ordered on its stream.
+ *     use, default priority) forked from and joined back to the caller's
+ *     stream with events inside the call, so that each has its own timing
+ *     events and counters; either way the call stays ordered on the
+ *     caller's stream.
  *   - Test hook: the environment variable MT_FLCE_GRID_CAP=n (> 0) caps the
  *     persistent bf16 GEMM grids (logits, recompute) and the dW grids at n
  *     workgroups, and the general backward takes n as the CU count when it

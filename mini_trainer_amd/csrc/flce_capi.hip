@@ -291,14 +291,46 @@ inline void launch_dx_reduce(const DxReduce& r, hipStream_t stream) {
 }
 
 // dX and dW of one block side by side: dX (tiles_m x tiles_n workgroups,
-// often fewer than the CUs or a partial last round) on the caller's stream,
-// dW (one workgroup per tile) on the library's side stream, forked from and
-// joined back to the caller's stream with events, so dW's workgroups take
-// the CUs dX leaves free and then the rest.  Both only read G and the X^T
-// block; whatever rewrites them is enqueued after the join.  red (K-split
-// dX): its reduction follows dX on the caller's stream, beside dW.
+// often fewer than the CUs or a partial last round) and dW (one workgroup
+// per tile, or persistent over the work queue) in one launch of
+// dx_dw_bf16_kernel on the caller's stream, dX's workgroups first, so dW's
+// take the CUs dX leaves free and then the rest.  Both only read G and the
+// X^T block; whatever rewrites them is enqueued after the launch.  red
+// (K-split dX): its reduction follows on the caller's stream.
+// Measurement hook MT_FLCE_SPLIT_PHASE=1: dX on the caller's stream, dW on
+// the library's side stream, forked from and joined back to the caller's
+// stream with events (the reduction follows dX, beside dW), each kernel
+// with its own timing events and counters.
+bool split_phase() {
+  const char* e = std::getenv("MT_FLCE_SPLIT_PHASE");
+  return e && e[0] == '1';
+}
+
 int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
                       const DxReduce* red = nullptr) {
+  if (!split_phase()) {
+    using K = void (*)(DxArgs, DwArgs, uint32_t);
+#define MT_DXDW(m) \
+  {{dx_dw_bf16_kernel<m, false, false>, dx_dw_bf16_kernel<m, false, true>}, \
+   {dx_dw_bf16_kernel<m, true, false>, dx_dw_bf16_kernel<m, true, true>}}
+    static const K kern[4][2][2] = {MT_DXDW(kDxStore), MT_DXDW(kDxAdd), MT_DXDW(kDxAddEmit),
+                                    MT_DXDW(kDxEmit)};
+#undef MT_DXDW
+    const double fx = dx_flops(x), fw = dw_flops(w);
+    const int64_t dxg = (int64_t)x.tiles_m * x.tiles_n * x.nsplit;
+    const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
+    const int64_t dwg = w.queue ? device_cus() : (cap > 0 ? std::min(dw_tiles, cap) : dw_tiles);
+    const int ph = prof_begin("dx_dw_phase", fx + fw, 0, stream);
+    hipLaunchKernelGGL(kern[x.mode & 3][w.queue ? 1 : 0][w.tiled ? 1 : 0], dim3((uint32_t)(dxg + dwg)),
+                       dim3(kThreadsBf), 0, stream, x, w, (uint32_t)dxg);
+    MT_TRY(check_launch("dx_dw_bf16_kernel"));
+    if (red) {
+      launch_dx_reduce(*red, stream);
+      MT_TRY(check_launch("dx_split_reduce_kernel"));
+    }
+    prof_end(ph, stream);
+    return MT_OK;
+  }
   SideStream* side = nullptr;
   MT_TRY(side_stream(&side));
   std::lock_guard<std::mutex> lock(side->use);

@@ -37,6 +37,11 @@ struct TileSeq {
     stride = gridDim.x;
     first = xcd_remap(blockIdx.x, gridDim.x);
   }
+  // workgroup b of nb (a launch that also holds other work)
+  __device__ __forceinline__ TileSeq(uint32_t total_, uint32_t b, uint32_t nb) : total(total_) {
+    stride = nb;
+    first = xcd_remap(b, nb);
+  }
   __device__ __forceinline__ int count() const {
     return first < total ? (int)((total - first + stride - 1) / stride) : 0;
   }
@@ -527,13 +532,12 @@ __device__ __forceinline__ void dx_epilogue_bf16(const f32x4_t (&acc)[8][8], con
 // with one the compiler rotated accumulators through VGPRs and spilled inside
 // the K loop (the next tile's operand set-up lives in that loop); with a
 // single tile the loop compiles to the MFMAs, LDS reads and DMA only.
+// Workgroup b of nb (b = blockIdx.x unless the launch holds dW as well).
 template <int kMode>
-MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+__device__ __forceinline__ void dx_bf16_body(char* lds, DxArgs a, uint32_t b, uint32_t nb) {
   // K split (nsplit > 1): workgroup b takes slice b % nsplit of tile b / nsplit:
   // the slice's first vocabulary entry becomes K = 0 of E and of W, and its
   // fp32 result goes to its own plane of accbuf
-  uint32_t b = blockIdx.x, nb = gridDim.x;
   if (a.nsplit > 1) {
     const uint32_t z = b % (uint32_t)a.nsplit;
     b /= (uint32_t)a.nsplit;
@@ -572,6 +576,12 @@ MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
         grouped_tile(tile, a.tiles_m, a.tiles_n, 4, tm, tn);
         dx_epilogue_bf16<kMode>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256);
       });
+}
+
+template <int kMode>
+MT_GEMM_BF16_KERNEL void dx_bf16_kernel(DxArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  dx_bf16_body<kMode>(lds, a, blockIdx.x, gridDim.x);
 }
 
 // dW tiles accumulate in place: a tile's accumulators start from the fp32
@@ -826,10 +836,9 @@ struct DwQueue {
 // work queue above (grid = one workgroup per CU, K >= 2 stages); otherwise
 // one workgroup per tile or a static persistent schedule (TileSeq).
 template <bool kQueue, bool kTiled>
-MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+__device__ __forceinline__ void dw_bf16_body(char* lds, const DwArgs& a, uint32_t b, uint32_t nb) {
   const uint32_t total = (uint32_t)(a.tiles_m * a.tiles_n);
-  const TileSeq seq(total);
+  const TileSeq seq(total, b, nb);
   DwQueue q;
   if constexpr (kQueue) q.start(a, total, lds);
   const EpiCoordsBf ec0;
@@ -888,6 +897,26 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
         if constexpr (kQueue) q.ask();
         dw_load_acc<kTiled>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0);
       });
+}
+
+template <bool kQueue, bool kTiled>
+MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  dw_bf16_body<kQueue, kTiled>(lds, a, blockIdx.x, gridDim.x);
+}
+
+// dX and dW of one block in one launch: workgroups [0, dx_blocks) are dX's
+// (dispatched first, so dX's long tiles start at once), the rest dW's (the
+// CUs dX leaves free, then the others; the work queue's XCD shares follow
+// the global workgroup index, which keeps the round-robin XCD placement).
+// Both only read G and the X^T block.
+template <int kMode, bool kQueue, bool kTiled>
+MT_GEMM_BF16_KERNEL void dx_dw_bf16_kernel(DxArgs x, DwArgs w, uint32_t dx_blocks) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  if (blockIdx.x < dx_blocks)
+    dx_bf16_body<kMode>(lds, x, blockIdx.x, dx_blocks);
+  else
+    dw_bf16_body<kQueue, kTiled>(lds, w, blockIdx.x - dx_blocks, gridDim.x - dx_blocks);
 }
 
 // Tiled fp32 dW (dw_bf16_kernel<*, true>) times *scale, narrowed to bf16 rows

@@ -120,14 +120,18 @@ def test_fused_out_of_range_logits_recompute_their_chunk(gpu, monkeypatch, shift
     assert torch.equal(l2.cpu(), loss)
 
 
-def test_fused_dw_work_queue_with_tails(gpu, monkeypatch):
+@pytest.mark.parametrize("split", ["0", "1"])
+def test_fused_dw_work_queue_with_tails(gpu, monkeypatch, split):
     # 257 x 5 = 1285 dW tiles per chunk, at least 4 per CU: dW runs
     # persistent over its work queue; a vocabulary tail (V = 65600) and a
     # hidden tail (H = 1056: the fifth column of tiles 32 wide), 256-row
-    # chunks.  Reference: the torch path on the GPU in fp32.
+    # chunks.  dX and dW in one launch, and (split = 1, the measurement
+    # hook) as two kernels on two streams.  Reference: the torch path on
+    # the GPU in fp32.
     from mini_trainer_amd.flce import profile_enable, profile_report
     from oracle.torch_path import torch_path
     monkeypatch.setenv(BACKWARD_BUDGET_ENV, "1")
+    monkeypatch.setenv("MT_FLCE_SPLIT_PHASE", split)
     T, H, V = 700, 1056, 65600
     X, W, y = make_case(T, H, V, torch.bfloat16, seed=51)
     n = int((y != -100).sum())
@@ -137,7 +141,10 @@ def test_fused_dw_work_queue_with_tails(gpu, monkeypatch):
         loss, dX, dW = run_fused(gpu, X, W, y, 1.0 / n)
     finally:
         profile_enable(False)
-    assert profile_report()["dw_bf16_kernel<queue>"]["launches"] == -(-n // 256)  # one per chunk
+    rep = profile_report()
+    assert rep["dx_dw_phase"]["launches"] == -(-n // 256)  # one per chunk
+    if split == "1":
+        assert rep["dw_bf16_kernel<queue>"]["launches"] == -(-n // 256)
     g = torch.full((T,), 1.0 / n, device=gpu)
     rl, rdX, rdW = torch_path(X.to(gpu), W.to(gpu), y.to(gpu), grad=g, upcast=True)
     valid = y != -100
@@ -208,11 +215,14 @@ def test_grad_scale_ignored_without_autograd(gpu):
     assert bool((acc == 0.5).all())
 
 
-def test_fused_concurrent_host_threads(gpu):
-    # Two host threads, each on its own stream, share the library's per-device
-    # side stream and fork / join events; every call must still order its dW
-    # after its own G and its caller's stream after its own dW.  Results are
-    # bit-identical to the same calls made one after the other.
+@pytest.mark.parametrize("split", ["0", "1"])
+def test_fused_concurrent_host_threads(gpu, monkeypatch, split):
+    # Two host threads, each on its own stream: every call orders its dW
+    # after its own G and its caller's stream after its own dW (split = 1:
+    # the two share the library's per-device side stream and fork / join
+    # events).  Results are bit-identical to the same calls made one after
+    # the other.
+    monkeypatch.setenv("MT_FLCE_SPLIT_PHASE", split)
     cases = []
     for seed in (31, 32):
         X, W, y = make_case(600, 128, 1500, torch.bfloat16, seed=seed)

@@ -377,7 +377,12 @@ def test_segment_sums_of_shifted_labels(gpu):
     assert np.allclose(sl.cpu().numpy(), want_l, rtol=1e-6, atol=0)
 
 
-def test_profile_hook_reports_the_fused_step(gpu):
+@pytest.mark.parametrize("split", ["0", "1"])
+def test_profile_hook_reports_the_fused_step(gpu, monkeypatch, split):
+    """The per-launch events of the reference step: dX and dW in one launch
+    (the phase), or (split = 1, the measurement hook) as two kernels inside
+    the phase, each with its own event."""
+    monkeypatch.setenv("MT_FLCE_SPLIT_PHASE", split)
     X, W, y = make_case(700, 128, 2560, torch.bfloat16, seed=41)
     n = int((y != -100).sum())
     profile_enable(True)
@@ -388,15 +393,19 @@ def test_profile_hook_reports_the_fused_step(gpu):
     rep = profile_report()
     assert path == "fused_unit"
     # (3 dX tiles: the fused dX is split over the vocabulary)
-    for k in ("fwd_bf16_kernel<store_e>", "dx_bf16_kernel<split>",
-              "dw_bf16_kernel", "dx_dw_phase", "scale_rows_kernel<dX>", "narrow_tiles_kernel<dW>"):
+    gemms = ("dx_bf16_kernel<split>", "dw_bf16_kernel") if split == "1" else ()
+    for k in ("fwd_bf16_kernel<store_e>", "dx_dw_phase", "scale_rows_kernel<dX>",
+              "narrow_tiles_kernel<dW>") + gemms:
         assert k in rep and rep[k]["launches"] >= 1 and rep[k]["ms_total"] > 0, k
+    if split == "0":
+        assert not any(k.startswith(("dx_bf16_kernel", "dw_bf16_kernel")) for k in rep)
     # algorithmic work: 2 H V n for each GEMM over all chunks, their sum for the phase
     f = 2.0 * 128 * 2560 * n
-    for k in ("fwd_bf16_kernel<store_e>", "dx_bf16_kernel<split>", "dw_bf16_kernel"):
+    for k in ("fwd_bf16_kernel<store_e>",) + gemms:
         assert rep[k]["flops"] == pytest.approx(f, rel=1e-9)
     assert rep["dx_dw_phase"]["flops"] == pytest.approx(2 * f, rel=1e-9)
-    assert rep["dx_dw_phase"]["ms_total"] >= rep["dw_bf16_kernel"]["ms_total"] * 0.5
+    if split == "1":
+        assert rep["dx_dw_phase"]["ms_total"] >= rep["dw_bf16_kernel"]["ms_total"] * 0.5
     # the report released its records; a disabled hook records nothing
     assert profile_report() == {}
     train_py_chain(gpu, X, W, y, 1, n)
@@ -411,4 +420,4 @@ def test_profile_hook_reports_the_fused_step(gpu):
     lib = _lib.load()
     need = ctypes.c_size_t(0)
     assert lib.mt_flce_profile_report(None, 0, ctypes.byref(need)) == 1 and need.value > 100
-    assert "dw_bf16_kernel" in profile_report()
+    assert "dx_dw_phase" in profile_report()
