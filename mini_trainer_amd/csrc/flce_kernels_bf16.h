@@ -716,10 +716,15 @@ __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const D
 }
 
 // Epilogue of a dW tile when the workgroup has a next tile (nm0, nh0): the
-// stores of this tile interleaved, fragment row by fragment row, with the
-// loads of the next tile's starting values into the same accumulators, so
-// that the loads' latency runs beside the remaining stores instead of
-// before the next tile's first multiplication.
+// stores of this tile and the loads of the next tile's starting values into
+// the same accumulators, so that the loads' latency runs beside the
+// remaining stores instead of before the next tile's first multiplication.
+// Row-major: interleaved fragment row by fragment row (each row's stores go
+// through the LDS transpose).  Tiled: all 64 stores, then all 64 loads, so
+// that the next tile's first multiplications wait for the vector-memory
+// counter to drop to the loads issued after their own, which it can count
+// (at most 63 outstanding); interleaved, they also waited for stores and
+// loads of later rows (phase -0.5% at config 3 on one box).
 template <bool kTiled>
 __device__ __forceinline__ void dw_store_then_load(f32x4_t (&acc)[8][8], const DwArgs& a,
                                                    const EpiCoordsBf& ec, int32_t m0, int32_t h0,
@@ -733,6 +738,10 @@ __device__ __forceinline__ void dw_store_then_load(f32x4_t (&acc)[8][8], const D
       for (int fn = 0; fn < 8; ++fn)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[fm][fn]), r,
                                                dw_tiled_off(ec, fm, fn), 0, 0);
+      sched_fence();
+    }
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
 #pragma unroll
       for (int fn = 0; fn < 8; ++fn)
         acc[fm][fn] = load ? __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
