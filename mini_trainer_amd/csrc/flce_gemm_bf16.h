@@ -89,6 +89,13 @@ __device__ __forceinline__ u32x2_t ds_read_tr(uint32_t addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
   return r;
 }
+// The same at addr + 2048 through the instruction's offset field (no
+// address add between a fragment's two reads).
+__device__ __forceinline__ u32x2_t ds_read_tr_2k(uint32_t addr) {
+  u32x2_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:2048" : "=v"(r) : "v"(addr));
+  return r;
+}
 
 // s_waitcnt vmcnt(0) only (expcnt and lgkmcnt left at their maximum).
 __device__ __forceinline__ void wait_vm0() {
@@ -212,13 +219,18 @@ __device__ __forceinline__ void mask_tail(u32x4_t (&fr)[8], int kk, uint32_t c_l
 // reads' bases differ by constants and share one XOR mask (the lane's K row
 // inside a fragment read, 8 g + 4 h + (L >> 2), fixes tr_swz independently
 // of kk and h).
+// A DMA's address is split into a per-lane part, min(row offset, limit) +
+// column offset, and a uniform scalar offset, base + stage * 64 rows: two
+// full-rate VALU instructions per DMA.  (Formed as base + k ld_b with k
+// clamped per lane, it took a quarter-rate 64-bit multiply-add right before
+// every DMA, which stalled the MFMA issue behind it.)
 struct TrOp {
   static constexpr bool kTr = true;
   rsrc_t rsrc;
   uint32_t base, ld_b;
   int32_t k_limit;
-  uint32_t krow0;
-  uint32_t moff[4];  // [(i >= 4) * 2 + (i & 1)]
+  uint32_t rowoff[kNIBf];  // (16 w + (l >> 5) + 2 i) ld_b: instruction i's K row
+  uint32_t moff[4];        // [(i >= 4) * 2 + (i & 1)]
   uint32_t fbase, fxor;
 
   // r, base: resource and byte offset of (K row 0, column 0) of the tile;
@@ -235,7 +247,9 @@ struct TrOp {
     ld_b = ld_b_;
     k_limit = k_limit_;
     const uint32_t l = lane_id(), w = wave_id();
-    krow0 = 16u * w + (l >> 5);
+    const uint32_t krow0 = 16u * w + (l >> 5);
+#pragma unroll
+    for (int i = 0; i < kNIBf; ++i) rowoff[i] = (krow0 + 2u * (uint32_t)i) * ld_b;
 #pragma unroll
     for (uint32_t p = 0; p < 4; ++p) {
       const uint32_t i = (p >> 1) * 4 + (p & 1);  // representative i of the pattern
@@ -250,11 +264,17 @@ struct TrOp {
     fbase = k * 512u + (c0 & ~15u) * 16u + (L & 1u) * 8u;
     fxor = ((c0 & 15u) ^ tr_swz(k) ^ ((L & 3u) >> 1)) * 16u;
   }
+  // K row kb + r (kb = 64 kt, r = the lane's row in the stage) clamped to
+  // k_limit - 1: kb ld_b goes to the scalar offset and the lane's part is
+  // min(r ld_b, (k_limit - 1 - kb) ld_b); the bound is uniform and at least
+  // 63 ld_b in every stage but a partial last one.
   __device__ __forceinline__ void issue_one(char* tile, int kt, int i) const {
-    int32_t k = kt * kBKBf + (int32_t)(krow0 + 2u * (uint32_t)i);
-    k = k < k_limit ? k : k_limit - 1;
+    const int32_t kb = kt * kBKBf;
+    const int32_t rem = k_limit - 1 - kb;
+    const uint32_t lim = (uint32_t)(rem > 0 ? rem : 0) * ld_b;
+    const uint32_t r = rowoff[i] < lim ? rowoff[i] : lim;
     dma16(rsrc, tile + (wave_id() * kNIBf + (uint32_t)i) * 1024u,
-          base + (uint32_t)k * ld_b + moff[(i >= 4 ? 2 : 0) + (i & 1)], 0u);
+          r + moff[(i >= 4 ? 2 : 0) + (i & 1)], base + (uint32_t)kb * ld_b);
   }
   __device__ __forceinline__ void issue(char* tile, int kt) const {
 #pragma unroll
@@ -265,8 +285,9 @@ struct TrOp {
   // read h add (32 kk + 4 h) K rows of 512 bytes to the base.
   __device__ __forceinline__ u32x4_t read(const char* tile, int kk, int f) const {
     const uint32_t t = lds_addr(tile) + fbase + ((32u * (uint32_t)f) ^ fxor);
-    const u32x2_t lo = ds_read_tr(t + (uint32_t)kk * 32u * 512u);
-    const u32x2_t hi = ds_read_tr(t + (uint32_t)kk * 32u * 512u + 4u * 512u);
+    const uint32_t tk = t + (uint32_t)kk * 32u * 512u;
+    const u32x2_t lo = ds_read_tr(tk);
+    const u32x2_t hi = ds_read_tr_2k(tk);  // 4 K rows of 512 bytes on
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
   }
 };
