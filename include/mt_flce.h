@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define MT_FLCE_ABI_VERSION 5
+#define MT_FLCE_ABI_VERSION 6
 
 typedef struct ihipStream_t* mt_stream_t; /* == hipStream_t */
 
@@ -160,6 +160,24 @@ int mt_flce_forward_noalloc(const void* X, const void* W, int64_t T, int64_t H,
 int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
                           int dtype, size_t budget_bytes, int64_t* chunk_rows,
                           int64_t* chunk_vocab, size_t* workspace_bytes);
+
+/*
+ * The blocking plan of mt_flce_backward_tiles (bf16 only), whose dW is
+ * fresh: with one row block (chunk_rows >= n_valid) and several vocabulary
+ * blocks of at least chunk_rows entries, the vocabulary blocks run last to
+ * first and dX's fp32 accumulator lives in the dW tiles of the first block,
+ * which only that block's dW writes (after its dX has read the accumulator
+ * for the last time).  The workspace then holds no accumulator, so the
+ * budget admits one row block -- every dW tile contracts all valid rows at
+ * once, with no read-modify-write of dW -- where mt_flce_backward_plan has to
+ * cut the rows.  Same arguments and outputs as mt_flce_backward_plan; the
+ * workspace it reports is what mt_flce_backward_tiles requires for that
+ * blocking.  (No reference counterpart: the blocking of the backward that
+ * replaces LIGER:ops/fused_linear_cross_entropy.py::fused_linear_cross_entropy_backward.)
+ */
+int mt_flce_backward_tiles_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
+                                int dtype, size_t budget_bytes, int64_t* chunk_rows,
+                                int64_t* chunk_vocab, size_t* workspace_bytes);
 
 /*
  * Backward: dX = G W and dW (+)= G^T X with

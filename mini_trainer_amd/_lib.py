@@ -10,7 +10,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p, c_char_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmt_flce.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MT_DTYPE_F32 = 0
 MT_DTYPE_BF16 = 1
@@ -40,6 +40,9 @@ SIGNATURES = {
                                         c_void_p, c_void_p, c_void_p]),
     "mt_flce_backward_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t,
                                       POINTER(c_int64), POINTER(c_int64), POINTER(c_size_t)]),
+    "mt_flce_backward_tiles_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t,
+                                            POINTER(c_int64), POINTER(c_int64),
+                                            POINTER(c_size_t)]),
     "mt_flce_backward": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                                  c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                  c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64,

@@ -259,18 +259,22 @@ inline Geometry geometry(int es) {
 inline double dx_flops(const DxArgs& x) { return 2.0 * x.Cn * (double)x.kv * x.H; }
 inline double dw_flops(const DwArgs& w) { return 2.0 * w.cv * (double)w.H * w.kt_rows; }
 inline const char* dx_name(int mode) {
-  static const char* const n[4] = {"dx_bf16_kernel<store>", "dx_bf16_kernel<add>",
-                                   "dx_bf16_kernel<add_emit>", "dx_bf16_kernel<emit>"};
-  return n[mode & 3];
+  static const char* const n[7] = {"dx_bf16_kernel<store>",       "dx_bf16_kernel<add>",
+                                   "dx_bf16_kernel<add_emit>",    "dx_bf16_kernel<emit>",
+                                   "dx_bf16_kernel<store_tiles>", "dx_bf16_kernel<add_tiles>",
+                                   "dx_bf16_kernel<add_emit_tiles>"};
+  return n[mode];
 }
 
 // One dX kernel instantiation per accumulation mode (uniform per launch); one
 // workgroup per output tile (the kernel multiplies exactly one tile, so the
 // grid is never capped).
 inline void launch_dx_bf16(const DxArgs& x, hipStream_t stream) {
-  static void (*const kern[4])(DxArgs) = {dx_bf16_kernel<kDxStore>, dx_bf16_kernel<kDxAdd>,
-                                          dx_bf16_kernel<kDxAddEmit>, dx_bf16_kernel<kDxEmit>};
-  hipLaunchKernelGGL(kern[x.mode & 3], dim3((uint32_t)(x.tiles_m * x.tiles_n * x.nsplit)),
+  static void (*const kern[7])(DxArgs) = {
+      dx_bf16_kernel<kDxStore>, dx_bf16_kernel<kDxAdd>, dx_bf16_kernel<kDxAddEmit>,
+      dx_bf16_kernel<kDxEmit>, dx_bf16_kernel<kDxTiledAcc + kDxStore>,
+      dx_bf16_kernel<kDxTiledAcc + kDxAdd>, dx_bf16_kernel<kDxTiledAcc + kDxAddEmit>};
+  hipLaunchKernelGGL(kern[x.mode], dim3((uint32_t)(x.tiles_m * x.tiles_n * x.nsplit)),
                      dim3(kThreadsBf), 0, stream, x);
 }
 
@@ -313,16 +317,24 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
 #define MT_DXDW(m) \
   {{dx_dw_bf16_kernel<m, false, false>, dx_dw_bf16_kernel<m, false, true>}, \
    {dx_dw_bf16_kernel<m, true, false>, dx_dw_bf16_kernel<m, true, true>}}
-    static const K kern[4][2][2] = {MT_DXDW(kDxStore), MT_DXDW(kDxAdd), MT_DXDW(kDxAddEmit),
-                                    MT_DXDW(kDxEmit)};
+    // (a tiled dX accumulator lives in tiled dW's allocation: tiled dW only)
+#define MT_DXDW_T(m) \
+  {{nullptr, dx_dw_bf16_kernel<kDxTiledAcc + m, false, true>}, \
+   {nullptr, dx_dw_bf16_kernel<kDxTiledAcc + m, true, true>}}
+    static const K kern[7][2][2] = {MT_DXDW(kDxStore),     MT_DXDW(kDxAdd),   MT_DXDW(kDxAddEmit),
+                                    MT_DXDW(kDxEmit),      MT_DXDW_T(kDxStore), MT_DXDW_T(kDxAdd),
+                                    MT_DXDW_T(kDxAddEmit)};
 #undef MT_DXDW
+#undef MT_DXDW_T
+    const K k = kern[x.mode][w.queue ? 1 : 0][w.tiled ? 1 : 0];
+    if (!k) return fail(MT_ERR_UNSUPPORTED, "tiled dX accumulator without tiled dW");
     const double fx = dx_flops(x), fw = dw_flops(w);
     const int64_t dxg = (int64_t)x.tiles_m * x.tiles_n * x.nsplit;
     const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
     const int64_t dwg = w.queue ? device_cus() : (cap > 0 ? std::min(dw_tiles, cap) : dw_tiles);
     const int ph = prof_begin("dx_dw_phase", fx + fw, 0, stream);
-    hipLaunchKernelGGL(kern[x.mode & 3][w.queue ? 1 : 0][w.tiled ? 1 : 0], dim3((uint32_t)(dxg + dwg)),
-                       dim3(kThreadsBf), 0, stream, x, w, (uint32_t)dxg);
+    hipLaunchKernelGGL(k, dim3((uint32_t)(dxg + dwg)), dim3(kThreadsBf), 0, stream, x, w,
+                       (uint32_t)dxg);
     MT_TRY(check_launch("dx_dw_bf16_kernel"));
     if (red) {
       launch_dx_reduce(*red, stream);
@@ -408,10 +420,19 @@ size_t forward_ws(const FwdPlan& p, int64_t n_valid) {
 }
 
 // --------------------------------------------------------------- backward
-size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es) {
+// The tiled entry (a fresh dW, never added into) with one row block (C >= N)
+// and several vocabulary blocks runs the blocks last to first and keeps dX's
+// fp32 accumulator in the dW tiles of the first block (v0 = 0), which only
+// that block's dW writes, after its dX has read the accumulator for the last
+// time.  Those tiles hold Cv x round_up(H, 256) floats >= C x H when Cv >= C.
+inline bool acc_in_tiles(int64_t N, int64_t C, int64_t Cv, int64_t V, int es) {
+  return es == 2 && C >= N && Cv < V && Cv >= C;
+}
+
+size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es, bool acc_in_dw = false) {
   if (C == 0) return 0;
   size_t g = align_up((size_t)C * Cv * es);
-  size_t acc = Cv < V ? align_up((size_t)C * H * sizeof(float)) : 0;
+  size_t acc = Cv < V && !acc_in_dw ? align_up((size_t)C * H * sizeof(float)) : 0;
   size_t xt = align_up((size_t)H * C * es);
   size_t queue = es == 2 ? align_up(kQueueWords * sizeof(uint32_t)) : 0;  // dW work queue
   return g + acc + xt + queue;
@@ -503,7 +524,9 @@ struct BwdPlan {
   size_t ws = 0;
 };
 
-BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t budget) {
+// tiles: the plan of mt_flce_backward_tiles (dW fresh, acc_in_tiles applies).
+BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t budget,
+                      bool tiles = false) {
   BwdPlan best;
   if (N <= 0) return best;
   if (budget == 0) budget = (size_t)((double)T * V * es * 0.05);
@@ -511,14 +534,14 @@ BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t
   BwdPlan smallest;
   smallest.C = 256;
   smallest.Cv = 256;
-  smallest.ws = backward_ws(256, 256, H, V, es);
+  smallest.ws = backward_ws(256, 256, H, V, es, tiles && acc_in_tiles(N, 256, 256, V, es));
   const int64_t max_nt = std::min<int64_t>(cdiv(N, 256), 128);
   const int64_t max_nv = std::min<int64_t>(cdiv(V, 256), 128);
   for (int64_t nt = 1; nt <= max_nt; ++nt) {
     const int64_t C = round_up(cdiv(N, nt), 256);
     for (int64_t nv = 1; nv <= max_nv; ++nv) {
       const int64_t Cv = round_up(cdiv(V, nv), 256);
-      const size_t ws = backward_ws(C, Cv, H, V, es);
+      const size_t ws = backward_ws(C, Cv, H, V, es, tiles && acc_in_tiles(N, C, Cv, V, es));
       // G and X^T are read through 32-bit buffer offsets
       // G, X^T and the block's weight rows (bf16) within one buffer's reach
       const uint64_t lim = buffer_limit();
@@ -630,10 +653,17 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
   constexpr int es = sizeof(T);
   const Geometry geo = geometry(es);
   const int64_t nv = cdiv(V, Cv);
+  // one row block and several vocabulary blocks: the blocks run last to
+  // first (on every path, so that tiled and row-major dW sum dX in the same
+  // order), and into fresh tiles dX's accumulator lives in the tiles of
+  // block 0 (acc_in_tiles)
+  const bool rev = C >= N && nv > 1;
+  const bool acc_dw = tiled && acc_in_tiles(N, C, Cv, V, es);
   char* G = ws;
   float* accbuf = nv > 1 ? reinterpret_cast<float*>(ws + align_up((size_t)C * Cv * es)) : nullptr;
+  if (acc_dw) accbuf = dW + dw_tiles_pad(H);
   char* XcT = ws + align_up((size_t)C * Cv * es) +
-              (nv > 1 ? align_up((size_t)C * H * sizeof(float)) : 0);
+              (nv > 1 && !acc_dw ? align_up((size_t)C * H * sizeof(float)) : 0);
   uint32_t* queue = reinterpret_cast<uint32_t*>(XcT + align_up((size_t)H * C * es));
   const int64_t ldg_b = Cv * es, ldxt_b = C * es;
 
@@ -644,8 +674,8 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
                        dim3(256), 0, stream, static_cast<const char*>(X), ldx * es, row_index + c0,
                        (int32_t)cn, (int32_t)H, XcT, ldxt_b);
     MT_TRY(check_launch("gather_t_kernel"));
-    int64_t j = 0;
-    for (int64_t v0 = 0; v0 < V; v0 += Cv, ++j) {
+    for (int64_t j = 0; j < nv; ++j) {
+      const int64_t v0 = (rev ? nv - 1 - j : j) * Cv;
       const int64_t cv = std::min(Cv, V - v0);
       // the block's weight rows start at v0 (W rebased: 32-bit offsets)
       const char* Wv = static_cast<const char*>(W) + v0 * ldw * es;
@@ -706,20 +736,26 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       x.accbuf = accbuf;
       x.ld_acc = H;
       x.mode = nv == 1 ? kDxEmit : (j == 0 ? kDxStore : (j == nv - 1 ? kDxAddEmit : kDxAdd));
+      if (acc_dw) x.mode += kDxTiledAcc;  // (nv > 1: never kDxEmit)
       x.dX = static_cast<char*>(dX);
       x.lddx_b = lddx * es;
       x.row_index = row_index + c0;
       x.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       x.tiles_n = (int32_t)cdiv(H, geo.tile_n);
       // dX with fewer tiles than CUs leaves CUs idle for its whole (long) K:
-      // dW then runs beside it on the side stream.  Otherwise dX and the
+      // dW then runs beside it, in the same launch.  Otherwise dX and the
       // persistent dW run one after the other on the caller's stream
       // (measured: side by side costs config 3's general path 2%, gains
-      // config 5's 2%).
+      // config 5's 2%).  With the accumulator in the tiles (one row block),
+      // every block but block 0 runs dX and dW in one launch whatever dX's
+      // tile count (dW's workgroups fill the CUs dX's last round leaves);
+      // block 0, run last, runs dX (the accumulator's last reader) before dW
+      // (which overwrites it).
       // (the grid-cap test hook stands in for a smaller GPU here too, so small
       // tests reach the one-after-the-other form)
       const int64_t cus = grid_cap() > 0 ? std::min(grid_cap(), device_cus()) : device_cus();
-      const bool beside = sizeof(T) == 2 && (int64_t)x.tiles_m * x.tiles_n < cus;
+      const bool beside = sizeof(T) == 2 &&
+                          (acc_dw ? j < nv - 1 : (int64_t)x.tiles_m * x.tiles_n < cus);
       // dW beside dX over the work queue (as on the fused path), which the
       // recompute launch just before the fork clears
       const bool use_queue = beside && cdiv(cv, 256) * cdiv(H, 256) >= 4 * device_cus() &&
@@ -1188,9 +1224,13 @@ int mt_flce_forward_noalloc(const void* X, const void* W, int64_t T, int64_t H, 
   return MT_OK;
 }
 
-int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
-                          size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
-                          size_t* workspace_bytes) {
+}  // extern "C"
+
+namespace {
+
+int backward_plan_entry(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
+                        size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
+                        size_t* workspace_bytes, bool tiles) {
   const int es = esize_of(dtype);
   if (!es) return fail(MT_ERR_INVALID_ARGUMENT, "dtype %d is not MT_DTYPE_F32 or MT_DTYPE_BF16", dtype);
   if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0)
@@ -1198,11 +1238,31 @@ int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int 
                 (long long)n_valid, (long long)H, (long long)V);
   if (!chunk_rows || !chunk_vocab || !workspace_bytes)
     return fail(MT_ERR_INVALID_ARGUMENT, "null output pointer");
-  const BwdPlan p = plan_backward(T, n_valid, H, V, es, budget_bytes);
+  if (tiles && dtype != MT_DTYPE_BF16)
+    return fail(MT_ERR_UNSUPPORTED, "tiled dW is bf16 only (dtype %d)", dtype);
+  const BwdPlan p = plan_backward(T, n_valid, H, V, es, budget_bytes, tiles);
   *chunk_rows = p.C;
   *chunk_vocab = p.Cv;
   *workspace_bytes = p.ws;
   return MT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
+                          size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
+                          size_t* workspace_bytes) {
+  return backward_plan_entry(T, n_valid, H, V, dtype, budget_bytes, chunk_rows, chunk_vocab,
+                             workspace_bytes, false);
+}
+
+int mt_flce_backward_tiles_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
+                                size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
+                                size_t* workspace_bytes) {
+  return backward_plan_entry(T, n_valid, H, V, dtype, budget_bytes, chunk_rows, chunk_vocab,
+                             workspace_bytes, true);
 }
 
 }  // extern "C"
@@ -1244,7 +1304,8 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
                   "chunk_rows=%lld x chunk_vocab=%lld: G block, X^T or the block's weight rows beyond "
                   "one buffer's reach (4 GiB, or MT_FLCE_MAX_BUFFER_BYTES)",
                   (long long)chunk_rows, (long long)chunk_vocab);
-    const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es);
+    const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es,
+                                   tiled && acc_in_tiles(n_valid, chunk_rows, chunk_vocab, V, es));
     if (workspace_bytes < need || !workspace)
       return fail(MT_ERR_WORKSPACE_TOO_SMALL, "backward workspace %zu bytes < required %zu",
                   workspace_bytes, need);

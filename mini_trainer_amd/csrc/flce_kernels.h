@@ -425,6 +425,10 @@ MT_GEMM_KERNEL void recompute_kernel(RecompArgs a) {
 // Backward, step 2: dX rows of the block (+)= G . W[v0 : v0 + cv]
 // ===========================================================================
 enum DxMode : int32_t { kDxStore = 0, kDxAdd = 1, kDxAddEmit = 2, kDxEmit = 3 };
+// bf16 only: kDxStore / kDxAdd / kDxAddEmit with the fp32 accumulator held as
+// 256 x 256 tiles (accbuf + (tm * tiles_n + tn) * 65536 floats, each in the
+// order of the wave's accumulators: one contiguous KiB per load and store)
+constexpr int32_t kDxTiledAcc = 4;
 
 struct DxArgs {
   const char* G;
@@ -434,7 +438,7 @@ struct DxArgs {
   uint32_t g_range, w_range;  // bytes addressable from G, W
   int32_t V, v0, kv;  // K = vocabulary entries v0 .. v0 + kv
   int32_t H, Cn;
-  float* accbuf;  // fp32 [>= Cn][ld_acc]
+  float* accbuf;  // fp32 [>= Cn][ld_acc] (modes >= kDxTiledAcc: tiles_m x tiles_n tiles)
   int64_t ld_acc;
   int32_t mode;
   char* dX;

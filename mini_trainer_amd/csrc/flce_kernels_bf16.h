@@ -487,9 +487,58 @@ MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
 // fragment row at a time: bounds checks guard single stores, and a scheduling
 // fence after each half row -- in uniform control flow -- keeps one group's
 // values in registers.
+// kMode >= kDxTiledAcc: the accumulator of tile (row0, h0) is one 256 KiB
+// tile in the accumulators' own order (the wave's 64 KiB, fragment (fm, fn)
+// at (fm * 8 + fn) KiB of it, the lane's 16 bytes at lane * 16), so every
+// load and store covers one contiguous KiB.  Rows past Cn are neither
+// stored nor emitted (their accumulators are never read); the control flow
+// is that of the row-major modes (with unconditional stores the compiler
+// spilled the main loop's registers).
+template <int kMode>
+__device__ __forceinline__ void dx_epilogue_tiled_acc(const f32x4_t (&acc)[8][8], const DxArgs& a,
+                                                      const EpiCoordsBf& ec, int32_t row0,
+                                                      int32_t h0) {
+  constexpr int kM = kMode - kDxTiledAcc;
+  const int64_t tile = (int64_t)(row0 / 256) * a.tiles_n + h0 / 256;
+  float* const base =
+      a.accbuf + tile * 65536 + (int64_t)((ec.wm * 2u + ec.wn) * 16384u + ec.lane * 4u);
+#pragma unroll
+  for (int fm = 0; fm < 8; ++fm) {
+    const int32_t rowl = row0 + ec.row(fm);
+    const bool rv = rowl < a.Cn;
+    char* xrow = kM == kDxAddEmit ? a.dX + (int64_t)a.row_index[rv ? rowl : 0] * a.lddx_b : nullptr;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int fn = 4 * half + q;
+        const int32_t h = h0 + ec.col(fn);
+        float* const slot = base + (fm * 8 + fn) * 256;
+        f32x4_t v = acc[fm][fn];
+        if (rv && h < a.H) {
+          if (kM == kDxAdd || kM == kDxAddEmit) v += *reinterpret_cast<const f32x4_t*>(slot);
+          if (kM <= kDxAdd) {
+            *reinterpret_cast<f32x4_t*>(slot) = v;
+          } else {
+            u32x2_t o;
+            o[0] = pack_bf16x2(v[0], v[1]);
+            o[1] = pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<u32x2_t*>(xrow + (int64_t)h * 2) = o;
+          }
+        }
+      }
+      sched_fence();
+    }
+  }
+}
+
 template <int kMode>
 __device__ __forceinline__ void dx_epilogue_bf16(const f32x4_t (&acc)[8][8], const DxArgs& a,
                                                  const EpiCoordsBf& ec, int32_t row0, int32_t h0) {
+  if constexpr (kMode >= kDxTiledAcc) {
+    dx_epilogue_tiled_acc<kMode>(acc, a, ec, row0, h0);
+    return;
+  }
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
     const int32_t rowl = row0 + ec.row(fm);

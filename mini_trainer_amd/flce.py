@@ -106,15 +106,17 @@ def prepare_targets(target: torch.Tensor, vocab_size: int, ignore_index: int = -
 
 
 def backward_plan(T: int, n_valid: int, H: int, V: int, dtype: torch.dtype,
-                  budget_bytes: Optional[int] = None) -> Tuple[int, int, int]:
-    """(chunk_rows, chunk_vocab, workspace_bytes) of the backward blocking."""
+                  budget_bytes: Optional[int] = None, tiles: bool = False) -> Tuple[int, int, int]:
+    """(chunk_rows, chunk_vocab, workspace_bytes) of the backward blocking;
+    tiles: the plan of mt_flce_backward_tiles (a fresh tiled dW, which may
+    hold dX's accumulator), else of mt_flce_backward."""
     lib = load()
     if budget_bytes is None:
         budget_bytes = int(os.environ.get(BACKWARD_BUDGET_ENV, "0"))
     c, cv, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_size_t()
-    check(lib.mt_flce_backward_plan(T, n_valid, H, V, _dtype_code(dtype), budget_bytes,
-                                    ctypes.byref(c), ctypes.byref(cv), ctypes.byref(ws)),
-          "mt_flce_backward_plan")
+    fn = "mt_flce_backward_tiles_plan" if tiles else "mt_flce_backward_plan"
+    check(getattr(lib, fn)(T, n_valid, H, V, _dtype_code(dtype), budget_bytes, ctypes.byref(c),
+                           ctypes.byref(cv), ctypes.byref(ws)), fn)
     return c.value, cv.value, ws.value
 
 
@@ -264,9 +266,10 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         dev = X.device
         g, gstride = _grad_vector(grad_loss, T)
         dX = torch.empty((T, H), dtype=X.dtype, device=dev)
-        C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
+        tiles = acc is None and dt == MT_DTYPE_BF16
+        C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype, tiles=tiles)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        if acc is None and dt == MT_DTYPE_BF16:
+        if tiles:
             # dW as 256 x 256 fp32 tiles, narrowed into bf16 in its own allocation
             dW = _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX,
                                  C, Cv, ws)
@@ -356,7 +359,7 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         else:
             # a per-token gradient: the unit-gradient results cannot be
             # rescaled; recompute into the same buffers
-            C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
+            C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype, tiles=True)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
             _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX, C, Cv,
                             ws, dW)

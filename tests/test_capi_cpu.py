@@ -186,6 +186,27 @@ def test_backward_plan_fits_budget(key):
     assert ws == expect
 
 
+@pytest.mark.parametrize("key", [2, 3, 4, 5])
+def test_backward_tiles_plan_fits_budget(key):
+    """The tiled entry's plan: within the budget; with one row block and
+    several vocabulary blocks of at least C entries its workspace holds no dX
+    accumulator (it lives in the tiles), otherwise it is mt_flce_backward's.
+    Config 5 (H = 8192, a 210 MB budget) takes one row block per minibatch."""
+    cfg = synth.CONFIGS[key]
+    n = int((synth.make_batch(cfg, 0, with_tensors=False)["target"] != -100).sum())
+    C, Cv, ws = backward_plan(cfg.T, n, cfg.H, cfg.V, cfg.dtype, tiles=True)
+    assert C % 256 == 0 and Cv % 256 == 0 and ws <= 0.05 * cfg.T * cfg.V * 2
+    al = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    in_tiles = n <= C <= Cv < cfg.V
+    expect = (al(C * Cv * 2) + (al(C * cfg.H * 4) if Cv < cfg.V and not in_tiles else 0) +
+              al(cfg.H * C * 2) + al(8 * 4))
+    assert ws == expect
+    if key == 5:
+        assert in_tiles and C >= n
+    with pytest.raises(_lib.FlceError):
+        backward_plan(cfg.T, n, cfg.H, cfg.V, torch.float32, tiles=True)
+
+
 def test_backward_plan_budget_override_and_degenerate():
     C, Cv, ws = backward_plan(1000, 700, 128, 5000, torch.bfloat16, budget_bytes=1)
     assert (C, Cv) == (256, 256)  # smallest blocks when nothing fits

@@ -116,6 +116,40 @@ def test_general_backward_guards(gpu, case, monkeypatch, softcap):
     assert bool(torch.isfinite(dX[:, :H].float()).all()) and bool(torch.isfinite(dW[:, :H]).all())
 
 
+def test_backward_tiles_accumulator_in_tiles_guards(gpu, case):
+    """mt_flce_backward_tiles on one row block and several vocabulary blocks
+    (dX's fp32 accumulator in the first block's dW tiles), with exactly the
+    workspace mt_flce_backward_tiles_plan reports for that blocking."""
+    X, W, y, ri, rl, n = case
+    lib = _lib.load()
+    s = _stream(gpu)
+    wsb = lib.mt_flce_forward_workspace_bytes(T, n, H, V, _lib.MT_DTYPE_BF16)
+    loss = torch.empty(T, device=gpu)
+    lse = torch.empty(n, device=gpu)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    _lib.check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                   _p(ri), _p(rl), n, _p(loss), _p(lse), _p(ws), wsb, s), "forward")
+    C, Cv = 512, 512  # n < 512 rows; 1300 vocabulary entries in 3 blocks
+    assert n <= C < V
+    budget = C * Cv * 2 + H * C * 2 + 4096
+    pc, pcv, bws = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, tiles=True)
+    assert (pc, pcv) == (C, Cv)
+    assert bws < C * Cv * 2 + C * H * 4  # no accumulator in the workspace
+    grad = torch.rand(T, device=gpu)
+    gdx, dX = matrix(gpu, T, H, H + 8, torch.bfloat16)
+    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    gdw = Guarded(gpu, tb)
+    gws = Guarded(gpu, bws)
+    _lib.check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                          _p(ri), _p(rl), n, _p(lse), _p(grad), 1, gdx.ptr, H + 8,
+                                          gdw.ptr, tb, C, Cv, gws.ptr, bws, s), "backward_tiles")
+    torch.cuda.synchronize()
+    assert gdx.intact() and gdw.intact() and gws.intact()
+    assert pad_intact(dX, H)
+    assert bool(torch.isfinite(dX[:, :H].float()).all())
+    assert bool(torch.isfinite(gdw.view(torch.float32, (tb // 4,))).all())
+
+
 def test_fused_and_rescale_guards(gpu, case):
     X, W, y, ri, rl, n = case
     lib = _lib.load()

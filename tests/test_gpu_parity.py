@@ -122,6 +122,31 @@ def test_multi_block_backward(gpu, monkeypatch):
     check_parity(X, W, y, loss, dX, dW, grad=grad)
 
 
+def test_one_row_block_vocabulary_blocks_reference_chain(gpu, monkeypatch):
+    """The general path without dw_accumulator (mt_flce_backward_tiles) under a
+    budget that fits one row block and several vocabulary blocks: dX's fp32
+    accumulator lives in the tiles of the first vocabulary block (run last).
+    Loss, dX and the bf16 weight gradient against the torch path."""
+    from mini_trainer_amd.flce import FUSED_ENV, backward_plan
+
+    T, H, V = 1100, 128, 13000
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=17, mask_frac=0.2)
+    n = int((y != -100).sum())
+    budget = 1024 * 4096 * 2 + H * 1024 * 2 + (1 << 16)
+    C, Cv, _ = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, tiles=True)
+    assert n <= C <= Cv < V, (n, C, Cv)
+    monkeypatch.setenv(BACKWARD_BUDGET_ENV, str(budget))
+    monkeypatch.setenv(FUSED_ENV, "0")
+    grad = torch.rand(T, generator=torch.Generator().manual_seed(3))
+    Xd = X.to(gpu).requires_grad_(True)
+    Wd = W.to(gpu).requires_grad_(True)
+    loss = fused_linear_cross_entropy(Xd, Wd, y.to(gpu))
+    loss.backward(grad.to(gpu))
+    torch.cuda.synchronize()
+    assert Wd.grad.dtype == torch.bfloat16
+    check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(), grad=grad)
+
+
 def test_accumulate_into_fp32_dw(gpu):
     X, W, y = make_case(300, 128, 700, torch.bfloat16, seed=9)
     X2, _, y2 = make_case(200, 128, 700, torch.bfloat16, seed=10)

@@ -256,7 +256,8 @@ def test_fused_tiles_match_rows_bit_exact(gpu, T, H, V, budget):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("C,Cv,cap", [(256, 52736, None), (256, 16384, "3"), (512, 65600 + 192, None)])
+@pytest.mark.parametrize("C,Cv,cap", [(256, 52736, None), (256, 16384, "3"), (512, 65600 + 192, None),
+                                      (768, 16384, None), (768, 16384, "3")])
 def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     """mt_flce_backward_tiles against mt_flce_backward on the same inputs and
     blocks (per-token upstream gradient): dX the same bits, the tiles,
@@ -264,7 +265,9 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     two row blocks and a vocabulary split whose first block runs dW beside dX
     over the work queue; under a 3-CU grid cap dW runs after dX, three
     persistent workgroups carrying tiles; one block over the whole
-    vocabulary.  V = 65600, H = 1056 (tails in both)."""
+    vocabulary; one row block and five vocabulary blocks (run last to first,
+    the tiled entry's dX accumulator in the first block's tiles, with only the
+    workspace that layout needs).  V = 65600, H = 1056 (tails in both)."""
     print(f"case backward tiles C={C} Cv={Cv} cap={cap}", flush=True)
     if cap:
         monkeypatch.setenv("MT_FLCE_GRID_CAP", cap)
@@ -292,6 +295,10 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
     dX1 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
     dW1 = torch.full((tb // 4,), float("nan"), device=gpu)
+    acc_in_tiles = n <= C <= Cv < V
+    if acc_in_tiles:  # the tiled entry needs no accumulator in its workspace
+        wsb = al(C * Cv * 2) + al(H * C * 2) + al(32)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
     _lib.check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                           _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX1), H,
                                           _p(dW1), tb, C, Cv, _p(ws), wsb, s), "backward_tiles")
