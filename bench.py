@@ -487,7 +487,7 @@ def main():
         north["general_path_frac_of_peak"] = alg_flops / (ms_g / 1e3) / peak_flops
         log(f"promised-gradient step {ms_p:.2f} ms, general path {ms_g:.2f} ms")
         torch.cuda.empty_cache()
-    C, Cv, _ = backward_plan(T, n_valid[0], H, V, cfg.dtype, tiles=cfg.dtype == torch.bfloat16)
+    C, Cv, _ = backward_plan(T, n_valid[0], H, V, cfg.dtype, narrow=cfg.dtype == torch.bfloat16)
     gen_fwd = None
     if not args.step_only:
         gen_fwd = general_forward_roofline(data[0][0], W.detach(), data[0][1], peak_flops,

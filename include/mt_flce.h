@@ -162,22 +162,24 @@ int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
                           int64_t* chunk_vocab, size_t* workspace_bytes);
 
 /*
- * The blocking plan of mt_flce_backward_tiles (bf16 only), whose dW is
- * fresh: with one row block (chunk_rows >= n_valid) and several vocabulary
- * blocks of at least chunk_rows entries, the vocabulary blocks run last to
- * first and dX's fp32 accumulator lives in the dW tiles of the first block,
- * which only that block's dW writes (after its dX has read the accumulator
- * for the last time).  The workspace then holds no accumulator, so the
- * budget admits one row block -- every dW tile contracts all valid rows at
- * once, with no read-modify-write of dW -- where mt_flce_backward_plan has to
- * cut the rows.  Same arguments and outputs as mt_flce_backward_plan; the
- * workspace it reports is what mt_flce_backward_tiles requires for that
- * blocking.  (No reference counterpart: the blocking of the backward that
- * replaces LIGER:ops/fused_linear_cross_entropy.py::fused_linear_cross_entropy_backward.)
+ * The blocking plan of a bf16 backward whose weight gradient is wanted in
+ * bf16 and not added into anything (autograd's lm_head gradient,
+ * none_reduction_losses.py:35 through its backward).  When one row block
+ * (chunk_rows >= n_valid) fits the budget and its cost model ranks it first,
+ * the caller runs mt_flce_backward_narrow with it: every dW tile contracts
+ * all valid rows at once and is written once, in bf16 -- no read-modify-
+ * write of an fp32 dW, no narrowing pass -- and dX's fp32 accumulator lives
+ * in the dW buffer's unused half, so the workspace holds only the G block,
+ * X^T and counters.  Otherwise (chunk_rows < n_valid) the caller runs
+ * mt_flce_backward_tiles and mt_flce_narrow_tiles with the same blocking
+ * and workspace.  Same arguments and outputs as mt_flce_backward_plan.  (No
+ * reference counterpart: the blocking of the backward that replaces
+ * LIGER:ops/fused_linear_cross_entropy.py::fused_linear_cross_entropy_backward.)
  */
-int mt_flce_backward_tiles_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
-                                int dtype, size_t budget_bytes, int64_t* chunk_rows,
-                                int64_t* chunk_vocab, size_t* workspace_bytes);
+int mt_flce_backward_narrow_plan(int64_t T, int64_t n_valid, int64_t H,
+                                 int64_t V, int dtype, size_t budget_bytes,
+                                 int64_t* chunk_rows, int64_t* chunk_vocab,
+                                 size_t* workspace_bytes);
 
 /*
  * Backward: dX = G W and dW (+)= G^T X with
@@ -262,6 +264,29 @@ int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H,
                            int64_t chunk_rows, int64_t chunk_vocab,
                            void* workspace, size_t workspace_bytes,
                            mt_stream_t stream);
+
+/*
+ * mt_flce_backward for one row block (chunk_rows >= n_valid, from
+ * mt_flce_backward_narrow_plan) whose weight gradient is written in bf16,
+ * bf16 only, H a multiple of 8: dW_buf (mt_flce_dw_tiles_bytes(V, H) bytes)
+ * receives the gradient as contiguous bf16 rows [V, H] in its first V H 2
+ * bytes -- each 256 x 256 tile narrowed once from its fp32 accumulators
+ * (round to nearest even) -- and the rest of the buffer is scratch (dX's
+ * fp32 accumulator, when it fits).  Bit for bit what mt_flce_backward_tiles
+ * and mt_flce_narrow_tiles with a unit scale give for the same blocking.
+ * Replaces the same reference interface as mt_flce_backward (the lm_head
+ * backward's dW = dS^T X, none_reduction_losses.py:35 through autograd).
+ */
+int mt_flce_backward_narrow(const void* X, const void* W, int64_t T, int64_t H,
+                            int64_t V, int64_t ldx, int64_t ldw, int dtype,
+                            float softcap, const int32_t* row_index,
+                            const int32_t* row_label, int64_t n_valid,
+                            const float* lse, const float* grad_loss,
+                            int64_t grad_stride, void* dX, int64_t lddx,
+                            void* dW_buf, size_t dw_buf_bytes,
+                            int64_t chunk_rows, int64_t chunk_vocab,
+                            void* workspace, size_t workspace_bytes,
+                            mt_stream_t stream);
 
 /*
  * Bytes of the tiled fp32 weight gradient that mt_flce_fused_tiles and

@@ -40,7 +40,7 @@ SIGNATURES = {
                                         c_void_p, c_void_p, c_void_p]),
     "mt_flce_backward_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t,
                                       POINTER(c_int64), POINTER(c_int64), POINTER(c_size_t)]),
-    "mt_flce_backward_tiles_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t,
+    "mt_flce_backward_narrow_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t,
                                             POINTER(c_int64), POINTER(c_int64),
                                             POINTER(c_size_t)]),
     "mt_flce_backward": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
@@ -54,6 +54,10 @@ SIGNATURES = {
                               c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int,
                               c_int64, c_void_p, c_size_t, c_void_p]),
     "mt_flce_backward_tiles": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                       c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
+                                       c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                       c_size_t, c_int64, c_int64, c_void_p, c_size_t, c_void_p]),
+    "mt_flce_backward_narrow": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                        c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
                                        c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                                        c_size_t, c_int64, c_int64, c_void_p, c_size_t, c_void_p]),

@@ -314,20 +314,28 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
                       const DxReduce* red = nullptr) {
   if (!split_phase()) {
     using K = void (*)(DxArgs, DwArgs, uint32_t);
-#define MT_DXDW(m) \
-  {{dx_dw_bf16_kernel<m, false, false>, dx_dw_bf16_kernel<m, false, true>}, \
-   {dx_dw_bf16_kernel<m, true, false>, dx_dw_bf16_kernel<m, true, true>}}
-    // (a tiled dX accumulator lives in tiled dW's allocation: tiled dW only)
-#define MT_DXDW_T(m) \
-  {{nullptr, dx_dw_bf16_kernel<kDxTiledAcc + m, false, true>}, \
-   {nullptr, dx_dw_bf16_kernel<kDxTiledAcc + m, true, true>}}
-    static const K kern[7][2][2] = {MT_DXDW(kDxStore),     MT_DXDW(kDxAdd),   MT_DXDW(kDxAddEmit),
-                                    MT_DXDW(kDxEmit),      MT_DXDW_T(kDxStore), MT_DXDW_T(kDxAdd),
-                                    MT_DXDW_T(kDxAddEmit)};
+    // [dX mode][queue][dW output]; a tiled dX accumulator only beside the
+    // narrowing dW (the one-row-block entry), which never meets an untiled
+    // multi-block accumulator (kDxStore .. kDxAddEmit)
+#define MT_DXDW(m)                                                                        \
+  {{dx_dw_bf16_kernel<m, false, kDwRows>, dx_dw_bf16_kernel<m, false, kDwTiles>, nullptr}, \
+   {dx_dw_bf16_kernel<m, true, kDwRows>, dx_dw_bf16_kernel<m, true, kDwTiles>, nullptr}}
+#define MT_DXDW_N(m)                                                  \
+  {{nullptr, nullptr, dx_dw_bf16_kernel<m, false, kDwNarrow>}, \
+   {nullptr, nullptr, dx_dw_bf16_kernel<m, true, kDwNarrow>}}
+    static const K kern[7][2][3] = {
+        MT_DXDW(kDxStore), MT_DXDW(kDxAdd), MT_DXDW(kDxAddEmit),
+        {{dx_dw_bf16_kernel<kDxEmit, false, kDwRows>, dx_dw_bf16_kernel<kDxEmit, false, kDwTiles>,
+          dx_dw_bf16_kernel<kDxEmit, false, kDwNarrow>},
+         {dx_dw_bf16_kernel<kDxEmit, true, kDwRows>, dx_dw_bf16_kernel<kDxEmit, true, kDwTiles>,
+          dx_dw_bf16_kernel<kDxEmit, true, kDwNarrow>}},
+        MT_DXDW_N(kDxTiledAcc + kDxStore), MT_DXDW_N(kDxTiledAcc + kDxAdd),
+        MT_DXDW_N(kDxTiledAcc + kDxAddEmit)};
 #undef MT_DXDW
-#undef MT_DXDW_T
-    const K k = kern[x.mode][w.queue ? 1 : 0][w.tiled ? 1 : 0];
-    if (!k) return fail(MT_ERR_UNSUPPORTED, "tiled dX accumulator without tiled dW");
+#undef MT_DXDW_N
+    const int out = w.narrow ? kDwNarrow : (w.tiled ? kDwTiles : kDwRows);
+    const K k = kern[x.mode][w.queue ? 1 : 0][out];
+    if (!k) return fail(MT_ERR_UNSUPPORTED, "dX mode %d beside dW output %d", x.mode, out);
     const double fx = dx_flops(x), fw = dw_flops(w);
     const int64_t dxg = (int64_t)x.tiles_m * x.tiles_n * x.nsplit;
     const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
@@ -363,10 +371,15 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
   if (w.queue) {
     // persistent over the work queue: one workgroup per CU (a multiple of
     // the 8 XCDs), each tile >= 2 K stages (dw_bf16_kernel<true>)
-    void (*kern)(DwArgs) = w.tiled ? dw_bf16_kernel<true, true> : dw_bf16_kernel<true, false>;
+    static void (*const kq[3])(DwArgs) = {dw_bf16_kernel<true, kDwRows>, dw_bf16_kernel<true, kDwTiles>,
+                                          dw_bf16_kernel<true, kDwNarrow>};
+    void (*kern)(DwArgs) = kq[w.narrow ? kDwNarrow : (w.tiled ? kDwTiles : kDwRows)];
     hipLaunchKernelGGL(kern, dim3((uint32_t)device_cus()), dim3(kThreadsBf), 0, side->stream, w);
   } else {
-    void (*kern)(DwArgs) = w.tiled ? dw_bf16_kernel<false, true> : dw_bf16_kernel<false, false>;
+    static void (*const kd[3])(DwArgs) = {dw_bf16_kernel<false, kDwRows>,
+                                          dw_bf16_kernel<false, kDwTiles>,
+                                          dw_bf16_kernel<false, kDwNarrow>};
+    void (*kern)(DwArgs) = kd[w.narrow ? kDwNarrow : (w.tiled ? kDwTiles : kDwRows)];
     hipLaunchKernelGGL(kern, dim3((uint32_t)(cap > 0 ? std::min(dw_tiles, cap) : dw_tiles)),
                        dim3(kThreadsBf), 0, side->stream, w);
   }
@@ -420,19 +433,12 @@ size_t forward_ws(const FwdPlan& p, int64_t n_valid) {
 }
 
 // --------------------------------------------------------------- backward
-// The tiled entry (a fresh dW, never added into) with one row block (C >= N)
-// and several vocabulary blocks runs the blocks last to first and keeps dX's
-// fp32 accumulator in the dW tiles of the first block (v0 = 0), which only
-// that block's dW writes, after its dX has read the accumulator for the last
-// time.  Those tiles hold Cv x round_up(H, 256) floats >= C x H when Cv >= C.
-inline bool acc_in_tiles(int64_t N, int64_t C, int64_t Cv, int64_t V, int es) {
-  return es == 2 && C >= N && Cv < V && Cv >= C;
-}
-
-size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es, bool acc_in_dw = false) {
+// acc_outside: dX's accumulator lives outside the workspace (the narrowing
+// entry's dW buffer, narrow_acc).
+size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es, bool acc_outside = false) {
   if (C == 0) return 0;
   size_t g = align_up((size_t)C * Cv * es);
-  size_t acc = Cv < V && !acc_in_dw ? align_up((size_t)C * H * sizeof(float)) : 0;
+  size_t acc = Cv < V && !acc_outside ? align_up((size_t)C * H * sizeof(float)) : 0;
   size_t xt = align_up((size_t)H * C * es);
   size_t queue = es == 2 ? align_up(kQueueWords * sizeof(uint32_t)) : 0;  // dW work queue
   return g + acc + xt + queue;
@@ -464,13 +470,17 @@ double gemm_time(int64_t tiles, int64_t k, int64_t extra = 0) {
 // dX (dx_items tiles of depth dx_k, one per CU) beside dW (dw_tiles of depth
 // dw_k over the work queue): the CU time of both spread over the chip, but
 // never shorter than one dX tile.
-double phase_time(int64_t dx_items, int64_t dx_k, int64_t dw_tiles, int64_t dw_k) {
-  const double cu = dx_items * tile_time(dx_k) + dw_tiles * tile_time(dw_k, kDwRmwK);
+double phase_time(int64_t dx_items, int64_t dx_k, int64_t dw_tiles, int64_t dw_k,
+                  int64_t dw_extra = kDwRmwK) {
+  const double cu = dx_items * tile_time(dx_k) + dw_tiles * tile_time(dw_k, dw_extra);
   return std::max(cu / kCUs, tile_time(dx_k)) + 2 * kLaunch;
 }
 
-// Modelled seconds for one backward with blocks of C x Cv.
-double backward_cost(int64_t N, int64_t H, int64_t V, int64_t C, int64_t Cv, int es) {
+// Modelled seconds for one backward with blocks of C x Cv.  narrow: the
+// narrowing entry (one row block, dW tiles stored once in bf16, dX and dW
+// of every block in one launch).
+double backward_cost(int64_t N, int64_t H, int64_t V, int64_t C, int64_t Cv, int es,
+                     bool narrow = false) {
   (void)es;
   double t = 0, bytes = 0;
   for (int64_t c0 = 0; c0 < N; c0 += C) {
@@ -479,7 +489,9 @@ double backward_cost(int64_t N, int64_t H, int64_t V, int64_t C, int64_t Cv, int
     for (int64_t v0 = 0; v0 < V; v0 += Cv) {
       const int64_t cv = std::min(Cv, V - v0), tv = cdiv(cv, 256);
       t += gemm_time(tm * tv, H);
-      if (tm * th < kCUs)
+      if (narrow)
+        t += phase_time(tm * th, cv, tv * th, cn, 0);
+      else if (tm * th < kCUs)
         t += phase_time(tm * th, cv, tv * th, cn);  // dW beside dX
       else
         t += gemm_time(tm * th, cv) + gemm_time(tv * th, cn, kDwRmwK);
@@ -524,24 +536,45 @@ struct BwdPlan {
   size_t ws = 0;
 };
 
-// tiles: the plan of mt_flce_backward_tiles (dW fresh, acc_in_tiles applies).
+// Bytes of dX's fp32 accumulator as 256 x 256 tiles (kDxTiledAcc modes).
+size_t tiled_acc_bytes(int64_t C, int64_t H) {
+  return (size_t)cdiv(C, 256) * cdiv(H, 256) * 65536 * sizeof(float);
+}
+// The narrowing entry's dW buffer (mt_flce_dw_tiles_bytes) holds the bf16
+// gradient in its first V H 2 bytes; dX's tiled accumulator goes after them
+// when it fits (else into the workspace, row-major).
+size_t dw_tiles_bytes(int64_t V, int64_t H);
+inline size_t narrow_acc_offset(int64_t V, int64_t H) { return align_up((size_t)V * H * 2); }
+inline bool narrow_acc_in_buffer(int64_t V, int64_t H, int64_t C) {
+  return dw_tiles_bytes(V, H) >= narrow_acc_offset(V, H) + tiled_acc_bytes(C, H);
+}
+
+// narrow: the plan of a bf16 backward whose dW is wanted in bf16 without an
+// accumulator (mt_flce_backward_narrow_plan).  One row block (C >= N) runs
+// mt_flce_backward_narrow: no dW read-modify-write, no narrowing pass, and
+// dX's accumulator in the dW buffer; more row blocks run
+// mt_flce_backward_tiles and the narrowing pass, which the cost includes.
 BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t budget,
-                      bool tiles = false) {
+                      bool narrow = false) {
   BwdPlan best;
   if (N <= 0) return best;
   if (budget == 0) budget = (size_t)((double)T * V * es * 0.05);
+  narrow = narrow && es == 2;
   double best_cost = 1e300;
   BwdPlan smallest;
   smallest.C = 256;
   smallest.Cv = 256;
-  smallest.ws = backward_ws(256, 256, H, V, es, tiles && acc_in_tiles(N, 256, 256, V, es));
+  smallest.ws = backward_ws(256, 256, H, V, es,
+                            narrow && N <= 256 && narrow_acc_in_buffer(V, H, 256));
   const int64_t max_nt = std::min<int64_t>(cdiv(N, 256), 128);
   const int64_t max_nv = std::min<int64_t>(cdiv(V, 256), 128);
+  const double narrow_pass = (double)V * H * 6 / kBw + 10 * kLaunch;
   for (int64_t nt = 1; nt <= max_nt; ++nt) {
     const int64_t C = round_up(cdiv(N, nt), 256);
+    const bool one = narrow && nt == 1;
     for (int64_t nv = 1; nv <= max_nv; ++nv) {
       const int64_t Cv = round_up(cdiv(V, nv), 256);
-      const size_t ws = backward_ws(C, Cv, H, V, es, tiles && acc_in_tiles(N, C, Cv, V, es));
+      const size_t ws = backward_ws(C, Cv, H, V, es, one && narrow_acc_in_buffer(V, H, C));
       // G and X^T are read through 32-bit buffer offsets
       // G, X^T and the block's weight rows (bf16) within one buffer's reach
       const uint64_t lim = buffer_limit();
@@ -549,7 +582,8 @@ BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t
           (es == 2 && (uint64_t)Cv * H * es > lim))
         continue;
       if (ws > budget) continue;
-      const double cost = backward_cost(N, H, V, C, Cv, es);
+      const double cost =
+          backward_cost(N, H, V, C, Cv, es, one) + (narrow && !one ? narrow_pass : 0.0);
       if (cost < best_cost * 0.999) {
         best_cost = cost;
         best.C = C;
@@ -648,22 +682,19 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
                     int64_t ldw,
                     float softcap, const int32_t* row_index, const int32_t* row_label,
                     int64_t N, const float* lse, const float* grad, int64_t gstride, void* dX,
-                    int64_t lddx, float* dW, int64_t lddw, int accumulate, bool tiled, int64_t C,
-                    int64_t Cv, char* ws, hipStream_t stream) {
+                    int64_t lddx, float* dW, int64_t lddw, int accumulate, int dw_out, int64_t C,
+                    int64_t Cv, char* ws, hipStream_t stream, float* acc_ext = nullptr) {
   constexpr int es = sizeof(T);
   const Geometry geo = geometry(es);
   const int64_t nv = cdiv(V, Cv);
-  // one row block and several vocabulary blocks: the blocks run last to
-  // first (on every path, so that tiled and row-major dW sum dX in the same
-  // order), and into fresh tiles dX's accumulator lives in the tiles of
-  // block 0 (acc_in_tiles)
-  const bool rev = C >= N && nv > 1;
-  const bool acc_dw = tiled && acc_in_tiles(N, C, Cv, V, es);
+  // acc_ext (the narrowing entry, one row block): dX's accumulator as tiles
+  // outside the workspace
   char* G = ws;
   float* accbuf = nv > 1 ? reinterpret_cast<float*>(ws + align_up((size_t)C * Cv * es)) : nullptr;
-  if (acc_dw) accbuf = dW + dw_tiles_pad(H);
+  const bool acc_tiles = acc_ext != nullptr && nv > 1;
+  if (acc_tiles) accbuf = acc_ext;
   char* XcT = ws + align_up((size_t)C * Cv * es) +
-              (nv > 1 && !acc_dw ? align_up((size_t)C * H * sizeof(float)) : 0);
+              (nv > 1 && !acc_tiles ? align_up((size_t)C * H * sizeof(float)) : 0);
   uint32_t* queue = reinterpret_cast<uint32_t*>(XcT + align_up((size_t)H * C * es));
   const int64_t ldg_b = Cv * es, ldxt_b = C * es;
 
@@ -674,8 +705,8 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
                        dim3(256), 0, stream, static_cast<const char*>(X), ldx * es, row_index + c0,
                        (int32_t)cn, (int32_t)H, XcT, ldxt_b);
     MT_TRY(check_launch("gather_t_kernel"));
-    for (int64_t j = 0; j < nv; ++j) {
-      const int64_t v0 = (rev ? nv - 1 - j : j) * Cv;
+    int64_t j = 0;
+    for (int64_t v0 = 0; v0 < V; v0 += Cv, ++j) {
       const int64_t cv = std::min(Cv, V - v0);
       // the block's weight rows start at v0 (W rebased: 32-bit offsets)
       const char* Wv = static_cast<const char*>(W) + v0 * ldw * es;
@@ -736,7 +767,7 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       x.accbuf = accbuf;
       x.ld_acc = H;
       x.mode = nv == 1 ? kDxEmit : (j == 0 ? kDxStore : (j == nv - 1 ? kDxAddEmit : kDxAdd));
-      if (acc_dw) x.mode += kDxTiledAcc;  // (nv > 1: never kDxEmit)
+      if (acc_tiles) x.mode += kDxTiledAcc;  // (nv > 1: never kDxEmit)
       x.dX = static_cast<char*>(dX);
       x.lddx_b = lddx * es;
       x.row_index = row_index + c0;
@@ -746,16 +777,14 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       // dW then runs beside it, in the same launch.  Otherwise dX and the
       // persistent dW run one after the other on the caller's stream
       // (measured: side by side costs config 3's general path 2%, gains
-      // config 5's 2%).  With the accumulator in the tiles (one row block),
-      // every block but block 0 runs dX and dW in one launch whatever dX's
-      // tile count (dW's workgroups fill the CUs dX's last round leaves);
-      // block 0, run last, runs dX (the accumulator's last reader) before dW
-      // (which overwrites it).
+      // config 5's 2%).  The narrowing entry (one row block) runs dX and dW
+      // of every block in one launch whatever dX's tile count (dW's
+      // workgroups fill the CUs dX's last round leaves).
       // (the grid-cap test hook stands in for a smaller GPU here too, so small
       // tests reach the one-after-the-other form)
       const int64_t cus = grid_cap() > 0 ? std::min(grid_cap(), device_cus()) : device_cus();
       const bool beside = sizeof(T) == 2 &&
-                          (acc_dw ? j < nv - 1 : (int64_t)x.tiles_m * x.tiles_n < cus);
+                          (dw_out == kDwNarrow || (int64_t)x.tiles_m * x.tiles_n < cus);
       // dW beside dX over the work queue (as on the fused path), which the
       // recompute launch just before the fork clears
       const bool use_queue = beside && cdiv(cv, 256) * cdiv(H, 256) >= 4 * device_cus() &&
@@ -789,11 +818,12 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
       w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
       w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
-      if (tiled) {  // (bf16 only; the block's tile rows start at v0 / 256)
+      if (dw_out == kDwTiles) {  // (bf16 only; the block's tile rows start at v0 / 256)
         w.tiled = 1;
         w.tile_pad = dw_tiles_pad(H);
         w.lddw = 0;
       }
+      if (dw_out == kDwNarrow) w.narrow = 1;  // dW: bf16 rows of pitch lddw
       if (use_queue) w.queue = queue;
       if (beside) {
         // the next block's recompute (G) and gather (X^T) follow the join
@@ -801,7 +831,10 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       } else {
         if constexpr (sizeof(T) == 2) {
           const int pw = prof_begin("dw_bf16_kernel", dw_flops(w), 0, stream);
-          void (*kern)(DwArgs) = tiled ? dw_bf16_kernel<false, true> : dw_bf16_kernel<false, false>;
+          static void (*const kd[3])(DwArgs) = {dw_bf16_kernel<false, kDwRows>,
+                                                dw_bf16_kernel<false, kDwTiles>,
+                                                dw_bf16_kernel<false, kDwNarrow>};
+          void (*kern)(DwArgs) = kd[dw_out];
           hipLaunchKernelGGL(kern, dim3(persistent_grid(w.tiles_m * w.tiles_n)),
                              dim3(kThreadsBf), 0, stream, w);
           prof_end(pw, stream);
@@ -1230,7 +1263,7 @@ namespace {
 
 int backward_plan_entry(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
                         size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
-                        size_t* workspace_bytes, bool tiles) {
+                        size_t* workspace_bytes, bool narrow) {
   const int es = esize_of(dtype);
   if (!es) return fail(MT_ERR_INVALID_ARGUMENT, "dtype %d is not MT_DTYPE_F32 or MT_DTYPE_BF16", dtype);
   if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0)
@@ -1238,9 +1271,9 @@ int backward_plan_entry(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dt
                 (long long)n_valid, (long long)H, (long long)V);
   if (!chunk_rows || !chunk_vocab || !workspace_bytes)
     return fail(MT_ERR_INVALID_ARGUMENT, "null output pointer");
-  if (tiles && dtype != MT_DTYPE_BF16)
-    return fail(MT_ERR_UNSUPPORTED, "tiled dW is bf16 only (dtype %d)", dtype);
-  const BwdPlan p = plan_backward(T, n_valid, H, V, es, budget_bytes, tiles);
+  if (narrow && dtype != MT_DTYPE_BF16)
+    return fail(MT_ERR_UNSUPPORTED, "the narrowing backward is bf16 only (dtype %d)", dtype);
+  const BwdPlan p = plan_backward(T, n_valid, H, V, es, budget_bytes, narrow);
   *chunk_rows = p.C;
   *chunk_vocab = p.Cv;
   *workspace_bytes = p.ws;
@@ -1258,9 +1291,9 @@ int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int 
                              workspace_bytes, false);
 }
 
-int mt_flce_backward_tiles_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
-                                size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
-                                size_t* workspace_bytes) {
+int mt_flce_backward_narrow_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
+                                 size_t budget_bytes, int64_t* chunk_rows, int64_t* chunk_vocab,
+                                 size_t* workspace_bytes) {
   return backward_plan_entry(T, n_valid, H, V, dtype, budget_bytes, chunk_rows, chunk_vocab,
                              workspace_bytes, true);
 }
@@ -1269,22 +1302,31 @@ int mt_flce_backward_tiles_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V
 
 namespace {
 
-// mt_flce_backward (row-major dW) and mt_flce_backward_tiles (tiled dW of
-// dw_tiles_bytes, bf16 only, lddw == 0, never accumulated into).
+// mt_flce_backward (row-major dW), mt_flce_backward_tiles (tiled dW of
+// dw_tiles_bytes, bf16 only, lddw == 0, never accumulated into) and
+// mt_flce_backward_narrow (bf16 rows of pitch H at the start of a buffer of
+// dw_tiles_bytes, one row block, never accumulated into).
 int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
                    int64_t ldw, int dtype, float softcap, const int32_t* row_index,
                    const int32_t* row_label, int64_t n_valid, const float* lse,
                    const float* grad_loss, int64_t grad_stride, void* dX, int64_t lddx, float* dW,
-                   int64_t lddw, int accumulate_dW, bool tiled, int64_t chunk_rows,
+                   int64_t lddw, int accumulate_dW, int dw_out, int64_t chunk_rows,
                    int64_t chunk_vocab, void* workspace, size_t workspace_bytes, mt_stream_t stream) {
   MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
   const int es = esize_of(dtype);
   if (n_valid < 0 || n_valid > T)
     return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
-  if (lddx < H || (!tiled && lddw < H))
+  if (lddx < H || (dw_out == kDwRows && lddw < H))
     return fail(MT_ERR_INVALID_ARGUMENT, "lddx=%lld / lddw=%lld must be >= H", (long long)lddx, (long long)lddw);
   if ((lddx * es) % 16 != 0 || (lddw * 4) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "dX / dW row pitches must be multiples of 16 bytes");
+  if (dw_out == kDwNarrow && H % 8 != 0)
+    return fail(MT_ERR_UNSUPPORTED, "the narrowing backward needs H a multiple of 8 (H=%lld)",
+                (long long)H);
+  if (dw_out == kDwNarrow && n_valid > 0 && chunk_rows < n_valid)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "the narrowing backward runs one row block: chunk_rows=%lld < n_valid=%lld",
+                (long long)chunk_rows, (long long)n_valid);
   if (grad_stride < 0) return fail(MT_ERR_INVALID_ARGUMENT, "grad_stride must be >= 0");
   if (!dW || (T > 0 && (!dX || !row_index)) ||
       (n_valid > 0 && (!row_label || !lse || !grad_loss)))
@@ -1292,6 +1334,8 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
   if ((reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(dW) |
        reinterpret_cast<uintptr_t>(workspace)) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "dX, dW and workspace must be 16-byte aligned");
+  const bool acc_in_buf = dw_out == kDwNarrow && cdiv(V, std::max<int64_t>(chunk_vocab, 1)) > 1 &&
+                          narrow_acc_in_buffer(V, H, chunk_rows);
   if (n_valid > 0) {
     if (chunk_rows <= 0 || chunk_rows % 256 != 0 || chunk_vocab <= 0 || chunk_vocab % 256 != 0)
       return fail(MT_ERR_INVALID_ARGUMENT,
@@ -1304,8 +1348,7 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
                   "chunk_rows=%lld x chunk_vocab=%lld: G block, X^T or the block's weight rows beyond "
                   "one buffer's reach (4 GiB, or MT_FLCE_MAX_BUFFER_BYTES)",
                   (long long)chunk_rows, (long long)chunk_vocab);
-    const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es,
-                                   tiled && acc_in_tiles(n_valid, chunk_rows, chunk_vocab, V, es));
+    const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es, acc_in_buf);
     if (workspace_bytes < need || !workspace)
       return fail(MT_ERR_WORKSPACE_TOO_SMALL, "backward workspace %zu bytes < required %zu",
                   workspace_bytes, need);
@@ -1318,8 +1361,12 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
     MT_TRY(check_launch("zero_rows_kernel"));
   }
   if (n_valid == 0) {
-    if (tiled) {
+    if (dw_out == kDwTiles) {
       MT_TRY(zero_tiles(dW, V, H, s));
+    } else if (dw_out == kDwNarrow) {  // V x H bf16 = V x H / 2 floats
+      hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
+                         s, dW, V, H / 2, H / 2);
+      MT_TRY(check_launch("zero_matrix_f32_kernel"));
     } else if (!accumulate_dW) {
       hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
                          s, dW, V, H, lddw);
@@ -1327,12 +1374,17 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
     }
     return MT_OK;
   }
-  if (dtype == MT_DTYPE_BF16)
+  if (dtype == MT_DTYPE_BF16) {
+    float* acc_ext = acc_in_buf ? reinterpret_cast<float*>(reinterpret_cast<char*>(dW) +
+                                                           narrow_acc_offset(V, H))
+                                : nullptr;
     return launch_backward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
-                                   grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, tiled,
-                                   chunk_rows, chunk_vocab, static_cast<char*>(workspace), s);
+                                   grad_loss, grad_stride, dX, lddx, dW,
+                                   dw_out == kDwNarrow ? H : lddw, accumulate_dW, dw_out, chunk_rows,
+                                   chunk_vocab, static_cast<char*>(workspace), s, acc_ext);
+  }
   return launch_backward<float>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
-                                grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, false,
+                                grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, kDwRows,
                                 chunk_rows, chunk_vocab, static_cast<char*>(workspace), s);
 }
 
@@ -1347,7 +1399,7 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
                      int64_t lddw, int accumulate_dW, int64_t chunk_rows, int64_t chunk_vocab,
                      void* workspace, size_t workspace_bytes, mt_stream_t stream) {
   return backward_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid, lse,
-                        grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, false, chunk_rows,
+                        grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, kDwRows, chunk_rows,
                         chunk_vocab, workspace, workspace_bytes, stream);
 }
 
@@ -1364,8 +1416,25 @@ int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H, i
     return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles %zu bytes < mt_flce_dw_tiles_bytes = %zu",
                 dw_tiles_bytes_, dw_tiles_bytes(V, H));
   return backward_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid, lse,
-                        grad_loss, grad_stride, dX, lddx, dW_tiles, 0, 0, true, chunk_rows,
+                        grad_loss, grad_stride, dX, lddx, dW_tiles, 0, 0, kDwTiles, chunk_rows,
                         chunk_vocab, workspace, workspace_bytes, stream);
+}
+
+int mt_flce_backward_narrow(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
+                            int64_t ldx, int64_t ldw, int dtype, float softcap,
+                            const int32_t* row_index, const int32_t* row_label, int64_t n_valid,
+                            const float* lse, const float* grad_loss, int64_t grad_stride,
+                            void* dX, int64_t lddx, void* dW_buf, size_t dw_buf_bytes,
+                            int64_t chunk_rows, int64_t chunk_vocab, void* workspace,
+                            size_t workspace_bytes, mt_stream_t stream) {
+  if (dtype != MT_DTYPE_BF16)
+    return fail(MT_ERR_UNSUPPORTED, "the narrowing backward is bf16 only (dtype %d)", dtype);
+  if (H > 0 && V > 0 && dw_buf_bytes < dw_tiles_bytes(V, H))
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW buffer %zu bytes < mt_flce_dw_tiles_bytes = %zu",
+                dw_buf_bytes, dw_tiles_bytes(V, H));
+  return backward_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid, lse,
+                        grad_loss, grad_stride, dX, lddx, static_cast<float*>(dW_buf), 0, 0,
+                        kDwNarrow, chunk_rows, chunk_vocab, workspace, workspace_bytes, stream);
 }
 
 int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,

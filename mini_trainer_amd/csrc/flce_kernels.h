@@ -550,7 +550,16 @@ struct DwArgs {
   // ((w 64 + fm 8 + fn) 64 + lane) 4 within it
   int32_t tiled = 0;
   int64_t tile_pad = 0;
+  // narrow (bf16, a dW every tile completes in one pass): dW is bf16 rows of
+  // pitch lddw elements, each tile narrowed in its epilogue (kDwNarrow)
+  int32_t narrow = 0;
 };
+
+// Where a bf16 dW kernel puts its tiles (template argument kOut): fp32 rows
+// of pitch lddw, fp32 tiles (DwArgs::tiled), or -- for a dW that every tile
+// completes in one pass (one row block, nothing added into) -- bf16 rows of
+// pitch lddw (elements) at dW, narrowed in the epilogue.
+constexpr int kDwRows = 0, kDwTiles = 1, kDwNarrow = 2;
 
 template <int NFN, int WC>
 __device__ __forceinline__ void dw_epilogue(const f32x4_t (&acc)[8][NFN], const DwArgs& a,

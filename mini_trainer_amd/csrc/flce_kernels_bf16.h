@@ -669,6 +669,15 @@ __device__ __forceinline__ uint32_t dw_tiled_off(const EpiCoordsBf& ec, int fm, 
   return ((((ec.wm * 2u + ec.wn) * 64u + (uint32_t)fm * 8u + (uint32_t)fn) * 64u) + ec.lane) * 16u;
 }
 
+// Zero starting values of a tile the compiler cannot see as constants (with
+// known-zero accumulators it restructured the K loop and spilled).
+__device__ __forceinline__ f32x4_t opaque_zero4() {
+  uint32_t z = 0;
+  asm volatile("" : "+v"(z));
+  const float f = __builtin_bit_cast(float, z);
+  return f32x4_t{f, f, f, f};
+}
+
 // Accumulators of tile (m0, h0) from dW (or zero), fragment row fm of the
 // wave (its fragments' 16 rows x 4 columns per lane).
 __device__ __forceinline__ void dw_load_row(f32x4_t (&accrow)[8], const DwArgs& a,
@@ -684,11 +693,19 @@ __device__ __forceinline__ void dw_load_row(f32x4_t (&accrow)[8], const DwArgs& 
   }
 }
 
-template <bool kTiled>
+template <int kOut>
 __device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& a,
                                             const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                             bool load) {
-  if constexpr (kTiled) {
+  if constexpr (kOut == kDwNarrow) {
+    const f32x4_t z = opaque_zero4();
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn) acc[fm][fn] = z;
+    return;
+  }
+  if constexpr (kOut == kDwTiles) {
     const rsrc_t r = dw_tiled_rsrc(a, m0, h0);
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm)
@@ -737,11 +754,70 @@ __device__ __forceinline__ void dw_store_row(const f32x4_t (&accrow)[8], const D
   }
 }
 
-template <bool kTiled>
+// kDwNarrow: one fragment row of the tile's final values as bf16 rows
+// (round to nearest even), through the epilogue's free ring slot as
+// dw_store_row does: the wave writes its 16 x 128 fp32 fragment row into LDS
+// (XOR-swizzled 16-byte chunks) and reads it back as two rows of 512
+// contiguous bytes per instruction, each lane narrowing its 4 columns into
+// one 8-byte store -- 256 contiguous bytes per row and instruction.  (Packing
+// straight from the accumulators made the compiler spill them.)  The
+// resource ends at the tile's last element; lanes past it (rows past cv,
+// columns past H) get an offset beyond that end.
+__device__ __forceinline__ void dw_narrow_row(const f32x4_t (&accrow)[8], const EpiCoordsBf& ec,
+                                              const rsrc_t& dst, uint32_t rows, uint32_t cols,
+                                              uint32_t ldo_b, int fm, char* R) {
+  const uint32_t i = ec.lane & 15u, q = ec.lane >> 4;
+  const uint32_t rr = ec.lane >> 5, c = ec.lane & 31u;
+#pragma unroll
+  for (int fn = 0; fn < 8; ++fn)
+    lds_write16(R, i * 512u + ((((uint32_t)fn * 4u + q) ^ i) & 31u) * 16u,
+                __builtin_bit_cast(u32x4_t, accrow[fn]));
+  const uint32_t col = ec.wn * 128u + 4u * c;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t lrow = 2u * (uint32_t)j + rr;
+    const uint32_t row = ec.wm * 128u + (uint32_t)fm * 16u + lrow;
+    const f32x4_t v = __builtin_bit_cast(f32x4_t, lds_read16(R, lrow * 512u + ((c ^ lrow) & 31u) * 16u));
+    u32x2_t o;
+    o[0] = pack_bf16x2(v[0], v[1]);
+    o[1] = pack_bf16x2(v[2], v[3]);
+    const uint32_t off = row < rows && col < cols ? row * ldo_b + col * 2u : kDwOut;
+    __builtin_amdgcn_raw_buffer_store_b64(o, dst, off, 0, 0);
+  }
+}
+
+// The bf16 rows of tile (m0, h0): resource and valid extent.
+struct DwNarrowTile {
+  rsrc_t r;
+  uint32_t rows, cols, ldo_b;
+};
+__device__ __forceinline__ DwNarrowTile dw_narrow_tile(const DwArgs& a, int32_t m0, int32_t h0) {
+  DwNarrowTile t;
+  t.rows = (uint32_t)min(256, a.cv - m0);
+  t.cols = (uint32_t)min(256, a.H - h0);
+  t.ldo_b = (uint32_t)(a.lddw * 2);
+  t.r = make_rsrc(reinterpret_cast<char*>(a.dW) + (int64_t)(a.v0 + m0) * a.lddw * 2 + (int64_t)h0 * 2,
+                  (t.rows - 1u) * t.ldo_b + t.cols * 2u);
+  return t;
+}
+
+template <int kOut>
 __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const DwArgs& a,
                                              const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                              char* scratch) {
-  if constexpr (kTiled) {
+  if constexpr (kOut == kDwNarrow) {
+    const DwNarrowTile t = dw_narrow_tile(a, m0, h0);
+    char* R = scratch + (ec.wm * 2u + ec.wn) * 8192u;
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+      dw_narrow_row(acc[fm], ec, t.r, t.rows, t.cols, t.ldo_b, fm, R);
+      sched_fence();
+    }
+    lgkm_wait0();
+    __builtin_amdgcn_s_barrier();
+    return;
+  }
+  if constexpr (kOut == kDwTiles) {
     const rsrc_t r = dw_tiled_rsrc(a, m0, h0);
 #pragma unroll
     for (int fm = 0; fm < 8; ++fm) {
@@ -774,11 +850,28 @@ __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const D
 // counter to drop to the loads issued after their own, which it can count
 // (at most 63 outstanding); interleaved, they also waited for stores and
 // loads of later rows (phase -0.5% at config 3 on one box).
-template <bool kTiled>
+template <int kOut>
 __device__ __forceinline__ void dw_store_then_load(f32x4_t (&acc)[8][8], const DwArgs& a,
                                                    const EpiCoordsBf& ec, int32_t m0, int32_t h0,
                                                    char* scratch, int32_t nm0, int32_t nh0) {
-  if constexpr (kTiled) {
+  if constexpr (kOut == kDwNarrow) {
+    (void)nm0;
+    (void)nh0;
+    const DwNarrowTile t = dw_narrow_tile(a, m0, h0);
+    char* R = scratch + (ec.wm * 2u + ec.wn) * 8192u;
+#pragma unroll
+    for (int fm = 0; fm < 8; ++fm) {
+      dw_narrow_row(acc[fm], ec, t.r, t.rows, t.cols, t.ldo_b, fm, R);
+      const f32x4_t z = opaque_zero4();
+#pragma unroll
+      for (int fn = 0; fn < 8; ++fn) acc[fm][fn] = z;
+      sched_fence();
+    }
+    lgkm_wait0();
+    __builtin_amdgcn_s_barrier();
+    return;
+  }
+  if constexpr (kOut == kDwTiles) {
     const rsrc_t r = dw_tiled_rsrc(a, m0, h0), nr = dw_tiled_rsrc(a, nm0, nh0);
     const bool load = a.accumulate != 0;
 #pragma unroll
@@ -893,7 +986,7 @@ struct DwQueue {
 // B = X^T rows of the block (256 hidden rows).  kQueue: persistent over the
 // work queue above (grid = one workgroup per CU, K >= 2 stages); otherwise
 // one workgroup per tile or a static persistent schedule (TileSeq).
-template <bool kQueue, bool kTiled>
+template <bool kQueue, int kOut>
 __device__ __forceinline__ void dw_bf16_body(char* lds, const DwArgs& a, uint32_t b, uint32_t nb) {
   const uint32_t total = (uint32_t)(a.tiles_m * a.tiles_n);
   const TileSeq seq(total, b, nb);
@@ -941,10 +1034,10 @@ __device__ __forceinline__ void dw_bf16_body(char* lds, const DwArgs& a, uint32_
         if (next) {
           uint32_t ntm, ntn;
           grouped_tile(logical(k + 1), a.tiles_m, a.tiles_n, 4, ntm, ntn);
-          dw_store_then_load<kTiled>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch,
+          dw_store_then_load<kOut>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch,
                                      (int32_t)ntm * 256, (int32_t)ntn * 256);
         } else {
-          dw_store_acc<kTiled>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch);
+          dw_store_acc<kOut>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, scratch);
         }
       },
       // init: the first tile's starting values
@@ -953,14 +1046,14 @@ __device__ __forceinline__ void dw_bf16_body(char* lds, const DwArgs& a, uint32_
         uint32_t tm, tn;
         grouped_tile(logical(k), a.tiles_m, a.tiles_n, 4, tm, tn);
         if constexpr (kQueue) q.ask();
-        dw_load_acc<kTiled>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0);
+        dw_load_acc<kOut>(acc, a, ec, (int32_t)tm * 256, (int32_t)tn * 256, a.accumulate != 0);
       });
 }
 
-template <bool kQueue, bool kTiled>
+template <bool kQueue, int kOut>
 MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
-  dw_bf16_body<kQueue, kTiled>(lds, a, blockIdx.x, gridDim.x);
+  dw_bf16_body<kQueue, kOut>(lds, a, blockIdx.x, gridDim.x);
 }
 
 // dX and dW of one block in one launch: workgroups [0, dx_blocks) are dX's
@@ -968,13 +1061,13 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
 // CUs dX leaves free, then the others; the work queue's XCD shares follow
 // the global workgroup index, which keeps the round-robin XCD placement).
 // Both only read G and the X^T block.
-template <int kMode, bool kQueue, bool kTiled>
+template <int kMode, bool kQueue, int kOut>
 MT_GEMM_BF16_KERNEL void dx_dw_bf16_kernel(DxArgs x, DwArgs w, uint32_t dx_blocks) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
   if (blockIdx.x < dx_blocks)
     dx_bf16_body<kMode>(lds, x, blockIdx.x, dx_blocks);
   else
-    dw_bf16_body<kQueue, kTiled>(lds, w, blockIdx.x - dx_blocks, gridDim.x - dx_blocks);
+    dw_bf16_body<kQueue, kOut>(lds, w, blockIdx.x - dx_blocks, gridDim.x - dx_blocks);
 }
 
 // Tiled fp32 dW (dw_bf16_kernel<*, true>) times *scale, narrowed to bf16 rows

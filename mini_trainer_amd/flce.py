@@ -106,15 +106,17 @@ def prepare_targets(target: torch.Tensor, vocab_size: int, ignore_index: int = -
 
 
 def backward_plan(T: int, n_valid: int, H: int, V: int, dtype: torch.dtype,
-                  budget_bytes: Optional[int] = None, tiles: bool = False) -> Tuple[int, int, int]:
+                  budget_bytes: Optional[int] = None, narrow: bool = False) -> Tuple[int, int, int]:
     """(chunk_rows, chunk_vocab, workspace_bytes) of the backward blocking;
-    tiles: the plan of mt_flce_backward_tiles (a fresh tiled dW, which may
-    hold dX's accumulator), else of mt_flce_backward."""
+    narrow: the plan of a bf16 backward whose weight gradient is wanted in
+    bf16 and added into nothing (mt_flce_backward_narrow_plan: chunk_rows >=
+    n_valid means one row block through mt_flce_backward_narrow), else of
+    mt_flce_backward."""
     lib = load()
     if budget_bytes is None:
         budget_bytes = int(os.environ.get(BACKWARD_BUDGET_ENV, "0"))
     c, cv, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_size_t()
-    fn = "mt_flce_backward_tiles_plan" if tiles else "mt_flce_backward_plan"
+    fn = "mt_flce_backward_narrow_plan" if narrow else "mt_flce_backward_plan"
     check(getattr(lib, fn)(T, n_valid, H, V, _dtype_code(dtype), budget_bytes, ctypes.byref(c),
                            ctypes.byref(cv), ctypes.byref(ws)), fn)
     return c.value, cv.value, ws.value
@@ -266,16 +268,14 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         dev = X.device
         g, gstride = _grad_vector(grad_loss, T)
         dX = torch.empty((T, H), dtype=X.dtype, device=dev)
-        tiles = acc is None and dt == MT_DTYPE_BF16
-        C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype, tiles=tiles)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        if tiles:
-            # dW as 256 x 256 fp32 tiles, narrowed into bf16 in its own allocation
-            dW = _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX,
-                                 C, Cv, ws)
-            del ws
-            grad_w = _tiles_in_dtype(dW, (V, H), torch.ones(1, device=dev)) if need_w else None
+        if acc is None and dt == MT_DTYPE_BF16:
+            # dW in bf16 inside an allocation of the fp32 tiles' size
+            grad_w = _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride,
+                                           softcap, dX)
+            grad_w = grad_w if need_w else None
         else:
+            C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
             if acc is not None:
                 dW, accumulate = acc, 1
             else:
@@ -359,12 +359,9 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         else:
             # a per-token gradient: the unit-gradient results cannot be
             # rescaled; recompute into the same buffers
-            C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype, tiles=True)
-            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-            _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX, C, Cv,
-                            ws, dW)
-            del ws
-            dW_out = _tiles_in_dtype(dW, (V, H), torch.ones(1, device=dev)) if need_w else None
+            dW_out = _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride,
+                                           softcap, dX, dW)
+            dW_out = dW_out if need_w else None
         grad_x = dX.view(hshape) if need_x else None
         grad_w = dW_out if need_w else None
         return (grad_x, grad_w) + (None,) * 7
@@ -398,6 +395,37 @@ def _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap
                                      dWt.numel() * 4, C, Cv, _p(ws), ws.numel(),
                                      _stream(X.device)), "mt_flce_backward_tiles")
     return dWt
+
+
+def _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX,
+                          dWt: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The bf16 backward into dX and a weight gradient in bf16 (nothing
+    added into), as the contiguous [V, H] at the start of dWt (an fp32
+    allocation of mt_flce_dw_tiles_bytes; a new one if None): one row block
+    through mt_flce_backward_narrow when its plan says so, else the tiles and
+    the narrowing pass."""
+    T, H = X.shape
+    V = W.shape[0]
+    C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype, narrow=True)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=X.device)
+    if C < n:
+        dWt = _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX, C,
+                              Cv, ws, dWt)
+        del ws
+        return _tiles_in_dtype(dWt, (V, H), torch.ones(1, device=X.device))
+    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    if dWt is None:
+        dWt = torch.empty(tb // 4, dtype=torch.float32, device=X.device)
+    check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0),
+                                      MT_DTYPE_BF16, softcap, _p(row_index), _p(row_label), n,
+                                      _p(lse), _p(g), gstride, _p(dX), dX.stride(0), _p(dWt),
+                                      dWt.numel() * 4, C, Cv, _p(ws), ws.numel(),
+                                      _stream(X.device)), "mt_flce_backward_narrow")
+    del ws
+    out = torch.empty(0, dtype=torch.bfloat16, device=dWt.device)
+    # storage offsets count elements: one fp32 element is two 16-bit ones
+    out.set_(dWt.untyped_storage(), 2 * dWt.storage_offset(), (V, H), (H, 1))
+    return out
 
 
 def _tiles_in_dtype(dWt: torch.Tensor, shape: Tuple[int, int],

@@ -187,24 +187,43 @@ def test_backward_plan_fits_budget(key):
 
 
 @pytest.mark.parametrize("key", [2, 3, 4, 5])
-def test_backward_tiles_plan_fits_budget(key):
-    """The tiled entry's plan: within the budget; with one row block and
-    several vocabulary blocks of at least C entries its workspace holds no dX
-    accumulator (it lives in the tiles), otherwise it is mt_flce_backward's.
-    Config 5 (H = 8192, a 210 MB budget) takes one row block per minibatch."""
+def test_backward_narrow_plan_fits_budget(key):
+    """The narrowing plan: within the budget; one row block (C >= n) keeps
+    dX's accumulator in the dW buffer (the workspace holds G, X^T and the
+    counters only); more row blocks have mt_flce_backward's workspace.
+    Config 5 (H = 8192, a 210 MB budget) takes one row block per minibatch;
+    fp32 has no narrowing path."""
     cfg = synth.CONFIGS[key]
     n = int((synth.make_batch(cfg, 0, with_tensors=False)["target"] != -100).sum())
-    C, Cv, ws = backward_plan(cfg.T, n, cfg.H, cfg.V, cfg.dtype, tiles=True)
+    C, Cv, ws = backward_plan(cfg.T, n, cfg.H, cfg.V, cfg.dtype, narrow=True)
     assert C % 256 == 0 and Cv % 256 == 0 and ws <= 0.05 * cfg.T * cfg.V * 2
     al = lambda b: (b + 255) // 256 * 256  # noqa: E731
-    in_tiles = n <= C <= Cv < cfg.V
-    expect = (al(C * Cv * 2) + (al(C * cfg.H * 4) if Cv < cfg.V and not in_tiles else 0) +
+    one = C >= n
+    expect = (al(C * Cv * 2) + (al(C * cfg.H * 4) if Cv < cfg.V and not one else 0) +
               al(cfg.H * C * 2) + al(8 * 4))
     assert ws == expect
     if key == 5:
-        assert in_tiles and C >= n
+        assert one
     with pytest.raises(_lib.FlceError):
-        backward_plan(cfg.T, n, cfg.H, cfg.V, torch.float32, tiles=True)
+        backward_plan(cfg.T, n, cfg.H, cfg.V, torch.float32, narrow=True)
+
+
+def test_backward_narrow_host_checks():
+    """mt_flce_backward_narrow refuses fp32, H not a multiple of 8, a dW buffer
+    smaller than mt_flce_dw_tiles_bytes and more than one row block, before
+    touching any pointer."""
+    lib = _lib.load()
+    T, H, V, n = 1000, 128, 5000, 700
+    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    p = 16  # a dummy, aligned, never-dereferenced address
+
+    def call(dtype=1, h=H, ld=H, dwb=tb, C=768, Cv=1024):
+        return lib.mt_flce_backward_narrow(p, p, T, h, V, ld, ld, dtype, 0.0, p, p, n, p, p, 0, p,
+                                           ld, p, dwb, C, Cv, p, 1 << 40, None)
+    assert call(dtype=0) == 3
+    assert call(h=100, ld=104) == 3
+    assert call(dwb=tb - 1) == 1
+    assert call(C=512) == 1
 
 
 def test_backward_plan_budget_override_and_degenerate():

@@ -116,10 +116,11 @@ def test_general_backward_guards(gpu, case, monkeypatch, softcap):
     assert bool(torch.isfinite(dX[:, :H].float()).all()) and bool(torch.isfinite(dW[:, :H]).all())
 
 
-def test_backward_tiles_accumulator_in_tiles_guards(gpu, case):
-    """mt_flce_backward_tiles on one row block and several vocabulary blocks
-    (dX's fp32 accumulator in the first block's dW tiles), with exactly the
-    workspace mt_flce_backward_tiles_plan reports for that blocking."""
+def test_backward_narrow_guards(gpu, case):
+    """mt_flce_backward_narrow: one row block and several vocabulary blocks
+    (dX's fp32 accumulator in the dW buffer's second half, dW written as bf16
+    rows in its first), with exactly the workspace mt_flce_backward_narrow_plan
+    reports for that blocking."""
     X, W, y, ri, rl, n = case
     lib = _lib.load()
     s = _stream(gpu)
@@ -132,7 +133,7 @@ def test_backward_tiles_accumulator_in_tiles_guards(gpu, case):
     C, Cv = 512, 512  # n < 512 rows; 1300 vocabulary entries in 3 blocks
     assert n <= C < V
     budget = C * Cv * 2 + H * C * 2 + 4096
-    pc, pcv, bws = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, tiles=True)
+    pc, pcv, bws = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, narrow=True)
     assert (pc, pcv) == (C, Cv)
     assert bws < C * Cv * 2 + C * H * 4  # no accumulator in the workspace
     grad = torch.rand(T, device=gpu)
@@ -140,14 +141,15 @@ def test_backward_tiles_accumulator_in_tiles_guards(gpu, case):
     tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
     gdw = Guarded(gpu, tb)
     gws = Guarded(gpu, bws)
-    _lib.check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
-                                          _p(ri), _p(rl), n, _p(lse), _p(grad), 1, gdx.ptr, H + 8,
-                                          gdw.ptr, tb, C, Cv, gws.ptr, bws, s), "backward_tiles")
+    _lib.check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                           _p(ri), _p(rl), n, _p(lse), _p(grad), 1, gdx.ptr,
+                                           H + 8, gdw.ptr, tb, C, Cv, gws.ptr, bws, s),
+               "backward_narrow")
     torch.cuda.synchronize()
     assert gdx.intact() and gdw.intact() and gws.intact()
     assert pad_intact(dX, H)
     assert bool(torch.isfinite(dX[:, :H].float()).all())
-    assert bool(torch.isfinite(gdw.view(torch.float32, (tb // 4,))).all())
+    assert bool(torch.isfinite(gdw.view(torch.bfloat16, (tb // 2,))[: V * H].float()).all())
 
 
 def test_fused_and_rescale_guards(gpu, case):

@@ -123,9 +123,9 @@ def test_multi_block_backward(gpu, monkeypatch):
 
 
 def test_one_row_block_vocabulary_blocks_reference_chain(gpu, monkeypatch):
-    """The general path without dw_accumulator (mt_flce_backward_tiles) under a
-    budget that fits one row block and several vocabulary blocks: dX's fp32
-    accumulator lives in the tiles of the first vocabulary block (run last).
+    """The general path without dw_accumulator under a budget that fits one
+    row block and several vocabulary blocks (mt_flce_backward_narrow: dW
+    written in bf16 by its GEMM, dX's fp32 accumulator in the dW buffer).
     Loss, dX and the bf16 weight gradient against the torch path."""
     from mini_trainer_amd.flce import FUSED_ENV, backward_plan
 
@@ -133,8 +133,8 @@ def test_one_row_block_vocabulary_blocks_reference_chain(gpu, monkeypatch):
     X, W, y = make_case(T, H, V, torch.bfloat16, seed=17, mask_frac=0.2)
     n = int((y != -100).sum())
     budget = 1024 * 4096 * 2 + H * 1024 * 2 + (1 << 16)
-    C, Cv, _ = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, tiles=True)
-    assert n <= C <= Cv < V, (n, C, Cv)
+    C, Cv, _ = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, narrow=True)
+    assert n <= C and Cv < V, (n, C, Cv)
     monkeypatch.setenv(BACKWARD_BUDGET_ENV, str(budget))
     monkeypatch.setenv(FUSED_ENV, "0")
     grad = torch.rand(T, generator=torch.Generator().manual_seed(3))

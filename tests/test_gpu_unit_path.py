@@ -265,9 +265,8 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     two row blocks and a vocabulary split whose first block runs dW beside dX
     over the work queue; under a 3-CU grid cap dW runs after dX, three
     persistent workgroups carrying tiles; one block over the whole
-    vocabulary; one row block and five vocabulary blocks (run last to first,
-    the tiled entry's dX accumulator in the first block's tiles, with only the
-    workspace that layout needs).  V = 65600, H = 1056 (tails in both)."""
+    vocabulary; one row block and five vocabulary blocks.  V = 65600, H = 1056
+    (tails in both)."""
     print(f"case backward tiles C={C} Cv={Cv} cap={cap}", flush=True)
     if cap:
         monkeypatch.setenv("MT_FLCE_GRID_CAP", cap)
@@ -295,16 +294,32 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
     dX1 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
     dW1 = torch.full((tb // 4,), float("nan"), device=gpu)
-    acc_in_tiles = n <= C <= Cv < V
-    if acc_in_tiles:  # the tiled entry needs no accumulator in its workspace
-        wsb = al(C * Cv * 2) + al(H * C * 2) + al(32)
-        ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
     _lib.check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                           _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX1), H,
                                           _p(dW1), tb, C, Cv, _p(ws), wsb, s), "backward_tiles")
     torch.cuda.synchronize()
     assert torch.equal(dX0, dX1)
     assert torch.equal(_untile(dW1, V, H), dW0)
+    if C < n:
+        return
+    # one row block: mt_flce_backward_narrow (dW narrowed in its epilogue,
+    # dX's accumulator in the buffer's second half, no accumulator in the
+    # workspace) against the tiles narrowed by mt_flce_narrow_tiles
+    one = torch.ones(1, device=gpu)
+    want = torch.empty(V, H, dtype=torch.bfloat16, device=gpu)
+    _lib.check(lib.mt_flce_narrow_tiles(_p(one), _p(dW1), tb, V, H, _p(want), H,
+                                        _lib.MT_DTYPE_BF16, s), "narrow_tiles")
+    nwsb = al(C * Cv * 2) + al(H * C * 2) + al(32)
+    nws = torch.empty(nwsb, dtype=torch.uint8, device=gpu)
+    dX2 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    dW2 = torch.full((tb // 4,), float("nan"), device=gpu)
+    _lib.check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                           _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX2), H,
+                                           _p(dW2), tb, C, Cv, _p(nws), nwsb, s),
+               "backward_narrow")
+    torch.cuda.synchronize()
+    assert torch.equal(dX2, dX0)
+    assert torch.equal(dW2.view(torch.bfloat16)[: V * H].view(V, H), want)
 
 
 def test_fused_tiles_all_masked_and_narrow_phases(gpu):
