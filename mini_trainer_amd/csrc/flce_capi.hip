@@ -433,13 +433,13 @@ size_t forward_ws(const FwdPlan& p, int64_t n_valid) {
 }
 
 // --------------------------------------------------------------- backward
-// acc_outside: dX's accumulator lives outside the workspace (the narrowing
-// entry's dW buffer, narrow_acc).
-size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es, bool acc_outside = false) {
+// outside: dX's accumulator and X^T live outside the workspace (in the
+// narrowing entry's dW buffer, narrow_scratch_fits).
+size_t backward_ws(int64_t C, int64_t Cv, int64_t H, int64_t V, int es, bool outside = false) {
   if (C == 0) return 0;
   size_t g = align_up((size_t)C * Cv * es);
-  size_t acc = Cv < V && !acc_outside ? align_up((size_t)C * H * sizeof(float)) : 0;
-  size_t xt = align_up((size_t)H * C * es);
+  size_t acc = Cv < V && !outside ? align_up((size_t)C * H * sizeof(float)) : 0;
+  size_t xt = outside ? 0 : align_up((size_t)H * C * es);
   size_t queue = es == 2 ? align_up(kQueueWords * sizeof(uint32_t)) : 0;  // dW work queue
   return g + acc + xt + queue;
 }
@@ -540,13 +540,17 @@ struct BwdPlan {
 size_t tiled_acc_bytes(int64_t C, int64_t H) {
   return (size_t)cdiv(C, 256) * cdiv(H, 256) * 65536 * sizeof(float);
 }
-// The narrowing entry's dW buffer (mt_flce_dw_tiles_bytes) holds the bf16
-// gradient in its first V H 2 bytes; dX's tiled accumulator goes after them
-// when it fits (else into the workspace, row-major).
+// The narrowing entry's dW buffer (mt_flce_dw_tiles_bytes, the size of the
+// fp32 gradient) holds the bf16 gradient in its first V H 2 bytes; dX's
+// tiled accumulator and the block's X^T go after them when both fit (else
+// into the workspace, the accumulator row-major).
 size_t dw_tiles_bytes(int64_t V, int64_t H);
 inline size_t narrow_acc_offset(int64_t V, int64_t H) { return align_up((size_t)V * H * 2); }
-inline bool narrow_acc_in_buffer(int64_t V, int64_t H, int64_t C) {
-  return dw_tiles_bytes(V, H) >= narrow_acc_offset(V, H) + tiled_acc_bytes(C, H);
+inline size_t narrow_xt_offset(int64_t V, int64_t H, int64_t C) {
+  return narrow_acc_offset(V, H) + align_up(tiled_acc_bytes(C, H));
+}
+inline bool narrow_scratch_fits(int64_t V, int64_t H, int64_t C) {
+  return dw_tiles_bytes(V, H) >= narrow_xt_offset(V, H, C) + align_up((size_t)H * C * 2);
 }
 
 // narrow: the plan of a bf16 backward whose dW is wanted in bf16 without an
@@ -565,7 +569,7 @@ BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t
   smallest.C = 256;
   smallest.Cv = 256;
   smallest.ws = backward_ws(256, 256, H, V, es,
-                            narrow && N <= 256 && narrow_acc_in_buffer(V, H, 256));
+                            narrow && N <= 256 && narrow_scratch_fits(V, H, 256));
   const int64_t max_nt = std::min<int64_t>(cdiv(N, 256), 128);
   const int64_t max_nv = std::min<int64_t>(cdiv(V, 256), 128);
   const double narrow_pass = (double)V * H * 6 / kBw + 10 * kLaunch;
@@ -574,7 +578,7 @@ BwdPlan plan_backward(int64_t T, int64_t N, int64_t H, int64_t V, int es, size_t
     const bool one = narrow && nt == 1;
     for (int64_t nv = 1; nv <= max_nv; ++nv) {
       const int64_t Cv = round_up(cdiv(V, nv), 256);
-      const size_t ws = backward_ws(C, Cv, H, V, es, one && narrow_acc_in_buffer(V, H, C));
+      const size_t ws = backward_ws(C, Cv, H, V, es, one && narrow_scratch_fits(V, H, C));
       // G and X^T are read through 32-bit buffer offsets
       // G, X^T and the block's weight rows (bf16) within one buffer's reach
       const uint64_t lim = buffer_limit();
@@ -683,19 +687,25 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
                     float softcap, const int32_t* row_index, const int32_t* row_label,
                     int64_t N, const float* lse, const float* grad, int64_t gstride, void* dX,
                     int64_t lddx, float* dW, int64_t lddw, int accumulate, int dw_out, int64_t C,
-                    int64_t Cv, char* ws, hipStream_t stream, float* acc_ext = nullptr) {
+                    int64_t Cv, char* ws, hipStream_t stream, char* scratch_ext = nullptr) {
   constexpr int es = sizeof(T);
   const Geometry geo = geometry(es);
   const int64_t nv = cdiv(V, Cv);
-  // acc_ext (the narrowing entry, one row block): dX's accumulator as tiles
-  // outside the workspace
+  // scratch_ext (the narrowing entry, one row block): dX's accumulator (as
+  // tiles) and X^T in the dW buffer past the bf16 gradient
   char* G = ws;
   float* accbuf = nv > 1 ? reinterpret_cast<float*>(ws + align_up((size_t)C * Cv * es)) : nullptr;
-  const bool acc_tiles = acc_ext != nullptr && nv > 1;
-  if (acc_tiles) accbuf = acc_ext;
   char* XcT = ws + align_up((size_t)C * Cv * es) +
-              (nv > 1 && !acc_tiles ? align_up((size_t)C * H * sizeof(float)) : 0);
-  uint32_t* queue = reinterpret_cast<uint32_t*>(XcT + align_up((size_t)H * C * es));
+              (nv > 1 ? align_up((size_t)C * H * sizeof(float)) : 0);
+  const bool acc_tiles = scratch_ext != nullptr && nv > 1;
+  if (scratch_ext) {
+    accbuf = reinterpret_cast<float*>(scratch_ext + narrow_acc_offset(V, H));
+    XcT = scratch_ext + narrow_xt_offset(V, H, C);
+  }
+  char* const ws_end = ws + align_up((size_t)C * Cv * es) +
+                       (nv > 1 && !scratch_ext ? align_up((size_t)C * H * sizeof(float)) : 0) +
+                       (scratch_ext ? 0 : align_up((size_t)H * C * es));
+  uint32_t* queue = reinterpret_cast<uint32_t*>(ws_end);
   const int64_t ldg_b = Cv * es, ldxt_b = C * es;
 
   for (int64_t c0 = 0; c0 < N; c0 += C) {
@@ -1334,8 +1344,7 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
   if ((reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(dW) |
        reinterpret_cast<uintptr_t>(workspace)) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "dX, dW and workspace must be 16-byte aligned");
-  const bool acc_in_buf = dw_out == kDwNarrow && cdiv(V, std::max<int64_t>(chunk_vocab, 1)) > 1 &&
-                          narrow_acc_in_buffer(V, H, chunk_rows);
+  const bool outside = dw_out == kDwNarrow && narrow_scratch_fits(V, H, chunk_rows);
   if (n_valid > 0) {
     if (chunk_rows <= 0 || chunk_rows % 256 != 0 || chunk_vocab <= 0 || chunk_vocab % 256 != 0)
       return fail(MT_ERR_INVALID_ARGUMENT,
@@ -1348,7 +1357,7 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
                   "chunk_rows=%lld x chunk_vocab=%lld: G block, X^T or the block's weight rows beyond "
                   "one buffer's reach (4 GiB, or MT_FLCE_MAX_BUFFER_BYTES)",
                   (long long)chunk_rows, (long long)chunk_vocab);
-    const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es, acc_in_buf);
+    const size_t need = backward_ws(chunk_rows, chunk_vocab, H, V, es, outside);
     if (workspace_bytes < need || !workspace)
       return fail(MT_ERR_WORKSPACE_TOO_SMALL, "backward workspace %zu bytes < required %zu",
                   workspace_bytes, need);
@@ -1375,13 +1384,11 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
     return MT_OK;
   }
   if (dtype == MT_DTYPE_BF16) {
-    float* acc_ext = acc_in_buf ? reinterpret_cast<float*>(reinterpret_cast<char*>(dW) +
-                                                           narrow_acc_offset(V, H))
-                                : nullptr;
+    char* scratch_ext = outside ? reinterpret_cast<char*>(dW) : nullptr;
     return launch_backward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                    grad_loss, grad_stride, dX, lddx, dW,
                                    dw_out == kDwNarrow ? H : lddw, accumulate_dW, dw_out, chunk_rows,
-                                   chunk_vocab, static_cast<char*>(workspace), s, acc_ext);
+                                   chunk_vocab, static_cast<char*>(workspace), s, scratch_ext);
   }
   return launch_backward<float>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                 grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, kDwRows,

@@ -189,18 +189,21 @@ def test_backward_plan_fits_budget(key):
 @pytest.mark.parametrize("key", [2, 3, 4, 5])
 def test_backward_narrow_plan_fits_budget(key):
     """The narrowing plan: within the budget; one row block (C >= n) keeps
-    dX's accumulator in the dW buffer (the workspace holds G, X^T and the
-    counters only); more row blocks have mt_flce_backward's workspace.
-    Config 5 (H = 8192, a 210 MB budget) takes one row block per minibatch;
-    fp32 has no narrowing path."""
+    dX's accumulator and X^T in the dW buffer (the workspace holds the G
+    block and the counters only); more row blocks have mt_flce_backward's
+    workspace.  Config 5 (H = 8192, a 210 MB budget) takes one row block per
+    minibatch; fp32 has no narrowing path."""
     cfg = synth.CONFIGS[key]
     n = int((synth.make_batch(cfg, 0, with_tensors=False)["target"] != -100).sum())
     C, Cv, ws = backward_plan(cfg.T, n, cfg.H, cfg.V, cfg.dtype, narrow=True)
     assert C % 256 == 0 and Cv % 256 == 0 and ws <= 0.05 * cfg.T * cfg.V * 2
     al = lambda b: (b + 255) // 256 * 256  # noqa: E731
     one = C >= n
-    expect = (al(C * Cv * 2) + (al(C * cfg.H * 4) if Cv < cfg.V and not one else 0) +
-              al(cfg.H * C * 2) + al(8 * 4))
+    if one:
+        expect = al(C * Cv * 2) + al(8 * 4)
+    else:
+        expect = (al(C * Cv * 2) + (al(C * cfg.H * 4) if Cv < cfg.V else 0) +
+                  al(cfg.H * C * 2) + al(8 * 4))
     assert ws == expect
     if key == 5:
         assert one

@@ -118,9 +118,9 @@ def test_general_backward_guards(gpu, case, monkeypatch, softcap):
 
 def test_backward_narrow_guards(gpu, case):
     """mt_flce_backward_narrow: one row block and several vocabulary blocks
-    (dX's fp32 accumulator in the dW buffer's second half, dW written as bf16
-    rows in its first), with exactly the workspace mt_flce_backward_narrow_plan
-    reports for that blocking."""
+    (dX's fp32 accumulator and X^T in the dW buffer's second half, dW written
+    as bf16 rows in its first), with exactly the workspace
+    mt_flce_backward_narrow_plan reports for that blocking."""
     X, W, y, ri, rl, n = case
     lib = _lib.load()
     s = _stream(gpu)
@@ -135,7 +135,7 @@ def test_backward_narrow_guards(gpu, case):
     budget = C * Cv * 2 + H * C * 2 + 4096
     pc, pcv, bws = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, narrow=True)
     assert (pc, pcv) == (C, Cv)
-    assert bws < C * Cv * 2 + C * H * 4  # no accumulator in the workspace
+    assert bws < C * Cv * 2 + H * C * 2  # no accumulator or X^T in the workspace
     grad = torch.rand(T, device=gpu)
     gdx, dX = matrix(gpu, T, H, H + 8, torch.bfloat16)
     tb = int(lib.mt_flce_dw_tiles_bytes(V, H))

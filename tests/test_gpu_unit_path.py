@@ -303,13 +303,13 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     if C < n:
         return
     # one row block: mt_flce_backward_narrow (dW narrowed in its epilogue,
-    # dX's accumulator in the buffer's second half, no accumulator in the
-    # workspace) against the tiles narrowed by mt_flce_narrow_tiles
+    # dX's accumulator and X^T in the buffer's second half, only the G block
+    # in the workspace) against the tiles narrowed by mt_flce_narrow_tiles
     one = torch.ones(1, device=gpu)
     want = torch.empty(V, H, dtype=torch.bfloat16, device=gpu)
     _lib.check(lib.mt_flce_narrow_tiles(_p(one), _p(dW1), tb, V, H, _p(want), H,
                                         _lib.MT_DTYPE_BF16, s), "narrow_tiles")
-    nwsb = al(C * Cv * 2) + al(H * C * 2) + al(32)
+    nwsb = al(C * Cv * 2) + al(32)  # the G block and the counters
     nws = torch.empty(nwsb, dtype=torch.uint8, device=gpu)
     dX2 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
     dW2 = torch.full((tb // 4,), float("nan"), device=gpu)
