@@ -119,6 +119,28 @@ int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H,
                     mt_stream_t stream);
 
 /*
+ * mt_flce_forward (bf16, softcap off) that also keeps, for the backward,
+ * the exponentials exp(logit) (rounded to bf16) of vocabulary columns
+ * [0, keep_cols) of every valid row: keep receives them as rows of keep_cols
+ * entries (round_up(n_valid, 256) rows, keep_bytes >= that times keep_cols
+ * times 2), keep_cols a multiple of 256 below V.  *guard (a device int32) is
+ * reset and then raised if some row's largest logit lies outside the range
+ * in which those exponentials hold their terms ([-48, 48]).  Handing keep
+ * (as the G block of the backward's workspace, keep_cols = chunk_vocab) and
+ * guard to mt_flce_backward_narrow spares that block's recomputation: the
+ * forward already computes every logit once (the Liger forward reached from
+ * none_reduction_losses.py:16-23 keeps its chunk's logits for the same
+ * reason).  Same loss and lse as mt_flce_forward, bit for bit.
+ */
+int mt_flce_forward_keep(const void* X, const void* W, int64_t T, int64_t H,
+                         int64_t V, int64_t ldx, int64_t ldw, int dtype,
+                         float softcap, const int32_t* row_index,
+                         const int32_t* row_label, int64_t n_valid,
+                         float* loss, float* lse, void* workspace,
+                         size_t workspace_bytes, void* keep, int64_t keep_cols,
+                         size_t keep_bytes, int32_t* guard, mt_stream_t stream);
+
+/*
  * Bytes one bf16 operand buffer may span (the kernels address X, the
  * weight's vocabulary blocks, G, the fused logits chunk and X^T with 32-bit
  * offsets): 4 GiB - 1, lowered by the test hook MT_FLCE_MAX_BUFFER_BYTES.
@@ -274,6 +296,12 @@ int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H,
  * (round to nearest even) -- and the rest of the buffer is scratch (dX's
  * fp32 accumulator, when it fits).  Bit for bit what mt_flce_backward_tiles
  * and mt_flce_narrow_tiles with a unit scale give for the same blocking.
+ *   kept_guard   NULL, or (softcap off, chunk_vocab < V) the guard word of an
+ *                mt_flce_forward_keep call that kept keep_cols = chunk_vocab
+ *                columns in this workspace's first bytes (the G block): the
+ *                first vocabulary block then takes its G from those
+ *                exponentials instead of recomputing its logits, unless the
+ *                guard was raised.
  * Replaces the same reference interface as mt_flce_backward (the lm_head
  * backward's dW = dS^T X, none_reduction_losses.py:35 through autograd).
  */
@@ -286,7 +314,7 @@ int mt_flce_backward_narrow(const void* X, const void* W, int64_t T, int64_t H,
                             void* dW_buf, size_t dw_buf_bytes,
                             int64_t chunk_rows, int64_t chunk_vocab,
                             void* workspace, size_t workspace_bytes,
-                            mt_stream_t stream);
+                            const int32_t* kept_guard, mt_stream_t stream);
 
 /*
  * Bytes of the tiled fp32 weight gradient that mt_flce_fused_tiles and

@@ -33,6 +33,10 @@ SIGNATURES = {
     "mt_flce_forward": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                                 c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                 c_void_p, c_size_t, c_void_p]),
+    "mt_flce_forward_keep": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                     c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
+                                     c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_int64,
+                                     c_size_t, c_void_p, c_void_p]),
     "mt_flce_noalloc_scratch_bytes": (c_size_t, []),
     "mt_flce_max_buffer_bytes": (ctypes.c_uint64, []),
     "mt_flce_forward_noalloc": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
@@ -58,9 +62,10 @@ SIGNATURES = {
                                        c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                                        c_size_t, c_int64, c_int64, c_void_p, c_size_t, c_void_p]),
     "mt_flce_backward_narrow": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
-                                       c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
-                                       c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
-                                       c_size_t, c_int64, c_int64, c_void_p, c_size_t, c_void_p]),
+                                        c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
+                                        c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                        c_size_t, c_int64, c_int64, c_void_p, c_size_t, c_void_p,
+                                        c_void_p]),
     "mt_flce_dw_tiles_bytes": (c_size_t, [c_int64, c_int64]),
     "mt_flce_fused_tiles": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                     c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,

@@ -604,7 +604,8 @@ template <typename T>
 int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V, int64_t ldx,
                    int64_t ldw, float softcap, const int32_t* row_index, const int32_t* row_label,
                    int64_t n_valid, float* loss, float* lse, const FwdPlan& p, char* ws,
-                   hipStream_t stream) {
+                   hipStream_t stream, char* keep = nullptr, int64_t keep_cols = 0,
+                   int32_t* guard = nullptr) {
   constexpr int es = sizeof(T);
   FwdArgs a;
   a.X = static_cast<const char*>(X);
@@ -638,20 +639,33 @@ int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t 
          {fwd_bf16_kernel<false, kStoreNone, true, false>, fwd_bf16_kernel<false, kStoreNone, true, true>}},
         {{fwd_bf16_kernel<true, kStoreNone, false, false>, fwd_bf16_kernel<true, kStoreNone, false, true>},
          {fwd_bf16_kernel<true, kStoreNone, true, false>, fwd_bf16_kernel<true, kStoreNone, true, true>}}};
+    // keep (softcap off): vocabulary columns [0, keep_cols) first, storing
+    // their exponentials exp(z) as bf16 rows of keep_cols entries (the next
+    // backward's first G block) and resetting *guard, which the finalize
+    // raises for a row whose largest logit leaves [kGuardLo, kGuardHi]
+    static void (*const kerns_keep[2])(FwdArgs) = {fwd_bf16_kernel<false, kStoreExp, false, false>,
+                                                   fwd_bf16_kernel<false, kStoreExp, false, true>};
     const int64_t vb = vocab_block_rows(V, ldw);
-    for (int64_t v0 = 0; v0 < V; v0 += vb) {
-      const int64_t vn = std::min(vb, V - v0);
+    for (int64_t v0 = 0; v0 < V;) {
+      const bool kb = keep && v0 == 0;
+      const int64_t vn = kb ? keep_cols : std::min(vb, V - v0);
       a.W = static_cast<const char*>(W) + v0 * ldw * es;
       a.V = (int32_t)vn;
       a.vcol0 = (int32_t)v0;
       a.w_range = range_of(vn, ldw * es);
       a.vt_total = (int32_t)cdiv(vn, geometry(es).tile_n);
-      void (*kern)(FwdArgs) = kerns[softcap > 0.f][vn % 256 != 0][ktail];
-      const int pf = prof_begin("fwd_bf16_kernel", 2.0 * H * (double)vn * n_valid, 0, stream);
+      a.S = kb ? keep : nullptr;
+      a.lds_b = kb ? keep_cols * 2 : 0;
+      a.s_range = kb ? range_of(p.tiles_m * 256, keep_cols * 2) : 0;
+      a.guard_reset = kb ? guard : nullptr;
+      void (*kern)(FwdArgs) = kb ? kerns_keep[ktail] : kerns[softcap > 0.f][vn % 256 != 0][ktail];
+      const int pf = prof_begin(kb ? "fwd_bf16_kernel<keep>" : "fwd_bf16_kernel",
+                                2.0 * H * (double)vn * n_valid, 0, stream);
       hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * a.vt_total)), dim3(kThreadsBf), 0,
                          stream, a);
       prof_end(pf, stream);
       MT_TRY(check_launch("fwd_bf16_kernel"));
+      v0 += vn;
     }
   } else {
     void (*kern)(FwdArgs) = ktail ? fwd_kernel<T, true> : fwd_kernel<T, false>;
@@ -659,7 +673,7 @@ int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t 
     MT_TRY(check_launch("fwd_kernel"));
   }
   hipLaunchKernelGGL(fwd_finalize_kernel, dim3((uint32_t)cdiv(n_valid, 4)), dim3(256), 0, stream,
-                     a.part, a.xy, a.N, a.splits, row_index, loss, lse, static_cast<int32_t*>(nullptr));
+                     a.part, a.xy, a.N, a.splits, row_index, loss, lse, guard);
   return check_launch("fwd_finalize_kernel");
 }
 
@@ -687,7 +701,8 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
                     float softcap, const int32_t* row_index, const int32_t* row_label,
                     int64_t N, const float* lse, const float* grad, int64_t gstride, void* dX,
                     int64_t lddx, float* dW, int64_t lddw, int accumulate, int dw_out, int64_t C,
-                    int64_t Cv, char* ws, hipStream_t stream, char* scratch_ext = nullptr) {
+                    int64_t Cv, char* ws, hipStream_t stream, char* scratch_ext = nullptr,
+                    const int32_t* kept_guard = nullptr) {
   constexpr int es = sizeof(T);
   const Geometry geo = geometry(es);
   const int64_t nv = cdiv(V, Cv);
@@ -744,6 +759,17 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       r.tiles_m = (int32_t)cdiv(cn, geo.tile_m);
       r.tiles_n = (int32_t)cdiv(cv, geo.tile_n);
       if constexpr (sizeof(T) == 2) r.zero_words = queue;
+      // kept_guard (one row block, softcap off): the G block of vocabulary
+      // block 0 holds the forward's exponentials; they become G in place,
+      // unless the guard was raised, in which case the block is recomputed
+      const bool kept = kept_guard != nullptr && v0 == 0 && c0 == 0;
+      if (kept) {
+        hipLaunchKernelGGL(exp_to_grad_kernel, dim3((uint32_t)round_up(cn, 256)), dim3(256), 0, stream,
+                           G, ldg_b, (int32_t)cv, (int32_t)cn, lse + c0, grad, gstride,
+                           row_index + c0, row_label + c0, kept_guard);
+        MT_TRY(check_launch("exp_to_grad_kernel"));
+        r.run_if = kept_guard;
+      }
       if constexpr (sizeof(T) == 2) {
         static void (*const kerns[2][2][2])(RecompArgs) = {
             {{recompute_bf16_kernel<false, false, false>, recompute_bf16_kernel<false, false, true>},
@@ -1169,6 +1195,56 @@ int mt_flce_forward(const void* X, const void* W, int64_t T, int64_t H, int64_t 
                                lse, p, static_cast<char*>(workspace), s);
 }
 
+int mt_flce_forward_keep(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
+                         int64_t ldx, int64_t ldw, int dtype, float softcap,
+                         const int32_t* row_index, const int32_t* row_label, int64_t n_valid,
+                         float* loss, float* lse, void* workspace, size_t workspace_bytes,
+                         void* keep, int64_t keep_cols, size_t keep_bytes, int32_t* guard,
+                         mt_stream_t stream) {
+  if (dtype != MT_DTYPE_BF16)
+    return fail(MT_ERR_UNSUPPORTED, "mt_flce_forward_keep is bf16 only (dtype %d)", dtype);
+  if (softcap > 0.f)
+    return fail(MT_ERR_UNSUPPORTED, "mt_flce_forward_keep keeps exponentials without softcap");
+  if (keep_cols <= 0 || keep_cols % 256 != 0 || keep_cols >= V)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "keep_cols=%lld must be a positive multiple of 256 below V=%lld",
+                (long long)keep_cols, (long long)V);
+  if (n_valid > 0 &&
+      (!keep || !guard || keep_bytes < (size_t)round_up(n_valid, 256) * keep_cols * 2 ||
+       reinterpret_cast<uintptr_t>(keep) % 16 != 0))
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "keep needs %zu bytes (round_up(n_valid, 256) x keep_cols bf16, 16-byte aligned) "
+                "and a guard word", (size_t)round_up(n_valid, 256) * keep_cols * 2);
+  if ((uint64_t)keep_cols * ldw * 2 > buffer_limit() ||
+      (uint64_t)round_up(n_valid, 256) * keep_cols * 2 > buffer_limit())
+    return fail(MT_ERR_UNSUPPORTED, "keep_cols=%lld: kept block beyond one buffer's reach",
+                (long long)keep_cols);
+  MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
+  if (n_valid < 0 || n_valid > T)
+    return fail(MT_ERR_INVALID_ARGUMENT, "n_valid=%lld outside [0, T=%lld]", (long long)n_valid, (long long)T);
+  if (T == 0) return MT_OK;
+  if (!row_index || !loss || (n_valid > 0 && (!row_label || !lse)))
+    return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const FwdPlan p = plan_forward(n_valid, V, 2);
+  const size_t need = n_valid > 0 ? forward_ws(p, n_valid) : 0;
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(MT_ERR_WORKSPACE_TOO_SMALL, "forward workspace %zu bytes < required %zu",
+                workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (T - n_valid > 0) {
+    const int64_t n0 = T - n_valid;
+    hipLaunchKernelGGL(zero_scatter_f32_kernel, dim3((uint32_t)std::min<int64_t>(cdiv(n0, 256), 4096)),
+                       dim3(256), 0, s, loss, row_index + n_valid, n0);
+    MT_TRY(check_launch("zero_scatter_f32_kernel"));
+  }
+  if (n_valid == 0) return MT_OK;
+  return launch_forward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid,
+                                loss, lse, p, static_cast<char*>(workspace), s,
+                                static_cast<char*>(keep), keep_cols, guard);
+}
+
 }  // extern "C"
 
 // ------------------------------------------------- forward without allocation
@@ -1321,7 +1397,8 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
                    const int32_t* row_label, int64_t n_valid, const float* lse,
                    const float* grad_loss, int64_t grad_stride, void* dX, int64_t lddx, float* dW,
                    int64_t lddw, int accumulate_dW, int dw_out, int64_t chunk_rows,
-                   int64_t chunk_vocab, void* workspace, size_t workspace_bytes, mt_stream_t stream) {
+                   int64_t chunk_vocab, void* workspace, size_t workspace_bytes, mt_stream_t stream,
+                   const int32_t* kept_guard = nullptr) {
   MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
   const int es = esize_of(dtype);
   if (n_valid < 0 || n_valid > T)
@@ -1338,6 +1415,10 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
                 "the narrowing backward runs one row block: chunk_rows=%lld < n_valid=%lld",
                 (long long)chunk_rows, (long long)n_valid);
   if (grad_stride < 0) return fail(MT_ERR_INVALID_ARGUMENT, "grad_stride must be >= 0");
+  if (kept_guard && (softcap > 0.f || chunk_vocab >= V))
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "a kept first block needs softcap off and chunk_vocab < V (chunk_vocab=%lld)",
+                (long long)chunk_vocab);
   if (!dW || (T > 0 && (!dX || !row_index)) ||
       (n_valid > 0 && (!row_label || !lse || !grad_loss)))
     return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
@@ -1388,7 +1469,8 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
     return launch_backward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                    grad_loss, grad_stride, dX, lddx, dW,
                                    dw_out == kDwNarrow ? H : lddw, accumulate_dW, dw_out, chunk_rows,
-                                   chunk_vocab, static_cast<char*>(workspace), s, scratch_ext);
+                                   chunk_vocab, static_cast<char*>(workspace), s, scratch_ext,
+                                   kept_guard);
   }
   return launch_backward<float>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                 grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, kDwRows,
@@ -1433,7 +1515,8 @@ int mt_flce_backward_narrow(const void* X, const void* W, int64_t T, int64_t H, 
                             const float* lse, const float* grad_loss, int64_t grad_stride,
                             void* dX, int64_t lddx, void* dW_buf, size_t dw_buf_bytes,
                             int64_t chunk_rows, int64_t chunk_vocab, void* workspace,
-                            size_t workspace_bytes, mt_stream_t stream) {
+                            size_t workspace_bytes, const int32_t* kept_guard,
+                            mt_stream_t stream) {
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "the narrowing backward is bf16 only (dtype %d)", dtype);
   if (H > 0 && V > 0 && dw_buf_bytes < dw_tiles_bytes(V, H))
@@ -1441,7 +1524,8 @@ int mt_flce_backward_narrow(const void* X, const void* W, int64_t T, int64_t H, 
                 dw_buf_bytes, dw_tiles_bytes(V, H));
   return backward_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid, lse,
                         grad_loss, grad_stride, dX, lddx, static_cast<float*>(dW_buf), 0, 0,
-                        kDwNarrow, chunk_rows, chunk_vocab, workspace, workspace_bytes, stream);
+                        kDwNarrow, chunk_rows, chunk_vocab, workspace, workspace_bytes, stream,
+                        kept_guard);
 }
 
 int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,

@@ -322,7 +322,51 @@ struct RecompArgs {
   int64_t ldg_b;
   int32_t tiles_m, tiles_n;
   uint32_t* zero_words = nullptr;  // cleared by the launch (dW's work queue, read after it)
+  // non-null (bf16): the launch computes nothing unless *run_if != 0 (the
+  // first vocabulary block, whose G a forward kept as exponentials, when
+  // those left their range); zero_words is cleared either way
+  const int32_t* run_if = nullptr;
 };
+
+// The first vocabulary block's G from the exponentials E = exp(z) that
+// mt_flce_forward_keep left in the G block (columns [0, cols), softcap off):
+// G = g (E exp(-lse) - onehot), in place, one workgroup per row of the block
+// (rows >= cn become 0).  Nothing when *skip_if != 0: some row's largest
+// logit left the range in which E holds its terms, and the block is
+// recomputed instead (recompute_bf16_kernel with run_if = the same word).
+// HBM-bound: one 16-byte read and one 16-byte write per 8 entries.
+__global__ __launch_bounds__(256) void exp_to_grad_kernel(char* G, int64_t ldg_b, int32_t cols,
+                                                          int32_t cn, const float* lse,
+                                                          const float* grad, int64_t gstride,
+                                                          const int32_t* row_index,
+                                                          const int32_t* row_label,
+                                                          const int32_t* skip_if) {
+  if (*skip_if != 0) return;
+  const int32_t row = (int32_t)blockIdx.x;
+  const bool rv = row < cn;
+  float s = 0.f, g = 0.f;
+  int32_t y = -1;
+  if (rv) {
+    g = grad[(int64_t)row_index[row] * gstride];
+    s = g * fast_exp2(-lse[row] * kLog2e);
+    y = row_label[row];
+  }
+  char* p = G + (int64_t)row * ldg_b;
+  for (int32_t c = (int32_t)threadIdx.x * 8; c < cols; c += 256 * 8) {
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(p + (int64_t)c * 2);
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float e0 = __builtin_bit_cast(float, v[j] << 16);
+      const float e1 = __builtin_bit_cast(float, v[j] & 0xffff0000u);
+      const int32_t c0 = c + 2 * j;
+      const float g0 = fmaf(s, e0, c0 == y ? -g : 0.f);
+      const float g1 = fmaf(s, e1, c0 + 1 == y ? -g : 0.f);
+      o[j] = rv ? pack_bf16x2(g0, g1) : 0u;
+    }
+    *reinterpret_cast<u32x4_t*>(p + (int64_t)c * 2) = o;
+  }
+}
 
 template <typename T>
 __device__ __forceinline__ void store4(char* p, const float (&o)[4]);

@@ -443,6 +443,7 @@ MT_GEMM_BF16_KERNEL void recompute_bf16_kernel(RecompArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
   if (a.zero_words && blockIdx.x == 0 && threadIdx.x < (uint32_t)kQueueWords)
     a.zero_words[threadIdx.x] = 0u;
+  if (a.run_if && *a.run_if == 0) return;
   const TileSeq seq((uint32_t)(a.tiles_m * a.tiles_n));
   const EpiCoordsBf ec0;
   const int KT = (a.H + kBKBf - 1) / kBKBf;

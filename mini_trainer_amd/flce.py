@@ -163,9 +163,12 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
 
     general     forward keeps lse (mt_flce_forward); the backward recomputes
                 the logits for whatever upstream gradient arrives
-                (mt_flce_backward; bf16 without dw_accumulator:
-                mt_flce_backward_tiles, dW as 256 x 256 fp32 tiles narrowed
-                by mt_flce_narrow_tiles).
+                (mt_flce_backward; bf16 without dw_accumulator: one row
+                block through mt_flce_backward_narrow, dW written in bf16 by
+                its GEMM -- the forward then also keeps the first vocabulary
+                block's exponentials for it, mt_flce_forward_keep, softcap
+                off -- else mt_flce_backward_tiles, dW as 256 x 256 fp32
+                tiles narrowed by mt_flce_narrow_tiles).
     fused       grad_scale promised the upstream gradient at the forward and
                 the planner expects the fused path to pay (bf16,
                 mt_flce_fused_plan): the forward also forms dX and dW for it
@@ -183,9 +186,9 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
                 for every token (stride 0, what sum() / mean() and train.py's
                 scaling give; mt_flce_scale_grads for dX and
                 mt_flce_narrow_tiles for dW read it on the device), and
-                otherwise recomputes with the saved lse (mt_flce_backward into
-                the tiles' allocation as a row-major fp32 [V, H]), exact for
-                any per-token gradient.
+                otherwise recomputes with the saved lse (the general path's
+                bf16 backward into the tiles' allocation), exact for any
+                per-token gradient.
     """
 
     @staticmethod
@@ -241,9 +244,25 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
             return loss.view(hidden.shape[:-1])
         ws_bytes = lib.mt_flce_forward_workspace_bytes(T, n, H, V, dt)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
-                                  float(softcap), _p(row_index), _p(row_label), n, _p(loss),
-                                  _p(lse), _p(ws), ws_bytes, _stream(dev)), "mt_flce_forward")
+        ctx.keep = None
+        plan = None
+        if dt == MT_DTYPE_BF16 and allow_unit and float(softcap) == 0.0 and n > 0:
+            plan = backward_plan(T, n, H, V, X.dtype, narrow=True)
+        if plan is not None and plan[0] >= n and plan[1] < V:
+            # one row block in the backward: this forward keeps the first
+            # vocabulary block's exponentials in that backward's G block
+            C, Cv, bws_bytes = plan
+            bws = torch.empty(bws_bytes, dtype=torch.uint8, device=dev)
+            guard = torch.empty(1, dtype=torch.int32, device=dev)
+            check(lib.mt_flce_forward_keep(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
+                                           0.0, _p(row_index), _p(row_label), n, _p(loss),
+                                           _p(lse), _p(ws), ws_bytes, _p(bws), Cv, bws_bytes,
+                                           _p(guard), _stream(dev)), "mt_flce_forward_keep")
+            ctx.keep = (C, Cv, bws, guard)
+        else:
+            check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
+                                      float(softcap), _p(row_index), _p(row_label), n, _p(loss),
+                                      _p(lse), _p(ws), ws_bytes, _stream(dev)), "mt_flce_forward")
         del ws
         ctx.save_for_backward(X, W, row_index, row_label, lse)
         ctx.meta = (n, float(softcap), hidden.shape, dt)
@@ -269,9 +288,11 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         g, gstride = _grad_vector(grad_loss, T)
         dX = torch.empty((T, H), dtype=X.dtype, device=dev)
         if acc is None and dt == MT_DTYPE_BF16:
-            # dW in bf16 inside an allocation of the fp32 tiles' size
+            # dW in bf16 inside an allocation of the fp32 tiles' size; the
+            # first backward takes the exponentials its forward kept
+            keep, ctx.keep = getattr(ctx, "keep", None), None
             grad_w = _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride,
-                                           softcap, dX)
+                                           softcap, dX, keep=keep)
             grad_w = grad_w if need_w else None
         else:
             C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
@@ -398,16 +419,22 @@ def _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap
 
 
 def _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX,
-                          dWt: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          dWt: Optional[torch.Tensor] = None, keep=None) -> torch.Tensor:
     """The bf16 backward into dX and a weight gradient in bf16 (nothing
     added into), as the contiguous [V, H] at the start of dWt (an fp32
     allocation of mt_flce_dw_tiles_bytes; a new one if None): one row block
     through mt_flce_backward_narrow when its plan says so, else the tiles and
-    the narrowing pass."""
+    the narrowing pass.  keep = (C, Cv, workspace, guard) of a forward that
+    kept the first vocabulary block's exponentials in that workspace
+    (mt_flce_forward_keep): its plan and workspace are used."""
     T, H = X.shape
     V = W.shape[0]
-    C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype, narrow=True)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=X.device)
+    guard = None
+    if keep is not None:
+        C, Cv, ws, guard = keep
+    else:
+        C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype, narrow=True)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=X.device)
     if C < n:
         dWt = _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX, C,
                               Cv, ws, dWt)
@@ -419,7 +446,7 @@ def _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride, s
     check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0),
                                       MT_DTYPE_BF16, softcap, _p(row_index), _p(row_label), n,
                                       _p(lse), _p(g), gstride, _p(dX), dX.stride(0), _p(dWt),
-                                      dWt.numel() * 4, C, Cv, _p(ws), ws.numel(),
+                                      dWt.numel() * 4, C, Cv, _p(ws), ws.numel(), _p(guard),
                                       _stream(X.device)), "mt_flce_backward_narrow")
     del ws
     out = torch.empty(0, dtype=torch.bfloat16, device=dWt.device)

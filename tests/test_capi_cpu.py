@@ -211,6 +211,25 @@ def test_backward_narrow_plan_fits_budget(key):
         backward_plan(cfg.T, n, cfg.H, cfg.V, torch.float32, narrow=True)
 
 
+def test_forward_keep_host_checks():
+    """mt_flce_forward_keep refuses fp32, a softcap, keep_cols not a multiple
+    of 256 or not below V, and a keep buffer below round_up(n_valid, 256) x
+    keep_cols bf16, before touching any pointer."""
+    lib = _lib.load()
+    T, H, V, n = 1000, 128, 5000, 700
+    p = 16
+
+    def call(dtype=1, cap=0.0, K=512, kb=768 * 512 * 2, guard=16):
+        return lib.mt_flce_forward_keep(p, p, T, H, V, H, H, dtype, cap, p, p, n, p, p, p,
+                                        1 << 30, p, K, kb, guard, None)
+    assert call(dtype=0) == 3
+    assert call(cap=5.0) == 3
+    assert call(K=500) == 1
+    assert call(K=5120) == 1
+    assert call(kb=768 * 512 * 2 - 2) == 1
+    assert call(guard=None) == 1
+
+
 def test_backward_narrow_host_checks():
     """mt_flce_backward_narrow refuses fp32, H not a multiple of 8, a dW buffer
     smaller than mt_flce_dw_tiles_bytes and more than one row block, before
@@ -222,7 +241,7 @@ def test_backward_narrow_host_checks():
 
     def call(dtype=1, h=H, ld=H, dwb=tb, C=768, Cv=1024):
         return lib.mt_flce_backward_narrow(p, p, T, h, V, ld, ld, dtype, 0.0, p, p, n, p, p, 0, p,
-                                           ld, p, dwb, C, Cv, p, 1 << 40, None)
+                                           ld, p, dwb, C, Cv, p, 1 << 40, None, None)
     assert call(dtype=0) == 3
     assert call(h=100, ld=104) == 3
     assert call(dwb=tb - 1) == 1

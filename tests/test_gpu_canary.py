@@ -143,7 +143,7 @@ def test_backward_narrow_guards(gpu, case):
     gws = Guarded(gpu, bws)
     _lib.check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                            _p(ri), _p(rl), n, _p(lse), _p(grad), 1, gdx.ptr,
-                                           H + 8, gdw.ptr, tb, C, Cv, gws.ptr, bws, s),
+                                           H + 8, gdw.ptr, tb, C, Cv, gws.ptr, bws, None, s),
                "backward_narrow")
     torch.cuda.synchronize()
     assert gdx.intact() and gdw.intact() and gws.intact()

@@ -147,6 +147,72 @@ def test_one_row_block_vocabulary_blocks_reference_chain(gpu, monkeypatch):
     check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(), grad=grad)
 
 
+def _keep_case_budget():
+    # one 1024-row block and 512-entry vocabulary blocks for T = 900, V = 2600
+    return 1024 * 512 * 2 + 4096
+
+
+def test_general_forward_keeps_first_block(gpu, monkeypatch):
+    """General path, one row block, softcap off: the forward keeps the first
+    vocabulary block's exponentials (mt_flce_forward_keep) and the narrowing
+    backward turns them into G instead of recomputing that block (the last
+    block a 40-column tail).  Loss, dX and the bf16 weight gradient against
+    the torch path; the forward launch with the kept block is on record."""
+    from mini_trainer_amd.flce import FUSED_ENV, backward_plan, profile_enable, profile_report
+
+    T, H, V = 900, 64, 2600
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=23, mask_frac=0.0, w_std=0.1)
+    n = T
+    C, Cv, _ = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=_keep_case_budget(),
+                             narrow=True)
+    assert (C, Cv) == (1024, 512)
+    monkeypatch.setenv(BACKWARD_BUDGET_ENV, str(_keep_case_budget()))
+    monkeypatch.setenv(FUSED_ENV, "0")
+    grad = torch.rand(T, generator=torch.Generator().manual_seed(4))
+    Xd = X.to(gpu).requires_grad_(True)
+    Wd = W.to(gpu).requires_grad_(True)
+    profile_enable(True)
+    try:
+        loss = fused_linear_cross_entropy(Xd, Wd, y.to(gpu))
+        loss.backward(grad.to(gpu))
+        torch.cuda.synchronize()
+    finally:
+        profile_enable(False)
+    rep = profile_report()
+    assert any("fwd_bf16_kernel<keep>" in k for k in rep), list(rep)
+    check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(), grad=grad)
+
+
+@pytest.mark.parametrize("shift", [56.0, -56.0])
+def test_general_kept_block_out_of_range_recomputes(gpu, monkeypatch, shift):
+    """The kept exponentials hold their terms while every row's largest logit
+    lies in [-48, 48]; here the first 256 rows' logits all move by `shift`, so
+    the guard is raised and the first vocabulary block is recomputed.  Logits
+    are exact multiples of 1/4 below 64 in magnitude (X in {-1, 0, 1}, W in
+    quarters), so every path rounds them the same way."""
+    from mini_trainer_amd.flce import FUSED_ENV
+
+    monkeypatch.setenv(BACKWARD_BUDGET_ENV, str(_keep_case_budget()))
+    monkeypatch.setenv(FUSED_ENV, "0")
+    g = torch.Generator().manual_seed(47)
+    T, H, V = 900, 64, 2600
+    X = torch.zeros(T, H)
+    W = torch.zeros(V, H)
+    X[:, 1:16] = torch.randint(-1, 2, (T, 15), generator=g).float()
+    W[:, 1:16] = torch.randint(-1, 2, (V, 15), generator=g).float() / 4
+    X[:256, 0] = shift
+    W[:, 0] = 1.0
+    X, W = X.to(torch.bfloat16), W.to(torch.bfloat16)
+    y = torch.randint(0, V, (T,), generator=g)
+    grad = torch.full((T,), 1.0 / T)
+    Xd = X.to(gpu).requires_grad_(True)
+    Wd = W.to(gpu).requires_grad_(True)
+    loss = fused_linear_cross_entropy(Xd, Wd, y.to(gpu))
+    loss.backward(grad.to(gpu))
+    torch.cuda.synchronize()
+    check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(), grad=grad)
+
+
 def test_accumulate_into_fp32_dw(gpu):
     X, W, y = make_case(300, 128, 700, torch.bfloat16, seed=9)
     X2, _, y2 = make_case(200, 128, 700, torch.bfloat16, seed=10)

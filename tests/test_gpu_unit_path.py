@@ -315,11 +315,52 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     dW2 = torch.full((tb // 4,), float("nan"), device=gpu)
     _lib.check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                            _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX2), H,
-                                           _p(dW2), tb, C, Cv, _p(nws), nwsb, s),
+                                           _p(dW2), tb, C, Cv, _p(nws), nwsb, None, s),
                "backward_narrow")
     torch.cuda.synchronize()
     assert torch.equal(dX2, dX0)
     assert torch.equal(dW2.view(torch.bfloat16)[: V * H].view(V, H), want)
+
+
+@pytest.mark.parametrize("shift", [0.0, 56.0])
+def test_forward_keep_matches_forward(gpu, shift):
+    """mt_flce_forward_keep against mt_flce_forward: loss and lse the same
+    bits; the kept block holds exp of the bf16 logits of vocabulary columns
+    [0, 512) for every valid row (within bf16 rounding of exp); the guard is 0
+    while every row's largest logit lies in [-48, 48] and 1 when the first
+    rows' logits are shifted by 56 (X column of 56 against a weight column of
+    ones)."""
+    print(f"case forward_keep shift={shift}", flush=True)
+    lib = _lib.load()
+    T, H, V, K = 600, 192, 1500, 512
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=71)
+    if shift:
+        X[:100, 0] = shift
+        W[:, 0] = 1.0
+    X, W, y = X.to(gpu), W.to(gpu), y.to(gpu)
+    ri, rl, n = prepare_targets(y, V)
+    s = _stream(gpu)
+    fwb = int(lib.mt_flce_forward_workspace_bytes(T, n, H, V, _lib.MT_DTYPE_BF16))
+    fws = torch.empty(fwb, dtype=torch.uint8, device=gpu)
+    loss0, lse0 = torch.empty(T, device=gpu), torch.empty(n, device=gpu)
+    _lib.check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0, _p(ri),
+                                   _p(rl), n, _p(loss0), _p(lse0), _p(fws), fwb, s), "forward")
+    rows = (n + 255) // 256 * 256
+    keep = torch.full((rows, K), float("nan"), dtype=torch.bfloat16, device=gpu)
+    guard = torch.full((1,), 7, dtype=torch.int32, device=gpu)
+    loss1, lse1 = torch.empty(T, device=gpu), torch.empty(n, device=gpu)
+    _lib.check(lib.mt_flce_forward_keep(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                        _p(ri), _p(rl), n, _p(loss1), _p(lse1), _p(fws), fwb,
+                                        _p(keep), K, keep.numel() * 2, _p(guard), s),
+               "forward_keep")
+    torch.cuda.synchronize()
+    assert torch.equal(loss0, loss1) and torch.equal(lse0, lse1)
+    assert int(guard.item()) == (1 if shift else 0)
+    if not shift:
+        z = (X[ri[:n].long()] @ W[:K].T).float()  # bf16 logits, as F.linear gives them
+        want = torch.exp(z)
+        got = keep[:n].float()
+        assert ((got - want).abs() <= want * 2e-2 + 1e-30).all()
 
 
 def test_fused_tiles_all_masked_and_narrow_phases(gpu):
