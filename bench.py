@@ -285,11 +285,14 @@ def roofline_of(report: dict, peak_flops: float, steps: int) -> tuple:
             kernels[name] = {"launches_per_step": n / steps, "ms_per_launch": ms / n,
                              "ms_per_step": ms / steps, "achieved_TFLOPs": ach / 1e12,
                              "frac": ach / peak_flops, "bound": "mfma"}
-        else:
+        elif r["bytes"] > 0:
             ach = r["bytes"] / (ms / 1e3)
             kernels[name] = {"launches_per_step": n / steps, "ms_per_launch": ms / n,
                              "ms_per_step": ms / steps, "achieved_GBs": ach / 1e9,
                              "frac": ach / PEAK_HBM, "bound": "hbm"}
+        else:  # a launch that works only if a device flag says so (time only)
+            kernels[name] = {"launches_per_step": n / steps, "ms_per_launch": ms / n,
+                             "ms_per_step": ms / steps, "bound": None}
     if "dx_dw_phase" in report:
         unit = "dx_dw_phase"
         # dX and dW share the chip inside the phase: each one's span runs

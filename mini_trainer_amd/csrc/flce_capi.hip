@@ -776,7 +776,10 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
              {recompute_bf16_kernel<false, true, false>, recompute_bf16_kernel<false, true, true>}},
             {{recompute_bf16_kernel<true, false, false>, recompute_bf16_kernel<true, false, true>},
              {recompute_bf16_kernel<true, true, false>, recompute_bf16_kernel<true, true, true>}}};
-        const int pr = prof_begin("recompute_bf16_kernel", 2.0 * H * (double)cn * cv, 0, stream);
+        // (a kept block's launch recomputes only if the guard was raised:
+        // recorded apart, without flops, so as not to inflate the rate)
+        const int pr = kept ? prof_begin("recompute_bf16_kernel<if_guard>", 0.0, 0, stream)
+                            : prof_begin("recompute_bf16_kernel", 2.0 * H * (double)cn * cv, 0, stream);
         hipLaunchKernelGGL(kerns[softcap > 0.f][cv % 256 != 0][H % kBKBf != 0],
                            dim3(persistent_grid(r.tiles_m * r.tiles_n)),
                            dim3(kThreadsBf), 0, stream, r);
