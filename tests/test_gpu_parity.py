@@ -183,6 +183,32 @@ def test_general_forward_keeps_first_block(gpu, monkeypatch):
     check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(), grad=grad)
 
 
+def test_general_kept_block_second_backward(gpu, monkeypatch):
+    """A second backward through the same loss (retain_graph) cannot reuse the
+    kept exponentials (the first backward turned them into G): it recomputes
+    every block and gives the same gradients within the tolerance, and the
+    first backward's gradients match the torch path."""
+    from mini_trainer_amd.flce import FUSED_ENV
+
+    monkeypatch.setenv(BACKWARD_BUDGET_ENV, str(_keep_case_budget()))
+    monkeypatch.setenv(FUSED_ENV, "0")
+    T, H, V = 900, 64, 2600
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=29, mask_frac=0.0, w_std=0.1)
+    grad = torch.rand(T, generator=torch.Generator().manual_seed(5))
+    Xd = X.to(gpu).requires_grad_(True)
+    Wd = W.to(gpu).requires_grad_(True)
+    loss = fused_linear_cross_entropy(Xd, Wd, y.to(gpu))
+    loss.backward(grad.to(gpu), retain_graph=True)
+    gx1, gw1 = Xd.grad.clone(), Wd.grad.clone()
+    Xd.grad = None
+    Wd.grad = None
+    loss.backward(grad.to(gpu))
+    torch.cuda.synchronize()
+    check_parity(X, W, y, loss.detach().cpu(), gx1.cpu(), gw1.float().cpu(), grad=grad)
+    assert rel_fro(Xd.grad.float().cpu(), gx1.float().cpu()) <= 1e-2
+    assert rel_fro(Wd.grad.float().cpu(), gw1.float().cpu()) <= 1e-2
+
+
 @pytest.mark.parametrize("shift", [56.0, -56.0])
 def test_general_kept_block_out_of_range_recomputes(gpu, monkeypatch, shift):
     """The kept exponentials hold their terms while every row's largest logit
