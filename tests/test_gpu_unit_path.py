@@ -322,17 +322,17 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     assert torch.equal(dW2.view(torch.bfloat16)[: V * H].view(V, H), want)
 
 
-@pytest.mark.parametrize("shift", [0.0, 56.0])
-def test_forward_keep_matches_forward(gpu, shift):
+@pytest.mark.parametrize("shift,H", [(0.0, 192), (56.0, 192), (0.0, 200)])
+def test_forward_keep_matches_forward(gpu, shift, H):
     """mt_flce_forward_keep against mt_flce_forward: loss and lse the same
     bits; the kept block holds exp of the bf16 logits of vocabulary columns
     [0, 512) for every valid row (within bf16 rounding of exp); the guard is 0
     while every row's largest logit lies in [-48, 48] and 1 when the first
     rows' logits are shifted by 56 (X column of 56 against a weight column of
-    ones)."""
-    print(f"case forward_keep shift={shift}", flush=True)
+    ones).  H = 200: a partial last K stage."""
+    print(f"case forward_keep shift={shift} H={H}", flush=True)
     lib = _lib.load()
-    T, H, V, K = 600, 192, 1500, 512
+    T, V, K = 600, 1500, 512
     X, W, y = make_case(T, H, V, torch.bfloat16, seed=71)
     if shift:
         X[:100, 0] = shift
