@@ -315,20 +315,19 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
   if (!split_phase()) {
     using K = void (*)(DxArgs, DwArgs, uint32_t);
     // [dX mode][queue][dW output]; a tiled dX accumulator only beside the
-    // narrowing dW (the one-row-block entry), which never meets an untiled
-    // multi-block accumulator (kDxStore .. kDxAddEmit)
-#define MT_DXDW(m)                                                                        \
-  {{dx_dw_bf16_kernel<m, false, kDwRows>, dx_dw_bf16_kernel<m, false, kDwTiles>, nullptr}, \
-   {dx_dw_bf16_kernel<m, true, kDwRows>, dx_dw_bf16_kernel<m, true, kDwTiles>, nullptr}}
+    // narrowing dW (it lives in that entry's dW buffer); the narrowing dW
+    // also meets the row-major accumulator in the workspace (a buffer too
+    // small for it and X^T)
+#define MT_DXDW(m)                                                                          \
+  {{dx_dw_bf16_kernel<m, false, kDwRows>, dx_dw_bf16_kernel<m, false, kDwTiles>,             \
+    dx_dw_bf16_kernel<m, false, kDwNarrow>},                                                 \
+   {dx_dw_bf16_kernel<m, true, kDwRows>, dx_dw_bf16_kernel<m, true, kDwTiles>,               \
+    dx_dw_bf16_kernel<m, true, kDwNarrow>}}
 #define MT_DXDW_N(m)                                                  \
   {{nullptr, nullptr, dx_dw_bf16_kernel<m, false, kDwNarrow>}, \
    {nullptr, nullptr, dx_dw_bf16_kernel<m, true, kDwNarrow>}}
     static const K kern[7][2][3] = {
-        MT_DXDW(kDxStore), MT_DXDW(kDxAdd), MT_DXDW(kDxAddEmit),
-        {{dx_dw_bf16_kernel<kDxEmit, false, kDwRows>, dx_dw_bf16_kernel<kDxEmit, false, kDwTiles>,
-          dx_dw_bf16_kernel<kDxEmit, false, kDwNarrow>},
-         {dx_dw_bf16_kernel<kDxEmit, true, kDwRows>, dx_dw_bf16_kernel<kDxEmit, true, kDwTiles>,
-          dx_dw_bf16_kernel<kDxEmit, true, kDwNarrow>}},
+        MT_DXDW(kDxStore), MT_DXDW(kDxAdd), MT_DXDW(kDxAddEmit), MT_DXDW(kDxEmit),
         MT_DXDW_N(kDxTiledAcc + kDxStore), MT_DXDW_N(kDxTiledAcc + kDxAdd),
         MT_DXDW_N(kDxTiledAcc + kDxAddEmit)};
 #undef MT_DXDW

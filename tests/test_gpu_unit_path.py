@@ -322,6 +322,54 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     assert torch.equal(dW2.view(torch.bfloat16)[: V * H].view(V, H), want)
 
 
+def test_backward_narrow_accumulator_in_workspace(gpu):
+    """One row block and three vocabulary blocks where the dW buffer has no
+    room past the bf16 gradient for dX's accumulator and X^T (V = 1300 < 3 C):
+    mt_flce_backward_narrow keeps both in the workspace (the accumulator
+    row-major) and still matches mt_flce_backward_tiles + mt_flce_narrow_tiles
+    bit for bit, with the workspace mt_flce_backward_narrow_plan reports."""
+    from mini_trainer_amd.flce import backward_plan
+
+    print("case backward narrow, accumulator in the workspace", flush=True)
+    lib = _lib.load()
+    T, H, V = 900, 256, 1300
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=83, mask_frac=0.0)
+    X, W, y = X.to(gpu), W.to(gpu), y.to(gpu)
+    ri, rl, n = prepare_targets(y, V)
+    s = _stream(gpu)
+    loss = torch.empty(T, device=gpu)
+    lse = torch.empty(n, device=gpu)
+    fwb = int(lib.mt_flce_forward_workspace_bytes(T, n, H, V, _lib.MT_DTYPE_BF16))
+    fws = torch.empty(fwb, dtype=torch.uint8, device=gpu)
+    _lib.check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0, _p(ri),
+                                   _p(rl), n, _p(loss), _p(lse), _p(fws), fwb, s), "forward")
+    al = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    budget = al(1024 * 512 * 2) + al(1024 * H * 4) + al(H * 1024 * 2) + al(32)
+    C, Cv, wsb = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, narrow=True)
+    assert (C, Cv, wsb) == (1024, 512, budget)
+    g = torch.rand(T, device=gpu, generator=torch.Generator(device=gpu).manual_seed(9))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    dX1 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    dW1 = torch.full((tb // 4,), float("nan"), device=gpu)
+    _lib.check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                          _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX1), H,
+                                          _p(dW1), tb, C, Cv, _p(ws), wsb, s), "backward_tiles")
+    one = torch.ones(1, device=gpu)
+    want = torch.empty(V, H, dtype=torch.bfloat16, device=gpu)
+    _lib.check(lib.mt_flce_narrow_tiles(_p(one), _p(dW1), tb, V, H, _p(want), H,
+                                        _lib.MT_DTYPE_BF16, s), "narrow_tiles")
+    dX2 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    dW2 = torch.full((tb // 4,), float("nan"), device=gpu)
+    _lib.check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
+                                           _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX2), H,
+                                           _p(dW2), tb, C, Cv, _p(ws), wsb, None, s),
+               "backward_narrow")
+    torch.cuda.synchronize()
+    assert torch.equal(dX2, dX1)
+    assert torch.equal(dW2.view(torch.bfloat16)[: V * H].view(V, H), want)
+
+
 @pytest.mark.parametrize("shift,H", [(0.0, 192), (56.0, 192), (0.0, 200)])
 def test_forward_keep_matches_forward(gpu, shift, H):
     """mt_flce_forward_keep against mt_flce_forward: loss and lse the same
