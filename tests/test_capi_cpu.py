@@ -7,6 +7,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -209,6 +210,37 @@ def test_backward_narrow_plan_fits_budget(key):
         assert one
     with pytest.raises(_lib.FlceError):
         backward_plan(cfg.T, n, cfg.H, cfg.V, torch.float32, narrow=True)
+
+
+def test_backward_narrow_plan_workspace_formula():
+    """Over random shapes and budgets: the narrowing plan's blocks are
+    multiples of 256 and its workspace is the formula mt_flce_backward_narrow
+    checks -- the G block and the counters when one row block's accumulator
+    (as 256 x 256 tiles) and X^T fit in the dW buffer past the bf16 gradient,
+    else the G block, the row-major accumulator (several vocabulary blocks),
+    X^T and the counters; within the budget unless nothing fits (the 256 x
+    256 fallback)."""
+    lib = _lib.load()
+    rng = np.random.default_rng(3)
+    al = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    cd = lambda a, b: -(-a // b)  # noqa: E731
+    for _ in range(300):
+        T = int(rng.integers(1, 40000))
+        n = int(rng.integers(1, T + 1))
+        H = int(rng.integers(1, 80)) * 64
+        V = int(rng.integers(256, 160000))
+        budget = int(rng.choice([0, 1, int(rng.integers(1, 1 << 30))]))
+        C, Cv, ws = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, narrow=True)
+        assert C % 256 == 0 and Cv % 256 == 0 and C > 0 and Cv > 0
+        tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+        fits = C >= n and tb >= al(V * H * 2) + al(cd(C, 256) * cd(H, 256) * 65536 * 4) + al(H * C * 2)
+        if fits:
+            expect = al(C * Cv * 2) + al(32)
+        else:
+            expect = al(C * Cv * 2) + (al(C * H * 4) if Cv < V else 0) + al(H * C * 2) + al(32)
+        assert ws == expect, (T, n, H, V, budget, C, Cv)
+        b = budget or int(0.05 * T * V * 2)
+        assert ws <= b or (C, Cv) == (256, 256)
 
 
 def test_forward_keep_host_checks():
