@@ -33,6 +33,7 @@ import json
 import os
 import sys
 import time
+from typing import Optional
 
 import torch
 
@@ -209,18 +210,24 @@ class ForcedPath:
             os.environ[FUSED_ENV] = self.old
 
 
+def reference_minibatch(X, y, Wl, n_counted: int, paths=None):
+    """train.py:97-104 for one minibatch through the drop-in; W.grad
+    accumulates."""
+    Xl = X.detach().requires_grad_(True)
+    out_loss = drop_in(Xl, Wl, y)
+    if paths is not None:
+        paths.append(path_of(out_loss))
+    loss = out_loss.float().sum()
+    loss.item()  # train.py:99
+    loss = loss * WORLD_SIZE / n_counted  # train.py:102
+    loss.backward()  # train.py:104
+
+
 def reference_step(data, Wl, n_counted: int, paths=None):
     """train.py:97-104 for each minibatch through the drop-in, W.grad
     accumulating across them, cleared at the end (the optimizer's zero_grad)."""
     for X, y in data:
-        Xl = X.detach().requires_grad_(True)
-        out_loss = drop_in(Xl, Wl, y)
-        if paths is not None:
-            paths.append(path_of(out_loss))
-        loss = out_loss.float().sum()
-        loss.item()  # train.py:99
-        loss = loss * WORLD_SIZE / n_counted  # train.py:102
-        loss.backward()  # train.py:104
+        reference_minibatch(X, y, Wl, n_counted, paths)
     Wl.grad = None
 
 
@@ -236,42 +243,64 @@ def promise_step(data, Wl, n_counted: int, dW):
         (s * WORLD_SIZE / n_counted).backward()
 
 
-def timed(step, steps: int, warmup: int) -> float:
-    """ms per step over `steps` steps after `warmup` untimed ones, between
-    device synchronisations."""
+def timed(step, steps: int, warmup: int, stats: Optional[dict] = None) -> float:
+    """Median ms per step (BASELINE.md's statistic) over `steps` steps after
+    `warmup` untimed ones, between device synchronisations: one event after
+    each step on the current stream, each step's time the difference of
+    consecutive events.  stats, if given, receives the mean, min and max."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(steps):
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record()
+    for i in range(steps):
         step()
-    ev1.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
-    return ev0.elapsed_time(ev1) / steps
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    mid = len(per) // 2
+    median = per[mid] if len(per) % 2 else 0.5 * (per[mid - 1] + per[mid])
+    if stats is not None:
+        stats.update(mean=evs[0].elapsed_time(evs[-1]) / steps, min=per[0], max=per[-1])
+    return median
 
 
 def extra_hbm(data, Wl, n_counted: int, dtype) -> dict:
-    """Allocator peak of one minibatch of the reference step minus the live
-    inputs and the required outputs: loss [T] fp32, dX [T, H] (X.grad) and
-    the fp32 dW the library forms (W.grad, in the weight's dtype, is narrowed
-    into that same allocation)."""
-    X, y = data[0]
-    T, H = X.shape
-    V = Wl.shape[0]
+    """Device memory of the whole reference step, minibatch by minibatch
+    with W.grad accumulating across them: each minibatch's allocator peak
+    minus what is live when it starts (inputs, and W.grad so far) minus its
+    required outputs -- loss [T] fp32, dX [T, H] and the weight gradient in
+    the fp32 form the kernels accumulate it in (V H 4 bytes; a path that
+    never forms it, the narrowing backward, comes out below zero); the worst
+    minibatch is reported.  `..._over_bf16_outputs` counts the weight
+    gradient at its own dtype instead.  w_grad_storage_GB: the bytes
+    W.grad's storage holds after the step, against its nominal V H es."""
+    V, H = Wl.shape
     es = torch.finfo(dtype).bits // 8
-    dev = X.device
+    dev = Wl.device
     Wl.grad = None
-    torch.cuda.synchronize()
-    torch.cuda.reset_peak_memory_stats(dev)
-    base = torch.cuda.memory_allocated(dev)
-    reference_step([(X, y)], Wl, n_counted)
-    torch.cuda.synchronize()
-    peak = torch.cuda.max_memory_allocated(dev)
-    outputs = T * 4 + T * H * es + V * H * 4
-    return {"extra_hbm_GB": (peak - base - outputs) / 1e9,
+    worst, worst_own, peak_all = -float("inf"), -float("inf"), 0
+    for X, y in data:
+        T = X.shape[0]
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        reference_minibatch(X, y, Wl, n_counted)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated(dev)
+        peak_all = max(peak_all, peak)
+        common = T * 4 + T * H * es
+        worst = max(worst, peak - base - common - V * H * 4)
+        worst_own = max(worst_own, peak - base - common - V * H * es)
+    storage = Wl.grad.untyped_storage().nbytes()
+    Wl.grad = None
+    T = data[0][0].shape[0]
+    return {"extra_hbm_GB": worst / 1e9,
             "extra_hbm_budget_GB": 0.05 * T * V * es / 1e9,
-            "peak_memory_GB": peak / 1e9}
+            "extra_hbm_over_bf16_outputs_GB": worst_own / 1e9,
+            "w_grad_storage_GB": storage / 1e9,
+            "w_grad_nominal_GB": V * H * es / 1e9,
+            "peak_memory_GB": peak_all / 1e9}
 
 
 def roofline_of(report: dict, peak_flops: float, steps: int) -> tuple:
@@ -449,9 +478,10 @@ def main():
     mem = extra_hbm(data, Wl, N_total, cfg.dtype)
     log(f"reference step: path {paths[0]}, extra HBM {mem['extra_hbm_GB']:.3f} GB")
 
-    ms = timed(lambda: reference_step(data, Wl, N_total), args.steps, args.warmup)
+    step_stats = {}
+    ms = timed(lambda: reference_step(data, Wl, N_total), args.steps, args.warmup, step_stats)
     t_step = ms / 1e3
-    log(f"reference step: {ms:.2f} ms")
+    log(f"reference step: median {ms:.2f} ms, mean {step_stats['mean']:.2f} ms")
 
     # the same steps again with the library's per-launch events: the roofline
     # unit and the per-kernel table of the timed step
@@ -505,6 +535,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "ms_per_step_stat": "median of the timed steps (per-step HIP events)",
+        "ms_per_step_mean": step_stats["mean"],
+        "ms_per_step_min": step_stats["min"],
+        "ms_per_step_max": step_stats["max"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define MT_FLCE_ABI_VERSION 6
+#define MT_FLCE_ABI_VERSION 7
 
 typedef struct ihipStream_t* mt_stream_t; /* == hipStream_t */
 
@@ -190,9 +190,10 @@ int mt_flce_backward_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
  * (chunk_rows >= n_valid) fits the budget and its cost model ranks it first,
  * the caller runs mt_flce_backward_narrow with it: every dW tile contracts
  * all valid rows at once and is written once, in bf16 -- no read-modify-
- * write of an fp32 dW, no narrowing pass -- and dX's fp32 accumulator lives
- * in the dW buffer's unused half, so the workspace holds only the G block,
- * X^T and counters.  Otherwise (chunk_rows < n_valid) the caller runs
+ * write of an fp32 dW, no narrowing pass -- and dX's fp32 accumulator and
+ * X^T live in the scratch buffer of mt_flce_narrow_scratch_bytes (in the
+ * room a bf16 gradient leaves of the fp32 one the budget counts), so the
+ * workspace holds only the G block and counters.  Otherwise (chunk_rows < n_valid) the caller runs
  * mt_flce_backward_tiles and mt_flce_narrow_tiles with the same blocking
  * and workspace.  Same arguments and outputs as mt_flce_backward_plan.  (No
  * reference counterpart: the blocking of the backward that replaces
@@ -235,15 +236,20 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H,
  * X^T, its row factors and a few counters -- fits budget_bytes (0 = default:
  * 5% of T*V*2), then evened out over
  * the chunks.  Writes the chunk size, the workspace size and *pays = 1 if
- * a cost model expects the fused path to beat the general one
- * (mt_flce_forward + mt_flce_backward) under the same budget, else 0: small
- * budgets force small chunks, with few long dX tiles and one dW
- * read-modify-write per chunk, which the general path's two-dimensional
- * blocking avoids.
+ * a cost model expects the fused path to beat the general one under the
+ * same budget, else 0: small budgets force small chunks, with few long dX
+ * tiles and one dW read-modify-write per chunk, which the general path's
+ * two-dimensional blocking avoids.  with_accumulator != 0: the weight
+ * gradient is added into an fp32 accumulator, and the general path priced
+ * is mt_flce_forward + mt_flce_backward; 0: it is wanted in bf16, and the
+ * general path priced is the one mt_flce_backward_narrow_plan plans (one
+ * row block through mt_flce_backward_narrow after mt_flce_forward_keep, or
+ * mt_flce_backward_tiles and the narrowing pass).
  */
 int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V,
-                       int dtype, size_t budget_bytes, int64_t* chunk_rows,
-                       size_t* workspace_bytes, int* pays);
+                       int dtype, size_t budget_bytes, int with_accumulator,
+                       int64_t* chunk_rows, size_t* workspace_bytes,
+                       int* pays);
 
 /*
  * Fused forward + backward for a caller that knows the upstream gradient of
@@ -268,13 +274,14 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
                   void* workspace, size_t workspace_bytes, mt_stream_t stream);
 
 /*
- * mt_flce_backward with dW formed as tiles (layout of
- * mt_flce_dw_tiles_bytes) instead of rows, bf16 only: the same arithmetic,
- * so mt_flce_narrow_tiles of the result equals mt_flce_backward +
- * mt_flce_scale_grads bit for bit.  dW is never accumulated into (a
- * dw_accumulator stays on mt_flce_backward).  Replaces the same reference
- * interface as mt_flce_backward (the lm_head backward's dW = dS^T X,
- * none_reduction_losses.py:35 through autograd).
+ * mt_flce_backward with dW formed as 256 x 256 fp32 tiles in the two buffers
+ * of mt_flce_dw_tiles_layout instead of rows, bf16 only: the same
+ * arithmetic, so mt_flce_narrow_tiles of the result equals mt_flce_backward
+ * + mt_flce_scale_grads bit for bit.  accumulate_dW != 0 adds into the
+ * tiles already there (a call split over row ranges), else they are
+ * overwritten.  Replaces the same reference interface as mt_flce_backward
+ * (the lm_head backward's dW = dS^T X, none_reduction_losses.py:35 through
+ * autograd).
  */
 int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H,
                            int64_t V, int64_t ldx, int64_t ldw, int dtype,
@@ -282,7 +289,8 @@ int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H,
                            const int32_t* row_label, int64_t n_valid,
                            const float* lse, const float* grad_loss,
                            int64_t grad_stride, void* dX, int64_t lddx,
-                           float* dW_tiles, size_t dw_tiles_bytes,
+                           void* dW_lo, size_t dw_lo_bytes, float* dW_hi,
+                           size_t dw_hi_bytes, int accumulate_dW,
                            int64_t chunk_rows, int64_t chunk_vocab,
                            void* workspace, size_t workspace_bytes,
                            mt_stream_t stream);
@@ -290,12 +298,16 @@ int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H,
 /*
  * mt_flce_backward for one row block (chunk_rows >= n_valid, from
  * mt_flce_backward_narrow_plan) whose weight gradient is written in bf16,
- * bf16 only, H a multiple of 8: dW_buf (mt_flce_dw_tiles_bytes(V, H) bytes)
- * receives the gradient as contiguous bf16 rows [V, H] in its first V H 2
- * bytes -- each 256 x 256 tile narrowed once from its fp32 accumulators
- * (round to nearest even) -- and the rest of the buffer is scratch (dX's
- * fp32 accumulator, when it fits).  Bit for bit what mt_flce_backward_tiles
- * and mt_flce_narrow_tiles with a unit scale give for the same blocking.
+ * bf16 only, H a multiple of 8: dW_out (at least V H 2 bytes, 16-byte
+ * aligned) receives the gradient as contiguous bf16 rows [V, H] -- each
+ * 256 x 256 tile narrowed once from its fp32 accumulators (round to nearest
+ * even).  scratch (mt_flce_narrow_scratch_bytes(V, H, chunk_rows) bytes; may
+ * be NULL when that is 0) holds dX's fp32 accumulator and the block's X^T
+ * for the duration of the call: the plan puts them there when they fit in
+ * the V H 2 bytes that a bf16 gradient leaves of an fp32 one, so the call's
+ * peak is that of an fp32 weight gradient, and the weight gradient is the
+ * right size afterwards.  Bit for bit what mt_flce_backward_tiles and
+ * mt_flce_narrow_tiles with a unit scale give for the same blocking.
  *   kept_guard   NULL, or (softcap off, chunk_vocab < V) the guard word of an
  *                mt_flce_forward_keep call that kept keep_cols = chunk_vocab
  *                columns in this workspace's first bytes (the G block): the
@@ -311,29 +323,43 @@ int mt_flce_backward_narrow(const void* X, const void* W, int64_t T, int64_t H,
                             const int32_t* row_label, int64_t n_valid,
                             const float* lse, const float* grad_loss,
                             int64_t grad_stride, void* dX, int64_t lddx,
-                            void* dW_buf, size_t dw_buf_bytes,
-                            int64_t chunk_rows, int64_t chunk_vocab,
-                            void* workspace, size_t workspace_bytes,
-                            const int32_t* kept_guard, mt_stream_t stream);
+                            void* dW_out, size_t dw_out_bytes, void* scratch,
+                            size_t scratch_bytes, int64_t chunk_rows,
+                            int64_t chunk_vocab, void* workspace,
+                            size_t workspace_bytes, const int32_t* kept_guard,
+                            mt_stream_t stream);
 
 /*
- * Bytes of the tiled fp32 weight gradient that mt_flce_fused_tiles and
- * mt_flce_backward_tiles form
- * (0 for sizes out of range): a pad of 256 * round_up(H, 256) bf16 elements,
- * then ceil(V/256) x ceil(H/256) tiles of 256 x 256 fp32 in the order the
- * dW GEMM holds them.  At least V * H * 4, so the same allocation also
- * serves as a row-major fp32 [V, H] (mt_flce_backward's recompute for a
- * per-token gradient).  No counterpart in the reference.
+ * Bytes of the scratch buffer mt_flce_backward_narrow needs for one row
+ * block of chunk_rows (0: dX's accumulator and X^T stay in the workspace,
+ * or bad sizes).  No counterpart in the reference.
  */
-size_t mt_flce_dw_tiles_bytes(int64_t V, int64_t H);
+size_t mt_flce_narrow_scratch_bytes(int64_t V, int64_t H, int64_t chunk_rows);
 
 /*
- * mt_flce_fused with dW formed as tiles (layout of mt_flce_dw_tiles_bytes)
- * instead of rows: every load and store of the dW GEMM's accumulators is one
- * contiguous KiB, without the transpose a row-major tile edge needs.  Same
- * arithmetic, so mt_flce_narrow_tiles of the result equals mt_flce_fused +
- * mt_flce_scale_grads bit for bit.  dW is never accumulated into (a
- * dw_accumulator stays on mt_flce_fused).  Replaces the same reference
+ * Layout of the tiled fp32 weight gradient that mt_flce_fused_tiles and
+ * mt_flce_backward_tiles form: ceil(V/256) x ceil(H/256) tiles of 256 x 256
+ * fp32 in the order the dW GEMM holds them, row-major over the tile grid,
+ * over two caller buffers.  dW_lo is the weight gradient's own buffer of
+ * *lo_bytes = V H 2 bytes (a bf16 [V, H]): after a pad of 256 *
+ * round_up(H, 256) bf16 elements it holds tile rows [0, *lo_tile_rows);
+ * dW_hi (*hi_bytes, 0 when every tile row fits in dW_lo) holds the rest.
+ * mt_flce_narrow_tiles narrows the gradient into dW_lo in place, after
+ * which dW_hi can be freed: the weight gradient then occupies exactly the
+ * V H 2 bytes of a bf16 tensor, while the two buffers together hold the
+ * fp32 gradient the kernels accumulate.  No counterpart in the reference.
+ */
+int mt_flce_dw_tiles_layout(int64_t V, int64_t H, size_t* lo_bytes,
+                            int64_t* lo_tile_rows, size_t* hi_bytes);
+
+/*
+ * mt_flce_fused with dW formed as tiles in the two buffers of
+ * mt_flce_dw_tiles_layout instead of rows: every load and store of the dW
+ * GEMM's accumulators is one contiguous KiB, without the transpose a
+ * row-major tile edge needs.  Same arithmetic, so mt_flce_narrow_tiles of
+ * the result equals mt_flce_fused + mt_flce_scale_grads bit for bit.
+ * accumulate_dW != 0 adds into the tiles already there (a call split over
+ * row ranges), else they are overwritten.  Replaces the same reference
  * interface as mt_flce_fused (none_reduction_losses.py:16-23 -> LIGER's
  * fused_linear_cross_entropy_forward, whose grad_weight is the tensor here).
  */
@@ -342,25 +368,24 @@ int mt_flce_fused_tiles(const void* X, const void* W, int64_t T, int64_t H,
                         float softcap, const int32_t* row_index,
                         const int32_t* row_label, int64_t n_valid,
                         const float* grad_loss, int64_t grad_stride, float* loss,
-                        float* lse, void* dX, int64_t lddx, float* dW_tiles,
-                        size_t dw_tiles_bytes, int64_t chunk_rows,
-                        void* workspace, size_t workspace_bytes,
-                        mt_stream_t stream);
+                        float* lse, void* dX, int64_t lddx, void* dW_lo,
+                        size_t dw_lo_bytes, float* dW_hi, size_t dw_hi_bytes,
+                        int accumulate_dW, int64_t chunk_rows, void* workspace,
+                        size_t workspace_bytes, mt_stream_t stream);
 
 /*
- * scale * tiled dW -> bf16 rows [V, H] of pitch ldo (the weight gradient in
- * the weight's dtype); the tiled counterpart of mt_flce_scale_grads's dW
- * part (LIGER's fused_linear_cross_entropy_backward: grad_weight times
- * grad_output[0]).  dW_out is either a separate buffer or dW_tiles itself
- * (ldo <= round_up(H, 256)): in place, row r lands at element r * ldo from
- * the base, and the tile rows are narrowed in launches {0}, {1}, [2, 4),
- * [4, 8), ... so that none is overwritten before it is read.  bf16 only,
- * H % 8 == 0; rounds to nearest even.  scale fp32 [1] on the device.
+ * scale * tiled dW (the two buffers of mt_flce_dw_tiles_layout) -> the
+ * weight gradient in bf16, rows [V, H] of pitch H in place in dW_lo; the
+ * tiled counterpart of mt_flce_scale_grads's dW part (LIGER's
+ * fused_linear_cross_entropy_backward: grad_weight times grad_output[0]).
+ * The tile rows are narrowed in launches {0}, {1}, [2, 4), [4, 8), ... so
+ * that none is overwritten before it is read; dW_hi is only read, and can
+ * be freed once the stream has passed this call.  bf16 output, H % 8 == 0;
+ * rounds to nearest even.  scale fp32 [1] on the device.
  */
-int mt_flce_narrow_tiles(const float* scale, const float* dW_tiles,
-                         size_t dw_tiles_bytes, int64_t V, int64_t H,
-                         void* dW_out, int64_t ldo, int dtype_out,
-                         mt_stream_t stream);
+int mt_flce_narrow_tiles(const float* scale, void* dW_lo, size_t dw_lo_bytes,
+                         const float* dW_hi, size_t dw_hi_bytes, int64_t V,
+                         int64_t H, mt_stream_t stream);
 
 /*
  * Per-sample sums over a packed batch (no counterpart in the reference, which

@@ -10,7 +10,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p, c_char_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmt_flce.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MT_DTYPE_F32 = 0
 MT_DTYPE_BF16 = 1
@@ -51,7 +51,7 @@ SIGNATURES = {
                                  c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                  c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64,
                                  c_int64, c_void_p, c_size_t, c_void_p]),
-    "mt_flce_fused_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t,
+    "mt_flce_fused_plan": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_size_t, c_int,
                                    POINTER(c_int64), POINTER(c_size_t), POINTER(c_int)]),
     "mt_flce_fused": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                               c_int, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
@@ -60,19 +60,23 @@ SIGNATURES = {
     "mt_flce_backward_tiles": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                        c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
                                        c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
-                                       c_size_t, c_int64, c_int64, c_void_p, c_size_t, c_void_p]),
+                                       c_size_t, c_void_p, c_size_t, c_int, c_int64, c_int64,
+                                       c_void_p, c_size_t, c_void_p]),
     "mt_flce_backward_narrow": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                         c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
                                         c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
-                                        c_size_t, c_int64, c_int64, c_void_p, c_size_t, c_void_p,
-                                        c_void_p]),
-    "mt_flce_dw_tiles_bytes": (c_size_t, [c_int64, c_int64]),
+                                        c_size_t, c_void_p, c_size_t, c_int64, c_int64, c_void_p,
+                                        c_size_t, c_void_p, c_void_p]),
+    "mt_flce_narrow_scratch_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
+    "mt_flce_dw_tiles_layout": (c_int, [c_int64, c_int64, POINTER(c_size_t), POINTER(c_int64),
+                                        POINTER(c_size_t)]),
     "mt_flce_fused_tiles": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                     c_int64, c_int, c_float, c_void_p, c_void_p, c_int64,
                                     c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
-                                    c_void_p, c_size_t, c_int64, c_void_p, c_size_t, c_void_p]),
-    "mt_flce_narrow_tiles": (c_int, [c_void_p, c_void_p, c_size_t, c_int64, c_int64, c_void_p,
-                                     c_int64, c_int, c_void_p]),
+                                    c_void_p, c_size_t, c_void_p, c_size_t, c_int, c_int64,
+                                    c_void_p, c_size_t, c_void_p]),
+    "mt_flce_narrow_tiles": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_size_t, c_int64,
+                                     c_int64, c_void_p]),
     "mt_segment_sum": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_int64,
                                c_void_p, c_void_p, c_void_p, c_void_p]),
     "mt_flce_scale_grads": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p,

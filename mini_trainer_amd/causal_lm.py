@@ -84,7 +84,7 @@ def patch_causal_lm(model: torch.nn.Module,
     CausalLMOutputWithPast (loss = per-token loss, logits = None).  Without
     labels the model's own forward runs unchanged.
 
-    Extra keywords of the patched forward: `grad_scale` (the upstream gradient
+    Extra keywords of the patched forward: `mt_grad_scale` (the upstream gradient
     of the per-token loss, known before the forward in train.py:97-104:
     world_size / batch_num_loss_counted_tokens) promises the gradient to the
     fused path; `cu_seqlens` (int32 [S + 1], the packed minibatch's sample
@@ -105,8 +105,8 @@ def patch_causal_lm(model: torch.nn.Module,
 
     def forward(input_ids=None, attention_mask=None, position_ids=None, past_key_values=None,
                 inputs_embeds=None, labels=None, use_cache=None, logits_to_keep=0,
-                shift_labels=None, grad_scale=None, cu_seqlens=None, ignore_index: int = -100,
-                **kwargs):
+                shift_labels=None, mt_grad_scale=None, cu_seqlens=None,
+                ignore_index: int = -100, **kwargs):
         kwargs.pop("num_items_in_batch", None)
         if labels is None and shift_labels is None:
             return original(input_ids=input_ids, attention_mask=attention_mask,
@@ -123,7 +123,7 @@ def patch_causal_lm(model: torch.nn.Module,
             hidden = hidden.to(head.weight.dtype)
         loss = causal_lm_loss(hidden, head.weight, labels=labels,
                               shift_labels=shift_labels, ignore_index=ignore_index,
-                              final_logit_softcapping=softcap, grad_scale=grad_scale,
+                              final_logit_softcapping=softcap, grad_scale=mt_grad_scale,
                               dw_accumulator=dw_accumulator)
         seg_loss = seg_cnt = None
         if cu_seqlens is not None:

@@ -539,17 +539,19 @@ struct BwdPlan {
 size_t tiled_acc_bytes(int64_t C, int64_t H) {
   return (size_t)cdiv(C, 256) * cdiv(H, 256) * 65536 * sizeof(float);
 }
-// The narrowing entry's dW buffer (mt_flce_dw_tiles_bytes, the size of the
-// fp32 gradient) holds the bf16 gradient in its first V H 2 bytes; dX's
-// tiled accumulator and the block's X^T go after them when both fit (else
-// into the workspace, the accumulator row-major).
+// The narrowing entry writes the bf16 gradient (V H 2 bytes) where the
+// budget counts an fp32 one (dw_tiles_bytes): dX's tiled accumulator and the
+// block's X^T go into a scratch buffer of the caller's
+// (mt_flce_narrow_scratch_bytes) when both fit in the difference (else into
+// the workspace, the accumulator row-major), so the call's peak stays that
+// of an fp32 gradient.
 size_t dw_tiles_bytes(int64_t V, int64_t H);
-inline size_t narrow_acc_offset(int64_t V, int64_t H) { return align_up((size_t)V * H * 2); }
-inline size_t narrow_xt_offset(int64_t V, int64_t H, int64_t C) {
-  return narrow_acc_offset(V, H) + align_up(tiled_acc_bytes(C, H));
+inline size_t narrow_xt_offset(int64_t H, int64_t C) { return align_up(tiled_acc_bytes(C, H)); }
+inline size_t narrow_scratch_need(int64_t H, int64_t C) {
+  return narrow_xt_offset(H, C) + align_up((size_t)H * C * 2);
 }
 inline bool narrow_scratch_fits(int64_t V, int64_t H, int64_t C) {
-  return dw_tiles_bytes(V, H) >= narrow_xt_offset(V, H, C) + align_up((size_t)H * C * 2);
+  return dw_tiles_bytes(V, H) >= align_up((size_t)V * H * 2) + narrow_scratch_need(H, C);
 }
 
 // narrow: the plan of a bf16 backward whose dW is wanted in bf16 without an
@@ -677,21 +679,58 @@ int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t 
 }
 
 // Tiled fp32 dW: 256 x 256 tiles (the grid padded to whole tiles), each
-// 256 KiB in the accumulators' own order, row-major over the tile grid,
-// after a leading pad of half a tile row (256 * Hp bf16 elements): the
-// bf16 rows narrowed out of tile row r then end at or before tile row r / 2
-// starts, so tile rows narrowed in launches {0}, {1}, [2, 4), [4, 8), ...
-// only overwrite tiles an earlier launch has read.
+// 256 KiB in the accumulators' own order, row-major over the tile grid, in
+// two buffers.  `lo` is the weight gradient's own bf16 [V, H] buffer (V H 2
+// bytes): after a leading pad of half a tile row (256 * Hp bf16 elements)
+// it holds tile rows [0, lo_rows), as many as fit; `hi` holds the rest.
+// The bf16 rows narrowed out of tile row r end at or before tile row r / 2
+// starts, so tile rows narrowed in place in launches {0}, {1}, [2, 4),
+// [4, 8), ... only overwrite tiles an earlier launch has read, and once
+// narrowed the gradient fills `lo` exactly: `hi` can be freed.
 int64_t dw_tiles_pad(int64_t H) { return 128 * round_up(H, 256); }  // floats
+size_t dw_tile_row_bytes(int64_t H) { return (size_t)cdiv(H, 256) * 65536 * 4; }
+// bytes of the one-buffer form of the layout (pad + every tile row): the
+// fp32 gradient the budget counts as an output, V H 4 bytes or a little more
 size_t dw_tiles_bytes(int64_t V, int64_t H) {
-  return (size_t)dw_tiles_pad(H) * 4 + (size_t)cdiv(V, 256) * cdiv(H, 256) * 65536 * 4;
+  return (size_t)dw_tiles_pad(H) * 4 + (size_t)cdiv(V, 256) * dw_tile_row_bytes(H);
+}
+size_t dw_lo_bytes(int64_t V, int64_t H) { return (size_t)V * H * 2; }
+int64_t dw_lo_rows(int64_t V, int64_t H) {
+  const size_t lo = dw_lo_bytes(V, H), pad = (size_t)dw_tiles_pad(H) * 4, tr = dw_tile_row_bytes(H);
+  return lo < pad + tr ? 0 : std::min<int64_t>(cdiv(V, 256), (int64_t)((lo - pad) / tr));
+}
+size_t dw_hi_bytes(int64_t V, int64_t H) {
+  return (size_t)(cdiv(V, 256) - dw_lo_rows(V, H)) * dw_tile_row_bytes(H);
+}
+// The two buffers of a tiled dW as the kernels take them.
+struct TiledDw {
+  float* lo = nullptr;  // the bf16 gradient's buffer (tiles after the pad)
+  float* hi = nullptr;
+  int32_t lo_rows = 0;
+};
+void set_tiled(DwArgs& w, const TiledDw& td, int64_t H) {
+  w.tiled = 1;
+  w.dW = td.lo;
+  w.tile_pad = dw_tiles_pad(H);
+  w.dW_hi = td.hi;
+  w.lo_rows = td.lo_rows;
+  w.lddw = 0;
 }
 // Every tile zero (the gradient of a call without valid rows), as 1 KiB rows.
-int zero_tiles(float* tiles, int64_t V, int64_t H, hipStream_t s) {
-  const int64_t rows = cdiv(V, 256) * cdiv(H, 256) * 256;
-  hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(rows, 8192)), dim3(256), 0, s,
-                     tiles + dw_tiles_pad(H), rows, (int64_t)256, (int64_t)256);
-  return check_launch("zero_matrix_f32_kernel");
+int zero_tiles(const TiledDw& td, int64_t V, int64_t H, hipStream_t s) {
+  const int64_t tn = cdiv(H, 256), R = cdiv(V, 256);
+  const int64_t rows_lo = td.lo_rows * tn * 256, rows_hi = (R - td.lo_rows) * tn * 256;
+  if (rows_lo > 0) {
+    hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(rows_lo, 8192)), dim3(256), 0,
+                       s, td.lo + dw_tiles_pad(H), rows_lo, (int64_t)256, (int64_t)256);
+    MT_TRY(check_launch("zero_matrix_f32_kernel"));
+  }
+  if (rows_hi > 0) {
+    hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(rows_hi, 8192)), dim3(256), 0,
+                       s, td.hi, rows_hi, (int64_t)256, (int64_t)256);
+    MT_TRY(check_launch("zero_matrix_f32_kernel"));
+  }
+  return MT_OK;
 }
 
 template <typename T>
@@ -701,20 +740,20 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
                     int64_t N, const float* lse, const float* grad, int64_t gstride, void* dX,
                     int64_t lddx, float* dW, int64_t lddw, int accumulate, int dw_out, int64_t C,
                     int64_t Cv, char* ws, hipStream_t stream, char* scratch_ext = nullptr,
-                    const int32_t* kept_guard = nullptr) {
+                    const int32_t* kept_guard = nullptr, const TiledDw* td = nullptr) {
   constexpr int es = sizeof(T);
   const Geometry geo = geometry(es);
   const int64_t nv = cdiv(V, Cv);
   // scratch_ext (the narrowing entry, one row block): dX's accumulator (as
-  // tiles) and X^T in the dW buffer past the bf16 gradient
+  // tiles) and X^T in the caller's scratch buffer
   char* G = ws;
   float* accbuf = nv > 1 ? reinterpret_cast<float*>(ws + align_up((size_t)C * Cv * es)) : nullptr;
   char* XcT = ws + align_up((size_t)C * Cv * es) +
               (nv > 1 ? align_up((size_t)C * H * sizeof(float)) : 0);
   const bool acc_tiles = scratch_ext != nullptr && nv > 1;
   if (scratch_ext) {
-    accbuf = reinterpret_cast<float*>(scratch_ext + narrow_acc_offset(V, H));
-    XcT = scratch_ext + narrow_xt_offset(V, H, C);
+    accbuf = reinterpret_cast<float*>(scratch_ext);
+    XcT = scratch_ext + narrow_xt_offset(H, C);
   }
   char* const ws_end = ws + align_up((size_t)C * Cv * es) +
                        (nv > 1 && !scratch_ext ? align_up((size_t)C * H * sizeof(float)) : 0) +
@@ -856,11 +895,7 @@ int launch_backward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t
       w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
       w.tiles_m = (int32_t)cdiv(cv, geo.tile_m);
       w.tiles_n = (int32_t)cdiv(H, geo.tile_n);
-      if (dw_out == kDwTiles) {  // (bf16 only; the block's tile rows start at v0 / 256)
-        w.tiled = 1;
-        w.tile_pad = dw_tiles_pad(H);
-        w.lddw = 0;
-      }
+      if (dw_out == kDwTiles) set_tiled(w, *td, H);  // (bf16; the block's tile rows start at v0 / 256)
       if (dw_out == kDwNarrow) w.narrow = 1;  // dW: bf16 rows of pitch lddw
       if (use_queue) w.queue = queue;
       if (beside) {
@@ -960,23 +995,44 @@ FusedPlan plan_fused(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) 
   return p;
 }
 
-// Is the fused path expected to beat the general one (forward + recompute
-// backward) under the same budget?  Small budgets force small chunks: few
-// dX tiles with a long K and one dW read-modify-write per chunk, which the
-// general path's two-dimensional blocking avoids.
-bool fused_pays(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget) {
+// Modelled seconds of the general path that a bf16 call would otherwise
+// take: the forward plus the planned backward.  narrow (no accumulator: the
+// weight gradient is wanted in bf16): the plan of
+// mt_flce_backward_narrow_plan -- one row block through the narrowing
+// backward, whose forward keeps the first vocabulary block (its recompute
+// skipped), or several row blocks on tiles plus the narrowing pass; else the
+// row-major fp32 backward into an accumulator.
+double general_cost(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget, bool narrow) {
+  const BwdPlan b = plan_backward(T, N, H, V, 2, budget, narrow);
+  if (!b.C) return 1e300;
+  double t = forward_cost(N, H, V);
+  if (!narrow) return t + backward_cost(N, H, V, b.C, b.Cv, 2);
+  if (b.C >= N) {
+    t += backward_cost(N, H, V, b.C, b.Cv, 2, true);
+    if (b.Cv < V) t -= gemm_time(cdiv(N, 256) * cdiv(b.Cv, 256), H);  // the kept block
+    return t;
+  }
+  return t + backward_cost(N, H, V, b.C, b.Cv, 2) + (double)V * H * 6 / kBw + 10 * kLaunch;
+}
+
+// Is the fused path expected to beat the general one under the same budget?
+// Small budgets force small chunks: few dX tiles with a long K and one dW
+// read-modify-write per chunk, which the general path's two-dimensional
+// blocking (or its one-row-block narrowing backward) avoids.  accumulator:
+// the weight gradient is added into an fp32 [V, H] (the general path is
+// then mt_flce_backward), else it is wanted in bf16.
+bool fused_pays(int64_t T, int64_t N, int64_t H, int64_t V, size_t budget, bool accumulator) {
   const FusedPlan f = plan_fused(T, N, H, V, budget);
-  const BwdPlan b = plan_backward(T, N, H, V, 2, budget);
-  if (!f.C || !b.C) return false;
-  return fused_cost(N, H, V, f.C) < 0.97 * (forward_cost(N, H, V) + backward_cost(N, H, V, b.C, b.Cv, 2));
+  if (!f.C) return false;
+  return fused_cost(N, H, V, f.C) < 0.97 * general_cost(T, N, H, V, budget, !accumulator);
 }
 
 int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V, int64_t ldx,
                  int64_t ldw,
                  float softcap, const int32_t* row_index, const int32_t* row_label, int64_t N,
                  const float* grad, int64_t gstride, float* loss, float* lse, void* dX,
-                 int64_t lddx, float* dW, int64_t lddw, int accumulate, bool tiled, int64_t C,
-                 char* ws, hipStream_t stream) {
+                 int64_t lddx, float* dW, int64_t lddw, int accumulate, const TiledDw* td,
+                 int64_t C, char* ws, hipStream_t stream) {
   const int64_t Vp = vocab_pad(V), vt = cdiv(V, 256);
   char* S = ws;
   float* part = reinterpret_cast<float*>(ws + align_up((size_t)C * Vp * 2));
@@ -1122,11 +1178,7 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
     w.accumulate = (accumulate || c0 > 0) ? 1 : 0;
     w.tiles_m = (int32_t)vt;
     w.tiles_n = (int32_t)cdiv(H, 256);
-    if (tiled) {
-      w.tiled = 1;
-      w.tile_pad = dw_tiles_pad(H);
-      w.lddw = 0;
-    }
+    if (td) set_tiled(w, *td, H);
     // the work queue pays where the tiles outnumber the CUs several times
     // and each has at least two K stages
     // (one workgroup per CU covers the 8 XCD shares only for a multiple of 8 CUs)
@@ -1390,17 +1442,18 @@ int mt_flce_backward_narrow_plan(int64_t T, int64_t n_valid, int64_t H, int64_t 
 
 namespace {
 
-// mt_flce_backward (row-major dW), mt_flce_backward_tiles (tiled dW of
-// dw_tiles_bytes, bf16 only, lddw == 0, never accumulated into) and
-// mt_flce_backward_narrow (bf16 rows of pitch H at the start of a buffer of
-// dw_tiles_bytes, one row block, never accumulated into).
+// mt_flce_backward (row-major dW), mt_flce_backward_tiles (tiled dW in the
+// two buffers of td, bf16 only, lddw == 0) and mt_flce_backward_narrow (bf16
+// rows of pitch H at dW, one row block, never accumulated into; dX's
+// accumulator and X^T in `scratch` when narrow_scratch_fits).
 int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
                    int64_t ldw, int dtype, float softcap, const int32_t* row_index,
                    const int32_t* row_label, int64_t n_valid, const float* lse,
                    const float* grad_loss, int64_t grad_stride, void* dX, int64_t lddx, float* dW,
                    int64_t lddw, int accumulate_dW, int dw_out, int64_t chunk_rows,
                    int64_t chunk_vocab, void* workspace, size_t workspace_bytes, mt_stream_t stream,
-                   const int32_t* kept_guard = nullptr) {
+                   const int32_t* kept_guard = nullptr, const TiledDw* td = nullptr,
+                   void* scratch = nullptr, size_t scratch_bytes = 0) {
   MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
   const int es = esize_of(dtype);
   if (n_valid < 0 || n_valid > T)
@@ -1427,7 +1480,12 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
   if ((reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(dW) |
        reinterpret_cast<uintptr_t>(workspace)) % 16 != 0)
     return fail(MT_ERR_INVALID_ARGUMENT, "dX, dW and workspace must be 16-byte aligned");
-  const bool outside = dw_out == kDwNarrow && narrow_scratch_fits(V, H, chunk_rows);
+  const bool outside = dw_out == kDwNarrow && n_valid > 0 && narrow_scratch_fits(V, H, chunk_rows);
+  if (outside && (!scratch || scratch_bytes < narrow_scratch_need(H, chunk_rows) ||
+                  reinterpret_cast<uintptr_t>(scratch) % 16 != 0))
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "narrowing scratch %zu bytes < mt_flce_narrow_scratch_bytes = %zu (or misaligned)",
+                scratch_bytes, narrow_scratch_need(H, chunk_rows));
   if (n_valid > 0) {
     if (chunk_rows <= 0 || chunk_rows % 256 != 0 || chunk_vocab <= 0 || chunk_vocab % 256 != 0)
       return fail(MT_ERR_INVALID_ARGUMENT,
@@ -1454,7 +1512,7 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
   }
   if (n_valid == 0) {
     if (dw_out == kDwTiles) {
-      MT_TRY(zero_tiles(dW, V, H, s));
+      if (!accumulate_dW) MT_TRY(zero_tiles(*td, V, H, s));
     } else if (dw_out == kDwNarrow) {  // V x H bf16 = V x H / 2 floats
       hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
                          s, dW, V, H / 2, H / 2);
@@ -1467,12 +1525,12 @@ int backward_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V
     return MT_OK;
   }
   if (dtype == MT_DTYPE_BF16) {
-    char* scratch_ext = outside ? reinterpret_cast<char*>(dW) : nullptr;
+    char* scratch_ext = outside ? static_cast<char*>(scratch) : nullptr;
     return launch_backward<__bf16>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                    grad_loss, grad_stride, dX, lddx, dW,
                                    dw_out == kDwNarrow ? H : lddw, accumulate_dW, dw_out, chunk_rows,
                                    chunk_vocab, static_cast<char*>(workspace), s, scratch_ext,
-                                   kept_guard);
+                                   kept_guard, td);
   }
   return launch_backward<float>(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, lse,
                                 grad_loss, grad_stride, dX, lddx, dW, lddw, accumulate_dW, kDwRows,
@@ -1494,45 +1552,91 @@ int mt_flce_backward(const void* X, const void* W, int64_t T, int64_t H, int64_t
                         chunk_vocab, workspace, workspace_bytes, stream);
 }
 
+}  // extern "C"
+
+namespace {
+
+// The two buffers of a tiled dW, checked against the layout of V x H.
+int tiled_args(int64_t V, int64_t H, void* lo, size_t lo_bytes, float* hi, size_t hi_bytes,
+               TiledDw& td) {
+  if (V <= 0 || H <= 0 || V > INT32_MAX || H > INT32_MAX)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes H=%lld V=%lld", (long long)H, (long long)V);
+  if (!lo || lo_bytes < dw_lo_bytes(V, H))
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_lo %zu bytes < V H 2 = %zu", lo_bytes, dw_lo_bytes(V, H));
+  const size_t need_hi = dw_hi_bytes(V, H);
+  if (hi_bytes < need_hi || (need_hi > 0 && !hi))
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_hi %zu bytes < mt_flce_dw_tiles_layout's %zu", hi_bytes,
+                need_hi);
+  if ((reinterpret_cast<uintptr_t>(lo) | reinterpret_cast<uintptr_t>(hi)) % 16 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_lo and dW_hi must be 16-byte aligned");
+  const char *l0 = static_cast<const char*>(lo), *l1 = l0 + dw_lo_bytes(V, H);
+  const char *h0 = reinterpret_cast<const char*>(hi), *h1 = h0 + need_hi;
+  if (need_hi > 0 && l0 < h1 && h0 < l1) return fail(MT_ERR_INVALID_ARGUMENT, "dW_lo and dW_hi overlap");
+  td.lo = static_cast<float*>(lo);
+  td.hi = hi;
+  td.lo_rows = (int32_t)dw_lo_rows(V, H);
+  return MT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_flce_dw_tiles_layout(int64_t V, int64_t H, size_t* lo_bytes, int64_t* lo_tile_rows,
+                            size_t* hi_bytes) {
+  if (V <= 0 || H <= 0 || V > INT32_MAX || H > INT32_MAX)
+    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes H=%lld V=%lld", (long long)H, (long long)V);
+  if (!lo_bytes || !lo_tile_rows || !hi_bytes) return fail(MT_ERR_INVALID_ARGUMENT, "null output pointer");
+  *lo_bytes = dw_lo_bytes(V, H);
+  *lo_tile_rows = dw_lo_rows(V, H);
+  *hi_bytes = dw_hi_bytes(V, H);
+  return MT_OK;
+}
+
+size_t mt_flce_narrow_scratch_bytes(int64_t V, int64_t H, int64_t chunk_rows) {
+  if (V <= 0 || H <= 0 || V > INT32_MAX || H > INT32_MAX || chunk_rows <= 0) return 0;
+  return narrow_scratch_fits(V, H, chunk_rows) ? narrow_scratch_need(H, chunk_rows) : 0;
+}
+
 int mt_flce_backward_tiles(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
                            int64_t ldx, int64_t ldw, int dtype, float softcap,
                            const int32_t* row_index, const int32_t* row_label, int64_t n_valid,
                            const float* lse, const float* grad_loss, int64_t grad_stride, void* dX,
-                           int64_t lddx, float* dW_tiles, size_t dw_tiles_bytes_,
-                           int64_t chunk_rows, int64_t chunk_vocab, void* workspace,
-                           size_t workspace_bytes, mt_stream_t stream) {
+                           int64_t lddx, void* dW_lo, size_t dw_lo_bytes_, float* dW_hi,
+                           size_t dw_hi_bytes_, int accumulate_dW, int64_t chunk_rows,
+                           int64_t chunk_vocab, void* workspace, size_t workspace_bytes,
+                           mt_stream_t stream) {
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "tiled dW is bf16 only (dtype %d)", dtype);
-  if (H > 0 && V > 0 && dw_tiles_bytes_ < dw_tiles_bytes(V, H))
-    return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles %zu bytes < mt_flce_dw_tiles_bytes = %zu",
-                dw_tiles_bytes_, dw_tiles_bytes(V, H));
+  TiledDw td;
+  MT_TRY(tiled_args(V, H, dW_lo, dw_lo_bytes_, dW_hi, dw_hi_bytes_, td));
   return backward_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid, lse,
-                        grad_loss, grad_stride, dX, lddx, dW_tiles, 0, 0, kDwTiles, chunk_rows,
-                        chunk_vocab, workspace, workspace_bytes, stream);
+                        grad_loss, grad_stride, dX, lddx, td.lo, 0, accumulate_dW ? 1 : 0, kDwTiles,
+                        chunk_rows, chunk_vocab, workspace, workspace_bytes, stream, nullptr, &td);
 }
 
 int mt_flce_backward_narrow(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
                             int64_t ldx, int64_t ldw, int dtype, float softcap,
                             const int32_t* row_index, const int32_t* row_label, int64_t n_valid,
                             const float* lse, const float* grad_loss, int64_t grad_stride,
-                            void* dX, int64_t lddx, void* dW_buf, size_t dw_buf_bytes,
-                            int64_t chunk_rows, int64_t chunk_vocab, void* workspace,
-                            size_t workspace_bytes, const int32_t* kept_guard,
-                            mt_stream_t stream) {
+                            void* dX, int64_t lddx, void* dW_out, size_t dw_out_bytes,
+                            void* scratch, size_t scratch_bytes, int64_t chunk_rows,
+                            int64_t chunk_vocab, void* workspace, size_t workspace_bytes,
+                            const int32_t* kept_guard, mt_stream_t stream) {
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "the narrowing backward is bf16 only (dtype %d)", dtype);
-  if (H > 0 && V > 0 && dw_buf_bytes < dw_tiles_bytes(V, H))
-    return fail(MT_ERR_INVALID_ARGUMENT, "dW buffer %zu bytes < mt_flce_dw_tiles_bytes = %zu",
-                dw_buf_bytes, dw_tiles_bytes(V, H));
+  if (H > 0 && V > 0 && dw_out_bytes < dw_lo_bytes(V, H))
+    return fail(MT_ERR_INVALID_ARGUMENT, "dW_out %zu bytes < V H 2 = %zu", dw_out_bytes,
+                dw_lo_bytes(V, H));
   return backward_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid, lse,
-                        grad_loss, grad_stride, dX, lddx, static_cast<float*>(dW_buf), 0, 0,
+                        grad_loss, grad_stride, dX, lddx, static_cast<float*>(dW_out), 0, 0,
                         kDwNarrow, chunk_rows, chunk_vocab, workspace, workspace_bytes, stream,
-                        kept_guard);
+                        kept_guard, nullptr, scratch, scratch_bytes);
 }
 
 int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype,
-                       size_t budget_bytes, int64_t* chunk_rows, size_t* workspace_bytes,
-                       int* pays) {
+                       size_t budget_bytes, int with_accumulator, int64_t* chunk_rows,
+                       size_t* workspace_bytes, int* pays) {
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "the fused path is bf16 only (dtype %d)", dtype);
   if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0)
@@ -1543,7 +1647,7 @@ int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dty
   const FusedPlan p = plan_fused(T, n_valid, H, V, budget_bytes);
   *chunk_rows = p.C;
   *workspace_bytes = p.ws;
-  *pays = fused_pays(T, n_valid, H, V, budget_bytes) ? 1 : 0;
+  *pays = fused_pays(T, n_valid, H, V, budget_bytes, with_accumulator != 0) ? 1 : 0;
   return MT_OK;
 }
 
@@ -1552,13 +1656,14 @@ int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dty
 namespace {
 
 // mt_flce_fused (row-major dW, lddw > 0) and mt_flce_fused_tiles (tiled dW
-// of dw_tiles_bytes, lddw == 0, never accumulated into).
+// in the two buffers of td, lddw == 0).
 int fused_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
                 int64_t ldw, int dtype, float softcap, const int32_t* row_index,
                 const int32_t* row_label, int64_t n_valid, const float* grad_loss,
                 int64_t grad_stride, float* loss, float* lse, void* dX, int64_t lddx, float* dW,
-                int64_t lddw, int accumulate_dW, bool tiled, int64_t chunk_rows, void* workspace,
-                size_t workspace_bytes, mt_stream_t stream) {
+                int64_t lddw, int accumulate_dW, const TiledDw* td, int64_t chunk_rows,
+                void* workspace, size_t workspace_bytes, mt_stream_t stream) {
+  const bool tiled = td != nullptr;
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "the fused path is bf16 only (dtype %d)", dtype);
   MT_TRY(check_common(X, W, T, H, V, ldx, ldw, dtype, softcap));
@@ -1605,7 +1710,7 @@ int fused_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V, i
   }
   if (n_valid == 0) {
     if (tiled) {
-      MT_TRY(zero_tiles(dW, V, H, s));
+      if (!accumulate_dW) MT_TRY(zero_tiles(*td, V, H, s));
     } else if (!accumulate_dW) {
       hipLaunchKernelGGL(zero_matrix_f32_kernel, dim3((uint32_t)std::min<int64_t>(V, 8192)), dim3(256), 0,
                          s, dW, V, H, lddw);
@@ -1614,7 +1719,7 @@ int fused_entry(const void* X, const void* W, int64_t T, int64_t H, int64_t V, i
     return MT_OK;
   }
   return launch_fused(X, W, T, H, V, ldx, ldw, softcap, row_index, row_label, n_valid, grad_loss,
-                      grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, tiled, chunk_rows,
+                      grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, td, chunk_rows,
                       static_cast<char*>(workspace), s);
 }
 
@@ -1629,27 +1734,22 @@ int mt_flce_fused(const void* X, const void* W, int64_t T, int64_t H, int64_t V,
                   int64_t lddw, int accumulate_dW, int64_t chunk_rows, void* workspace,
                   size_t workspace_bytes, mt_stream_t stream) {
   return fused_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid,
-                     grad_loss, grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, false,
+                     grad_loss, grad_stride, loss, lse, dX, lddx, dW, lddw, accumulate_dW, nullptr,
                      chunk_rows, workspace, workspace_bytes, stream);
-}
-
-size_t mt_flce_dw_tiles_bytes(int64_t V, int64_t H) {
-  if (V <= 0 || H <= 0 || V > INT32_MAX || H > INT32_MAX) return 0;
-  return dw_tiles_bytes(V, H);
 }
 
 int mt_flce_fused_tiles(const void* X, const void* W, int64_t T, int64_t H, int64_t V, int64_t ldx,
                         int64_t ldw, int dtype, float softcap, const int32_t* row_index,
                         const int32_t* row_label, int64_t n_valid, const float* grad_loss,
                         int64_t grad_stride, float* loss, float* lse, void* dX, int64_t lddx,
-                        float* dW_tiles, size_t dw_tiles_bytes_, int64_t chunk_rows,
-                        void* workspace, size_t workspace_bytes, mt_stream_t stream) {
-  if (H > 0 && V > 0 && dw_tiles_bytes_ < dw_tiles_bytes(V, H))
-    return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles %zu bytes < mt_flce_dw_tiles_bytes = %zu",
-                dw_tiles_bytes_, dw_tiles_bytes(V, H));
+                        void* dW_lo, size_t dw_lo_bytes_, float* dW_hi, size_t dw_hi_bytes_,
+                        int accumulate_dW, int64_t chunk_rows, void* workspace,
+                        size_t workspace_bytes, mt_stream_t stream) {
+  TiledDw td;
+  MT_TRY(tiled_args(V, H, dW_lo, dw_lo_bytes_, dW_hi, dw_hi_bytes_, td));
   return fused_entry(X, W, T, H, V, ldx, ldw, dtype, softcap, row_index, row_label, n_valid,
-                     grad_loss, grad_stride, loss, lse, dX, lddx, dW_tiles, 0, 0, true, chunk_rows,
-                     workspace, workspace_bytes, stream);
+                     grad_loss, grad_stride, loss, lse, dX, lddx, td.lo, 0, accumulate_dW ? 1 : 0, &td,
+                     chunk_rows, workspace, workspace_bytes, stream);
 }
 
 int mt_segment_sum(const float* loss, const int64_t* target, int64_t T, int64_t ignore_index,
@@ -1757,41 +1857,23 @@ int mt_flce_scale_grads(const float* scale, void* dX, int64_t T, int64_t H, int6
   return MT_OK;
 }
 
-int mt_flce_narrow_tiles(const float* scale, const float* dW_tiles, size_t dw_tiles_bytes_,
-                         int64_t V, int64_t H, void* dW_out, int64_t ldo, int dtype_out,
-                         mt_stream_t stream) {
-  if (dtype_out != MT_DTYPE_BF16)
-    return fail(MT_ERR_UNSUPPORTED, "tiled dW narrows to bf16 only (dtype_out %d)", dtype_out);
-  if (V <= 0 || H <= 0 || V > INT32_MAX || H > INT32_MAX)
-    return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes H=%lld V=%lld", (long long)H, (long long)V);
+int mt_flce_narrow_tiles(const float* scale, void* dW_lo, size_t dw_lo_bytes_, const float* dW_hi,
+                         size_t dw_hi_bytes_, int64_t V, int64_t H, mt_stream_t stream) {
+  if (!scale) return fail(MT_ERR_INVALID_ARGUMENT, "null scale");
+  TiledDw td;
+  MT_TRY(tiled_args(V, H, dW_lo, dw_lo_bytes_, const_cast<float*>(dW_hi), dw_hi_bytes_, td));
   if (H % 8 != 0) return fail(MT_ERR_UNSUPPORTED, "tiled dW narrowing needs H %% 8 == 0 (H=%lld)", (long long)H);
-  if (!scale || !dW_tiles || !dW_out) return fail(MT_ERR_INVALID_ARGUMENT, "null pointer argument");
-  if (dw_tiles_bytes_ < dw_tiles_bytes(V, H))
-    return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles %zu bytes < mt_flce_dw_tiles_bytes = %zu",
-                dw_tiles_bytes_, dw_tiles_bytes(V, H));
-  if (ldo < H || ldo > (int64_t)1 << 22 || (ldo * 2) % 16 != 0)
-    return fail(MT_ERR_INVALID_ARGUMENT, "ldo=%lld: needs H <= ldo <= 2^22, 16-byte row pitch", (long long)ldo);
-  if ((reinterpret_cast<uintptr_t>(dW_tiles) | reinterpret_cast<uintptr_t>(dW_out)) % 16 != 0)
-    return fail(MT_ERR_INVALID_ARGUMENT, "dW_tiles and dW_out must be 16-byte aligned");
   const int64_t tn = cdiv(H, 256), vt = cdiv(V, 256);
-  const char *t0 = static_cast<const char*>(static_cast<const void*>(dW_tiles)),
-             *t1 = t0 + dw_tiles_bytes(V, H);
-  const char *o0 = static_cast<const char*>(dW_out), *o1 = o0 + ((V - 1) * ldo + H) * 2;
-  const bool inplace = o0 == t0;
-  if (inplace && ldo > tn * 256)
-    return fail(MT_ERR_INVALID_ARGUMENT, "in-place narrowing needs ldo <= round_up(H, 256)");
-  if (!inplace && o0 < t1 && t0 < o1)
-    return fail(MT_ERR_INVALID_ARGUMENT, "dW_out partially overlaps dW_tiles");
   hipStream_t s = (hipStream_t)stream;
-  const float* tiles = dW_tiles + dw_tiles_pad(H);
   const int p = prof_begin("narrow_tiles_kernel<dW>", 0, (double)V * H * 6, s);
-  // in place: tile rows {0}, {1}, [2, 4), ... one launch each (the bf16
-  // rows of tile row r end where tile row r / 2 starts); else one launch
-  for (int64_t lo = 0, hi = inplace ? 1 : vt; lo < vt; lo = hi, hi = std::max<int64_t>(2 * lo, lo + 1)) {
+  // in place into dW_lo (pitch H): tile rows {0}, {1}, [2, 4), ... one
+  // launch each (the bf16 rows of tile row r end where tile row r / 2
+  // starts); the rows held in dW_hi are never overwritten
+  for (int64_t lo = 0, hi = 1; lo < vt; lo = hi, hi = std::max<int64_t>(2 * lo, lo + 1)) {
     const int64_t r1 = std::min(hi, vt);
     hipLaunchKernelGGL(narrow_tiles_kernel, dim3((uint32_t)((r1 - lo) * tn)), dim3(kThreadsBf), 0, s,
-                       scale, tiles, (int32_t)lo, (int32_t)tn, (int32_t)V, (int32_t)H,
-                       static_cast<char*>(dW_out), ldo * 2);
+                       scale, td.lo + dw_tiles_pad(H), td.hi, td.lo_rows, (int32_t)lo, (int32_t)tn,
+                       (int32_t)V, (int32_t)H, static_cast<char*>(dW_lo), H * 2);
     MT_TRY(check_launch("narrow_tiles_kernel"));
   }
   prof_end(p, s);

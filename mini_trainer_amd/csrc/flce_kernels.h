@@ -588,12 +588,15 @@ struct DwArgs {
   // kQueueWords counters, zero at launch, one per XCD's share of the tiles
   uint32_t* queue = nullptr;
   // tiled (bf16): dW in the library's tile order instead of rows of pitch
-  // lddw: tile (tm, tn) at floats tile_pad + (tm tiles_n + tn) 65536, tm
-  // counted from vocabulary row 0 (the block's tile rows start at v0 / 256,
-  // v0 a multiple of 256), wave w's fragment (fm, fn) at
-  // ((w 64 + fm 8 + fn) 64 + lane) 4 within it
+  // lddw, over two buffers: tile (tm, tn) at floats tile_pad + (tm tiles_n
+  // + tn) 65536 from dW for tm < lo_rows, else at ((tm - lo_rows) tiles_n +
+  // tn) 65536 from dW_hi; tm counted from vocabulary row 0 (the block's tile
+  // rows start at v0 / 256, v0 a multiple of 256), wave w's fragment (fm,
+  // fn) at ((w 64 + fm 8 + fn) 64 + lane) 4 within the tile
   int32_t tiled = 0;
   int64_t tile_pad = 0;
+  float* dW_hi = nullptr;
+  int32_t lo_rows = 0;
   // narrow (bf16, a dW every tile completes in one pass): dW is bf16 rows of
   // pitch lddw elements, each tile narrowed in its epilogue (kDwNarrow)
   int32_t narrow = 0;

@@ -663,8 +663,10 @@ __device__ __forceinline__ DwTile dw_tile(const DwArgs& a, int32_t m0, int32_t h
 // one contiguous KiB per instruction -- no transpose, no bounds (the tile
 // grid is padded; rows past V and columns past H are never read back).
 __device__ __forceinline__ rsrc_t dw_tiled_rsrc(const DwArgs& a, int32_t m0, int32_t h0) {
-  const int64_t tile = (int64_t)((a.v0 + m0) / 256) * a.tiles_n + h0 / 256;
-  return make_rsrc(a.dW + a.tile_pad + tile * 65536, 262144u);
+  const int32_t tm = (a.v0 + m0) / 256;
+  const float* base = tm < a.lo_rows ? a.dW + a.tile_pad + (int64_t)tm * a.tiles_n * 65536
+                                     : a.dW_hi + (int64_t)(tm - a.lo_rows) * a.tiles_n * 65536;
+  return make_rsrc(base + (int64_t)(h0 / 256) * 65536, 262144u);
 }
 __device__ __forceinline__ uint32_t dw_tiled_off(const EpiCoordsBf& ec, int fm, int fn) {
   return ((((ec.wm * 2u + ec.wn) * 64u + (uint32_t)fm * 8u + (uint32_t)fn) * 64u) + ec.lane) * 16u;
@@ -1071,15 +1073,17 @@ MT_GEMM_BF16_KERNEL void dx_dw_bf16_kernel(DxArgs x, DwArgs w, uint32_t dx_block
     dw_bf16_body<kQueue, kOut>(lds, w, blockIdx.x - dx_blocks, gridDim.x - dx_blocks);
 }
 
-// Tiled fp32 dW (dw_bf16_kernel<*, true>) times *scale, narrowed to bf16 rows
-// of pitch ldo_b bytes at `out` (V rows, H columns, H a multiple of 8): one
+// Tiled fp32 dW (dw_bf16_kernel<*, true>: tile rows [0, lo_rows) from
+// tiles_lo, the rest from tiles_hi) times *scale, narrowed to bf16 rows of
+// pitch ldo_b bytes at `out` (V rows, H columns, H a multiple of 8): one
 // workgroup per tile of tile rows tr0, tr0 + 1, ... (gridDim.x / tiles_n of
 // them).  Each lane reads its fragment pairs (fn = 2p, 2p + 1) as contiguous
 // KiB and, after one v_permlane16_swap per dword (the pairing the forward
 // uses for its chunk of exponentials), writes 8 consecutive columns.  The
 // output resource of a tile ends at its last element; lanes outside the
 // tile (rows past V, columns past H) get an offset past that end.
-__global__ __launch_bounds__(256) void narrow_tiles_kernel(const float* scale, const float* tiles,
+__global__ __launch_bounds__(256) void narrow_tiles_kernel(const float* scale, const float* tiles_lo,
+                                                           const float* tiles_hi, int32_t lo_rows,
                                                            int32_t tr0, int32_t tiles_n, int32_t V,
                                                            int32_t H, char* out, int64_t ldo_b) {
   const int32_t tile = tr0 * tiles_n + (int32_t)blockIdx.x;
@@ -1087,7 +1091,9 @@ __global__ __launch_bounds__(256) void narrow_tiles_kernel(const float* scale, c
   const uint32_t rows = (uint32_t)min(256, V - tm * 256), cols = (uint32_t)min(256, H - tn * 256);
   const float sc = *scale;
   const EpiCoordsBf ec;
-  const rsrc_t src = make_rsrc(tiles + (int64_t)tile * 65536, 262144u);
+  const float* tsrc = tm < lo_rows ? tiles_lo + (int64_t)tile * 65536
+                                   : tiles_hi + ((int64_t)(tm - lo_rows) * tiles_n + tn) * 65536;
+  const rsrc_t src = make_rsrc(tsrc, 262144u);
   const rsrc_t dst = make_rsrc(out + (int64_t)tm * 256 * ldo_b + (int64_t)tn * 512,
                                (rows - 1u) * (uint32_t)ldo_b + cols * 2u);
   const uint32_t q = ec.lane >> 4;

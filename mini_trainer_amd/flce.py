@@ -122,6 +122,13 @@ def backward_plan(T: int, n_valid: int, H: int, V: int, dtype: torch.dtype,
     return c.value, cv.value, ws.value
 
 
+def _default_budget(T: int, V: int, es: int) -> int:
+    """The workspace budget the planners use when given 0: the override in
+    MT_FLCE_BWD_BUDGET_BYTES, else 5% of the T x V logits in bytes."""
+    env = int(os.environ.get(BACKWARD_BUDGET_ENV, "0"))
+    return env if env > 0 else int(float(T) * V * es * 0.05)
+
+
 def _grad_vector(grad: torch.Tensor, T: int) -> Tuple[torch.Tensor, int]:
     g = grad.reshape(-1) if grad.dim() != 1 else grad
     if g.dtype != torch.float32:
@@ -158,6 +165,37 @@ def _check_inputs(hidden, weight, target):
     return X, W, T, H, V, dt
 
 
+class _TiledDw:
+    """The tiled fp32 weight gradient of mt_flce_fused_tiles /
+    mt_flce_backward_tiles in the two buffers of mt_flce_dw_tiles_layout:
+    `lo` is the bf16 [V, H] tensor the gradient is narrowed into in place
+    (it holds the first tile rows until then), `hi` the other tile rows,
+    dropped once narrowed -- so the weight gradient handed to autograd owns
+    exactly V * H * 2 bytes."""
+
+    def __init__(self, V: int, H: int, device: torch.device):
+        lib = load()
+        lo_b, rows, hi_b = ctypes.c_size_t(), ctypes.c_int64(), ctypes.c_size_t()
+        check(lib.mt_flce_dw_tiles_layout(V, H, ctypes.byref(lo_b), ctypes.byref(rows),
+                                          ctypes.byref(hi_b)), "mt_flce_dw_tiles_layout")
+        self.V, self.H = V, H
+        self.lo = torch.empty((V, H), dtype=torch.bfloat16, device=device)
+        self.hi = torch.empty(hi_b.value // 4, dtype=torch.float32, device=device)
+
+    def args(self) -> tuple:
+        """(lo, lo bytes, hi, hi bytes) as the C ABI takes them."""
+        return (_p(self.lo), self.lo.numel() * 2, _p(self.hi), self.hi.numel() * 4)
+
+    def narrow(self, scale: torch.Tensor) -> torch.Tensor:
+        """scale * the gradient in bf16, in place in `lo` (mt_flce_narrow_tiles);
+        `hi` is released (the caching allocator reuses it only after the
+        narrowing, on the same stream)."""
+        check(load().mt_flce_narrow_tiles(_p(scale), *self.args(), self.V, self.H,
+                                          _stream(self.lo.device)), "mt_flce_narrow_tiles")
+        self.hi = None
+        return self.lo
+
+
 class _FusedLinearCrossEntropyNone(torch.autograd.Function):
     """Per-token loss; three paths over the same arithmetic (ctx.path).
 
@@ -187,86 +225,130 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
                 scaling give; mt_flce_scale_grads for dX and
                 mt_flce_narrow_tiles for dW read it on the device), and
                 otherwise recomputes with the saved lse (the general path's
-                bf16 backward into the tiles' allocation), exact for any
-                per-token gradient.
+                bf16 backward into the same weight-gradient buffers), exact
+                for any per-token gradient.
+
+    `ranges` (row ranges [t0, t1) of X, each within one buffer's reach, in
+    order) splits a large call: every range is compacted, run and (in the
+    backward) recomputed on its own, into one dX and one weight gradient --
+    dW of a later range adds into the tiles (or dw_accumulator) the earlier
+    ones filled, so one weight-sized buffer serves the whole call.
     """
 
     @staticmethod
     def forward(ctx, hidden, weight, target, ignore_index, softcap, shift, dw_accumulator,
-                grad_scale, allow_unit):
+                grad_scale, allow_unit, ranges):
         X, W, T, H, V, dt = _check_inputs(hidden, weight, target)
         lib = load()
         dev = X.device
-        row_index, row_label, n = prepare_targets(target, V, ignore_index, shift)
+        tgt = target.reshape(-1)
+        if ranges is None:
+            ranges = [(0, T)]
+        parts = []  # (t0, t1, row_index, row_label, n) per range
+        for t0, t1 in ranges:
+            ri, rl, n = prepare_targets(tgt[t0:t1], V, ignore_index, shift)
+            parts.append((t0, t1, ri, rl, n))
+        n_tot = sum(p[4] for p in parts)
         loss = torch.empty(T, dtype=torch.float32, device=dev)
-        lse = torch.empty(n, dtype=torch.float32, device=dev)
         ctx.path = "general"
-        if dt == MT_DTYPE_BF16 and n > 0 and (grad_scale is not None or allow_unit):
-            C, ws_bytes, pays = fused_plan(T, n, H, V)
-            if C > 0 and _use_fused(pays):  # C = 0: the fused path cannot run this shape
+        ctx.ranges = [(p[0], p[1], p[4]) for p in parts]
+        plans = None
+        if dt == MT_DTYPE_BF16 and n_tot > 0 and (grad_scale is not None or allow_unit):
+            plans = [fused_plan(t1 - t0, n, H, V, accumulator=dw_accumulator is not None)
+                     if n > 0 else (0, 0, True) for t0, t1, _, _, n in parts]
+            live = [pl for pl, p in zip(plans, parts) if p[4] > 0]
+            # C = 0: the fused path cannot run that shape
+            if all(pl[0] > 0 for pl in live) and _use_fused(all(pl[2] for pl in live)):
                 ctx.path = "fused" if grad_scale is not None else "fused_unit"
         ctx.dw_accumulator = dw_accumulator
+        ctx.meta = (float(softcap), hidden.shape, dt)
+        lses = []
         if ctx.path != "general":
             if ctx.path == "fused":
                 g, gstride = _promised_grad(grad_scale, T, dev)
             else:
                 g, gstride = torch.ones(1, dtype=torch.float32, device=dev), 0
             dX = torch.empty((T, H), dtype=X.dtype, device=dev)
-            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-            if dw_accumulator is not None:
-                dW = dw_accumulator
-                check(lib.mt_flce_fused(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
-                                        float(softcap), _p(row_index), _p(row_label), n, _p(g),
-                                        gstride, _p(loss), _p(lse), _p(dX), dX.stride(0), _p(dW),
-                                        dW.stride(0), 1, C, _p(ws), ws_bytes, _stream(dev)),
-                      "mt_flce_fused")
-            else:
-                # dW as 256 x 256 tiles (mt_flce_dw_tiles_bytes), narrowed into
-                # the weight's dtype at the start of the same allocation later
-                tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
-                dW = torch.empty(tb // 4, dtype=torch.float32, device=dev)
-                check(lib.mt_flce_fused_tiles(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0),
-                                              dt, float(softcap), _p(row_index), _p(row_label),
-                                              n, _p(g), gstride, _p(loss), _p(lse), _p(dX),
-                                              dX.stride(0), _p(dW), tb, C, _p(ws), ws_bytes,
-                                              _stream(dev)), "mt_flce_fused_tiles")
-            del ws
+            dW = dw_accumulator if dw_accumulator is not None else _TiledDw(V, H, dev)
+            for r, ((t0, t1, ri, rl, n), (C, ws_bytes, _)) in enumerate(zip(parts, plans)):
+                ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+                lse = torch.empty(n, dtype=torch.float32, device=dev)
+                Xr, gr = X[t0:t1], (g[t0:t1] if gstride else g)
+                dXr, lr = dX[t0:t1], loss[t0:t1]
+                if dw_accumulator is not None:
+                    check(lib.mt_flce_fused(_p(Xr), _p(W), t1 - t0, H, V, X.stride(0),
+                                            W.stride(0), dt, float(softcap), _p(ri), _p(rl), n,
+                                            _p(gr), gstride, _p(lr), _p(lse), _p(dXr),
+                                            dX.stride(0), _p(dW), dW.stride(0), 1, C, _p(ws),
+                                            ws_bytes, _stream(dev)), "mt_flce_fused")
+                else:
+                    # dW as 256 x 256 tiles in the weight gradient's own bf16
+                    # buffer and a second one, narrowed into the first later
+                    check(lib.mt_flce_fused_tiles(_p(Xr), _p(W), t1 - t0, H, V, X.stride(0),
+                                                  W.stride(0), dt, float(softcap), _p(ri), _p(rl),
+                                                  n, _p(gr), gstride, _p(lr), _p(lse), _p(dXr),
+                                                  dX.stride(0), *dW.args(), int(r > 0), C,
+                                                  _p(ws), ws_bytes, _stream(dev)),
+                          "mt_flce_fused_tiles")
+                del ws
+                lses.append(lse)
             if ctx.path == "fused":
-                ctx.save_for_backward(row_index, g)
+                ctx.save_for_backward(g, *[p[2] for p in parts])
+                ctx.gstride = gstride
             else:  # kept for the recompute fallback of a per-token gradient
-                ctx.save_for_backward(X, W, row_index, row_label, lse)
-            ctx.meta = (n, gstride, hidden.shape, float(softcap), dt)
-            ctx.w_dtype = weight.dtype
+                ctx.save_for_backward(X, W, *[t for p, lse in zip(parts, lses)
+                                              for t in (p[2], p[3], lse)])
             ctx.w_shape = (V, H)
             ctx.dX = dX
             ctx.dW = None if dw_accumulator is not None else dW
             ctx.fused_consumed = False
             return loss.view(hidden.shape[:-1])
-        ws_bytes = lib.mt_flce_forward_workspace_bytes(T, n, H, V, dt)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         ctx.keep = None
-        plan = None
-        if dt == MT_DTYPE_BF16 and allow_unit and float(softcap) == 0.0 and n > 0:
-            plan = backward_plan(T, n, H, V, X.dtype, narrow=True)
-        if plan is not None and plan[0] >= n and plan[1] < V:
-            # one row block in the backward: this forward keeps the first
-            # vocabulary block's exponentials in that backward's G block
-            C, Cv, bws_bytes = plan
-            bws = torch.empty(bws_bytes, dtype=torch.uint8, device=dev)
-            guard = torch.empty(1, dtype=torch.int32, device=dev)
-            check(lib.mt_flce_forward_keep(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
-                                           0.0, _p(row_index), _p(row_label), n, _p(loss),
-                                           _p(lse), _p(ws), ws_bytes, _p(bws), Cv, bws_bytes,
-                                           _p(guard), _stream(dev)), "mt_flce_forward_keep")
-            ctx.keep = (C, Cv, bws, guard)
-        else:
-            check(lib.mt_flce_forward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
-                                      float(softcap), _p(row_index), _p(row_label), n, _p(loss),
-                                      _p(lse), _p(ws), ws_bytes, _stream(dev)), "mt_flce_forward")
-        del ws
-        ctx.save_for_backward(X, W, row_index, row_label, lse)
-        ctx.meta = (n, float(softcap), hidden.shape, dt)
+        for t0, t1, ri, rl, n in parts:
+            lse = torch.empty(n, dtype=torch.float32, device=dev)
+            lses.append(lse)
+            Xr, lr = X[t0:t1], loss[t0:t1]
+            plan = None
+            ws_bytes = lib.mt_flce_forward_workspace_bytes(t1 - t0, n, H, V, dt)
+            if (dt == MT_DTYPE_BF16 and allow_unit and float(softcap) == 0.0 and n > 0
+                    and len(parts) == 1):
+                # the kept block sits beside the forward's own workspace: plan
+                # it under what the budget leaves of that
+                left = _default_budget(T, V, 2) - ws_bytes
+                if left > 0:
+                    plan = backward_plan(T, n, H, V, X.dtype, budget_bytes=left, narrow=True)
+            if plan is not None and plan[0] >= n and plan[1] < V:
+                # one row block in the backward: the forward keeps the first
+                # vocabulary block's exponentials in that backward's G block,
+                # which lives from here to the backward (or until the loss's
+                # graph is freed, when no backward follows)
+                C, Cv, bws_bytes = plan
+                bws = torch.empty(bws_bytes, dtype=torch.uint8, device=dev)
+                guard = torch.empty(1, dtype=torch.int32, device=dev)
+                ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+                check(lib.mt_flce_forward_keep(_p(Xr), _p(W), t1 - t0, H, V, X.stride(0),
+                                               W.stride(0), dt, 0.0, _p(ri), _p(rl), n, _p(lr),
+                                               _p(lse), _p(ws), ws_bytes, _p(bws), Cv, bws_bytes,
+                                               _p(guard), _stream(dev)), "mt_flce_forward_keep")
+                ctx.keep = (C, Cv, bws, guard)
+            else:
+                ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+                check(lib.mt_flce_forward(_p(Xr), _p(W), t1 - t0, H, V, X.stride(0), W.stride(0),
+                                          dt, float(softcap), _p(ri), _p(rl), n, _p(lr), _p(lse),
+                                          _p(ws), ws_bytes, _stream(dev)), "mt_flce_forward")
+            del ws
+        ctx.save_for_backward(X, W, *[t for p, lse in zip(parts, lses) for t in (p[2], p[3], lse)])
         return loss.view(hidden.shape[:-1])
+
+    @staticmethod
+    def _range_tensors(ctx):
+        """X, W and [(t0, t1, n, row_index, row_label, lse)] per range."""
+        saved = ctx.saved_tensors
+        X, W, rest = saved[0], saved[1], saved[2:]
+        out = []
+        for i, (t0, t1, n) in enumerate(ctx.ranges):
+            out.append((t0, t1, n, rest[3 * i], rest[3 * i + 1], rest[3 * i + 2]))
+        return X, W, out
 
     @staticmethod
     def backward(ctx, grad_loss):
@@ -274,11 +356,11 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
             return _FusedLinearCrossEntropyNone._backward_fused(ctx, grad_loss)
         if ctx.path == "fused_unit":
             return _FusedLinearCrossEntropyNone._backward_fused_unit(ctx, grad_loss)
-        X, W, row_index, row_label, lse = ctx.saved_tensors
-        n, softcap, hshape, dt = ctx.meta
+        X, W, rngs = _FusedLinearCrossEntropyNone._range_tensors(ctx)
+        softcap, hshape, dt = ctx.meta
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         acc = ctx.dw_accumulator
-        none = (None,) * 7
+        none = (None,) * 8
         if not need_x and not need_w and acc is None:
             return (None, None) + none
         lib = load()
@@ -288,42 +370,44 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         g, gstride = _grad_vector(grad_loss, T)
         dX = torch.empty((T, H), dtype=X.dtype, device=dev)
         if acc is None and dt == MT_DTYPE_BF16:
-            # dW in bf16 inside an allocation of the fp32 tiles' size; the
-            # first backward takes the exponentials its forward kept
+            # dW in bf16; the first backward takes the exponentials its
+            # forward kept
             keep, ctx.keep = getattr(ctx, "keep", None), None
-            grad_w = _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride,
-                                           softcap, dX, keep=keep)
+            grad_w = _backward_bf16_weight(lib, X, W, rngs, g, gstride, softcap, dX, keep=keep)
             grad_w = grad_w if need_w else None
         else:
-            C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype)
-            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-            if acc is not None:
-                dW, accumulate = acc, 1
-            else:
-                dW, accumulate = torch.empty((V, H), dtype=torch.float32, device=dev), 0
-            check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0), dt,
-                                       softcap, _p(row_index), _p(row_label), n, _p(lse), _p(g),
-                                       gstride, _p(dX), dX.stride(0), _p(dW), dW.stride(0),
-                                       accumulate, C, Cv, _p(ws), ws_bytes, _stream(dev)),
-                  "mt_flce_backward")
-            del ws
+            dW = acc if acc is not None else torch.empty((V, H), dtype=torch.float32, device=dev)
+            for r, (t0, t1, n, ri, rl, lse) in enumerate(rngs):
+                C, Cv, ws_bytes = backward_plan(t1 - t0, n, H, V, X.dtype)
+                ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+                gr = g[t0:t1] if gstride else g
+                check(lib.mt_flce_backward(_p(X[t0:t1]), _p(W), t1 - t0, H, V, X.stride(0),
+                                           W.stride(0), dt, softcap, _p(ri), _p(rl), n, _p(lse),
+                                           _p(gr), gstride, _p(dX[t0:t1]), dX.stride(0), _p(dW),
+                                           dW.stride(0), int(acc is not None or r > 0), C, Cv,
+                                           _p(ws), ws_bytes, _stream(dev)), "mt_flce_backward")
+                del ws
             grad_w = _weight_grad_in_dtype(dW, W.dtype) if (need_w and acc is None) else None
         grad_x = dX.view(hshape) if need_x else None
         return (grad_x, grad_w) + none
 
     @staticmethod
     def _backward_fused(ctx, grad_loss):
-        row_index, g = ctx.saved_tensors
-        n, gstride, hshape, _, _ = ctx.meta
-        T = row_index.numel()
-        if n > 0:
-            gl = grad_loss.reshape(-1)
-            if gl.numel() == 1:
-                gl = gl.expand(T)
+        saved = ctx.saved_tensors
+        g, ris = saved[0], saved[1:]
+        gstride = ctx.gstride
+        _, hshape, _ = ctx.meta
+        T = sum(t1 - t0 for t0, t1, _ in ctx.ranges)
+        gl = grad_loss.reshape(-1)
+        if gl.numel() == 1:
+            gl = gl.expand(T)
+        for (t0, t1, n), ri in zip(ctx.ranges, ris):
+            if n == 0:
+                continue
             if gl.stride(0) == 0 and gstride == 0:  # one scalar against one scalar
                 got, want = gl[:1].float(), g
             else:
-                valid = row_index[:n].long()
+                valid = ri[:n].long() + t0
                 got, want = gl[valid].float(), (g.expand(n) if gstride == 0 else g[valid])
             if not _within_promise(got, want):
                 raise RuntimeError(
@@ -343,15 +427,13 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         grad_x = dX.view(hshape) if ctx.needs_input_grad[0] else None
         grad_w = None
         if ctx.needs_input_grad[1] and dW is not None:
-            one = torch.ones(1, dtype=torch.float32, device=dW.device)
-            grad_w = _tiles_in_dtype(dW, ctx.w_shape, one)
-        return (grad_x, grad_w) + (None,) * 7
-
+            grad_w = dW.narrow(torch.ones(1, dtype=torch.float32, device=dX.device))
+        return (grad_x, grad_w) + (None,) * 8
 
     @staticmethod
     def _backward_fused_unit(ctx, grad_loss):
-        X, W, row_index, row_label, lse = ctx.saved_tensors
-        n, _, hshape, softcap, dt = ctx.meta
+        X, W, rngs = _FusedLinearCrossEntropyNone._range_tensors(ctx)
+        softcap, hshape, dt = ctx.meta
         if ctx.fused_consumed:
             raise RuntimeError(
                 "the fused path formed dX and dW once, at the forward, and has already handed "
@@ -362,30 +444,27 @@ class _FusedLinearCrossEntropyNone(torch.autograd.Function):
         ctx.dX = ctx.dW = None
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         T, H = X.shape
-        V = W.shape[0]
         dev = X.device
         lib = load()
         g, gstride = _grad_vector(grad_loss, T)
         if gstride == 0:
             # one upstream scalar for every token: rescale the unit-gradient
             # dX in place and narrow the tiled dW, times the scalar, into the
-            # weight's dtype at the start of its own allocation
+            # weight gradient's own bf16 buffer
             scale = g.reshape(-1)[:1]
             if need_x:
                 check(lib.mt_flce_scale_grads(_p(scale), _p(dX), T, H, dX.stride(0), dt, None, 0,
                                               H, None, H, _dtype_code(W.dtype), _stream(dev)),
                       "mt_flce_scale_grads")
-            dW_out = _tiles_in_dtype(dW, (V, H), scale) if need_w else None
+            dW_out = dW.narrow(scale) if need_w else None
             del dW
         else:
             # a per-token gradient: the unit-gradient results cannot be
             # rescaled; recompute into the same buffers
-            dW_out = _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride,
-                                           softcap, dX, dW)
-            dW_out = dW_out if need_w else None
+            dW_out = _backward_bf16_weight(lib, X, W, rngs, g, gstride, softcap, dX, dW)
         grad_x = dX.view(hshape) if need_x else None
         grad_w = dW_out if need_w else None
-        return (grad_x, grad_w) + (None,) * 7
+        return (grad_x, grad_w) + (None,) * 8
 
 
 def _narrowed_view(dW: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
@@ -401,72 +480,63 @@ def _narrowed_view(dW: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return out
 
 
-def _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX, C, Cv, ws,
-                    dWt: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """mt_flce_backward_tiles (bf16) into dWt, or into a new tiles buffer of
-    mt_flce_dw_tiles_bytes; returns the buffer."""
-    T, H = X.shape
-    V = W.shape[0]
-    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
-    if dWt is None:
-        dWt = torch.empty(tb // 4, dtype=torch.float32, device=X.device)
-    check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0),
-                                     MT_DTYPE_BF16, softcap, _p(row_index), _p(row_label), n,
-                                     _p(lse), _p(g), gstride, _p(dX), dX.stride(0), _p(dWt),
-                                     dWt.numel() * 4, C, Cv, _p(ws), ws.numel(),
-                                     _stream(X.device)), "mt_flce_backward_tiles")
-    return dWt
-
-
-def _backward_bf16_weight(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX,
-                          dWt: Optional[torch.Tensor] = None, keep=None) -> torch.Tensor:
+def _backward_bf16_weight(lib, X, W, rngs, g, gstride, softcap, dX,
+                          dWt: Optional[_TiledDw] = None, keep=None) -> torch.Tensor:
     """The bf16 backward into dX and a weight gradient in bf16 (nothing
-    added into), as the contiguous [V, H] at the start of dWt (an fp32
-    allocation of mt_flce_dw_tiles_bytes; a new one if None): one row block
-    through mt_flce_backward_narrow when its plan says so, else the tiles and
-    the narrowing pass.  keep = (C, Cv, workspace, guard) of a forward that
-    kept the first vocabulary block's exponentials in that workspace
+    added into), returned as a bf16 [V, H] tensor of its own size: one row
+    block through mt_flce_backward_narrow when its plan says so (one range),
+    else tiles (dWt's buffers, or new ones; every range adding into them)
+    and the narrowing pass.  rngs: [(t0, t1, n, row_index, row_label, lse)]
+    per row range.  keep = (C, Cv, workspace, guard) of a forward that kept
+    the first vocabulary block's exponentials in that workspace
     (mt_flce_forward_keep): its plan and workspace are used."""
     T, H = X.shape
     V = W.shape[0]
+    dev = X.device
     guard = None
-    if keep is not None:
-        C, Cv, ws, guard = keep
-    else:
-        C, Cv, ws_bytes = backward_plan(T, n, H, V, X.dtype, narrow=True)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=X.device)
-    if C < n:
-        dWt = _backward_tiles(lib, X, W, row_index, row_label, n, lse, g, gstride, softcap, dX, C,
-                              Cv, ws, dWt)
-        del ws
-        return _tiles_in_dtype(dWt, (V, H), torch.ones(1, device=X.device))
-    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    one = len(rngs) == 1
+    if one:
+        n = rngs[0][2]
+        plan = keep[:3] if keep is not None else backward_plan(T, n, H, V, X.dtype, narrow=True)
+    if one and plan[0] >= n:
+        (t0, t1, n, ri, rl, lse), (C, Cv, ws) = rngs[0], plan
+        if keep is not None:
+            guard = keep[3]
+        else:
+            ws = torch.empty(ws, dtype=torch.uint8, device=dev)
+        out = dWt.lo if dWt is not None else torch.empty((V, H), dtype=torch.bfloat16, device=dev)
+        need = int(lib.mt_flce_narrow_scratch_bytes(V, H, C))
+        if dWt is not None and dWt.hi is not None and dWt.hi.numel() * 4 >= need:
+            scratch = dWt.hi
+        else:
+            scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+        nbytes = scratch.numel() * scratch.element_size()
+        check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0),
+                                          MT_DTYPE_BF16, softcap, _p(ri), _p(rl), n, _p(lse),
+                                          _p(g), gstride, _p(dX), dX.stride(0), _p(out),
+                                          out.numel() * 2, _p(scratch), nbytes, C, Cv, _p(ws),
+                                          ws.numel(), _p(guard), _stream(dev)),
+              "mt_flce_backward_narrow")
+        del ws, scratch
+        if dWt is not None:
+            dWt.hi = None
+        return out
     if dWt is None:
-        dWt = torch.empty(tb // 4, dtype=torch.float32, device=X.device)
-    check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, X.stride(0), W.stride(0),
-                                      MT_DTYPE_BF16, softcap, _p(row_index), _p(row_label), n,
-                                      _p(lse), _p(g), gstride, _p(dX), dX.stride(0), _p(dWt),
-                                      dWt.numel() * 4, C, Cv, _p(ws), ws.numel(), _p(guard),
-                                      _stream(X.device)), "mt_flce_backward_narrow")
-    del ws
-    out = torch.empty(0, dtype=torch.bfloat16, device=dWt.device)
-    # storage offsets count elements: one fp32 element is two 16-bit ones
-    out.set_(dWt.untyped_storage(), 2 * dWt.storage_offset(), (V, H), (H, 1))
-    return out
-
-
-def _tiles_in_dtype(dWt: torch.Tensor, shape: Tuple[int, int],
-                    scale: torch.Tensor) -> torch.Tensor:
-    """scale * the tiled fp32 weight gradient (mt_flce_fused_tiles) as the
-    contiguous bf16 [V, H] that mt_flce_narrow_tiles writes at the start of
-    the tiles' own allocation."""
-    V, H = shape
-    check(load().mt_flce_narrow_tiles(_p(scale), _p(dWt), dWt.numel() * 4, V, H, _p(dWt), H,
-                                      MT_DTYPE_BF16, _stream(dWt.device)), "mt_flce_narrow_tiles")
-    out = torch.empty(0, dtype=torch.bfloat16, device=dWt.device)
-    # storage offsets count elements: one fp32 element is two 16-bit ones
-    out.set_(dWt.untyped_storage(), 2 * dWt.storage_offset(), (V, H), (H, 1))
-    return out
+        dWt = _TiledDw(V, H, dev)
+    for r, (t0, t1, n, ri, rl, lse) in enumerate(rngs):
+        # one range: the narrowing plan (several row blocks here); more: the
+        # plan of mt_flce_backward_tiles itself (dX's accumulator and X^T in
+        # the workspace)
+        C, Cv, ws_bytes = (plan if one else backward_plan(t1 - t0, n, H, V, X.dtype))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        gr = g[t0:t1] if gstride else g
+        check(lib.mt_flce_backward_tiles(_p(X[t0:t1]), _p(W), t1 - t0, H, V, X.stride(0),
+                                         W.stride(0), MT_DTYPE_BF16, softcap, _p(ri), _p(rl), n,
+                                         _p(lse), _p(gr), gstride, _p(dX[t0:t1]), dX.stride(0),
+                                         *dWt.args(), int(r > 0), C, Cv, _p(ws), ws_bytes,
+                                         _stream(dev)), "mt_flce_backward_tiles")
+        del ws
+    return dWt.narrow(torch.ones(1, dtype=torch.float32, device=dev))
 
 
 def _weight_grad_in_dtype(dW: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
@@ -525,16 +595,19 @@ def profile_report() -> dict:
     return json.loads(buf.value.decode())
 
 
-def fused_plan(T: int, n_valid: int, H: int, V: int,
-               budget_bytes: Optional[int] = None) -> Tuple[int, int, bool]:
+def fused_plan(T: int, n_valid: int, H: int, V: int, budget_bytes: Optional[int] = None,
+               accumulator: bool = False) -> Tuple[int, int, bool]:
     """(chunk_rows, workspace_bytes, pays) of the fused forward + backward
-    (bf16); pays: the planner expects it to beat the general path."""
+    (bf16); pays: the planner expects it to beat the general path that the
+    same call would otherwise take (accumulator: the weight gradient added
+    into an fp32 dw_accumulator; else wanted in bf16, the narrowing plan)."""
     lib = load()
     if budget_bytes is None:
         budget_bytes = int(os.environ.get(BACKWARD_BUDGET_ENV, "0"))
     c, ws, pays = ctypes.c_int64(), ctypes.c_size_t(), ctypes.c_int()
-    check(lib.mt_flce_fused_plan(T, n_valid, H, V, MT_DTYPE_BF16, budget_bytes, ctypes.byref(c),
-                                 ctypes.byref(ws), ctypes.byref(pays)), "mt_flce_fused_plan")
+    check(lib.mt_flce_fused_plan(T, n_valid, H, V, MT_DTYPE_BF16, budget_bytes, int(accumulator),
+                                 ctypes.byref(c), ctypes.byref(ws), ctypes.byref(pays)),
+          "mt_flce_fused_plan")
     return c.value, ws.value, bool(pays.value)
 
 
@@ -629,31 +702,23 @@ def fused_linear_cross_entropy(hidden_states: torch.Tensor, lm_head_weight: torc
         target = torch.nn.functional.pad(target, (0, 1), value=int(ignore_index))[..., 1:]
         shift_labels = False
     # bf16 rows are addressed with 32-bit offsets: X beyond one buffer's
-    # reach (mt_flce_max_buffer_bytes) runs over row ranges; the lm_head
-    # gradient of every range accumulates (autograd, or dw_accumulator)
+    # reach (mt_flce_max_buffer_bytes) runs over row ranges inside one
+    # autograd node, whose lm_head gradient every range adds into
     T = target.numel()
+    ranges = None
     if hidden_states.dtype == torch.bfloat16 and T > 0:
         limit = int(load().mt_flce_max_buffer_bytes())
         pitch = -(-H // 8) * 8 * 2
         rows = max(1, limit // pitch)
         if T > rows:
-            hid = hidden_states.reshape(T, H)
-            tgt = target.reshape(T)
             if shift_labels:
-                tgt = torch.nn.functional.pad(tgt, (0, 1), value=int(ignore_index))[1:]
-            gs = grad_scale
-            parts = []
-            for t0 in range(0, T, rows):
-                t1 = min(T, t0 + rows)
-                g = gs[t0:t1] if isinstance(gs, torch.Tensor) and gs.numel() == T else gs
-                parts.append(_FusedLinearCrossEntropyNone.apply(
-                    hid[t0:t1], lm_head_weight, tgt[t0:t1], int(ignore_index), cap, False,
-                    dw_accumulator, g, allow_unit))
-            return torch.cat(parts).view(hidden_states.shape[:-1])
+                target = torch.nn.functional.pad(target.reshape(T), (0, 1),
+                                                 value=int(ignore_index))[1:]
+                shift_labels = False
+            ranges = [(t0, min(T, t0 + rows)) for t0 in range(0, T, rows)]
     return _FusedLinearCrossEntropyNone.apply(hidden_states, lm_head_weight, target,
                                               int(ignore_index), cap, bool(shift_labels),
-                                              dw_accumulator, grad_scale, allow_unit)
-
+                                              dw_accumulator, grad_scale, allow_unit, ranges)
 
 
 class _CrossEntropyNone(torch.autograd.Function):

@@ -13,6 +13,9 @@ import torch
 
 from .flce import cross_entropy_none, fused_linear_cross_entropy
 
+# The one keyword of **kwargs the drop-in reads (see its docstring).
+GRAD_SCALE_KWARG = "mt_grad_scale"
+
 
 def liger_fixed_fused_linear_cross_entropy_none_reduction(
     hidden_states: torch.Tensor,
@@ -29,14 +32,15 @@ def liger_fixed_fused_linear_cross_entropy_none_reduction(
     ignore_index and softcap=final_logit_softcapping to Liger's fused kernel
     and ignores num_items_in_batch and **kwargs (:9,12).  Returns fp32 [T]
     with +0.0 at ignored positions, differentiable in hidden_states and
-    lm_head_weight.  Of **kwargs only `grad_scale` is read (absent from the
-    reference's callers, so they get the general path): a caller that knows
-    the upstream gradient of the loss before the forward passes it to select
-    the fused path (see flce.fused_linear_cross_entropy).
+    lm_head_weight.  Of **kwargs only `mt_grad_scale` is read (absent from
+    the reference's callers, and named for this package so that no other
+    caller's keyword selects it): a caller that knows the upstream gradient
+    of the loss before the forward passes it to promise that gradient to the
+    fused path (flce.fused_linear_cross_entropy's grad_scale).
     """
     return fused_linear_cross_entropy(hidden_states, lm_head_weight, target,
                                       ignore_index=ignore_index, softcap=final_logit_softcapping,
-                                      grad_scale=kwargs.get("grad_scale"))
+                                      grad_scale=kwargs.get(GRAD_SCALE_KWARG))
 
 
 def hf_fixed_cross_entropy_none_reduction(

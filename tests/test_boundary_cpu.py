@@ -85,3 +85,21 @@ def test_hf_loss_dispatch_reaches_the_patched_function(monkeypatch):
     with pytest.raises(RuntimeError, match="ROCm device"):
         lu.ForCausalLMLoss(logits, labels, vocab_size=11)
     assert seen["args"] == ((6, 11), (6,), -100)
+
+
+def test_drop_in_reads_only_its_own_keyword(monkeypatch):
+    """Of **kwargs the drop-in reads `mt_grad_scale` alone: an unrelated
+    `grad_scale` a caller passes through the loss kwargs selects nothing."""
+    seen = []
+
+    def spy(hidden, weight, target, ignore_index=-100, softcap=None, grad_scale=None, **kw):
+        seen.append((ignore_index, softcap, grad_scale))
+        return "out"
+
+    monkeypatch.setattr(nrl, "fused_linear_cross_entropy", spy)
+    X, W, y = torch.zeros(2, 8), torch.zeros(3, 8), torch.zeros(2, dtype=torch.long)
+    nrl.liger_fixed_fused_linear_cross_entropy_none_reduction(X, W, y, 7, -5, 30.0,
+                                                               grad_scale=0.5)
+    nrl.liger_fixed_fused_linear_cross_entropy_none_reduction(X, W, y, mt_grad_scale=0.25)
+    assert seen == [(-5, 30.0, None), (-100, None, 0.25)]
+    assert nrl.GRAD_SCALE_KWARG == "mt_grad_scale"

@@ -124,51 +124,76 @@ def test_backward_and_misc_host_checks():
     assert lib.mt_ce_forward(None, 4, 10, 5, 1, None, -100, None, None, None, None) == 1
 
 
+def dw_layout(V, H):
+    lib = _lib.load()
+    lo, rows, hi = ctypes.c_size_t(), ctypes.c_int64(), ctypes.c_size_t()
+    st = lib.mt_flce_dw_tiles_layout(V, H, ctypes.byref(lo), ctypes.byref(rows), ctypes.byref(hi))
+    return st, lo.value, rows.value, hi.value
+
+
 def test_dw_tiles_layout_and_host_checks():
-    """Tiled dW: a pad of 256 * round_up(H, 256) bf16 elements, then whole
-    256 x 256 fp32 tiles -- never less than the row-major fp32 [V, H] the
-    same allocation also serves as.  Argument checks return before any
+    """Tiled dW over two buffers: `lo` is exactly the bf16 [V, H] gradient
+    (V H 2 bytes) and holds, after a pad of half a tile row, as many whole
+    tile rows as fit; `hi` holds the rest.  Together they hold at least the
+    fp32 gradient; the narrowing's in-place order is safe (the bf16 rows of
+    tile row r end before tile row floor((r + 1) / 2) starts, and every tile
+    row it writes over comes earlier).  Argument checks return before any
     launch."""
     lib = _lib.load()
-    for V, H in [(100, 64), (256, 256), (65600, 1056), (128256, 4096), (1, 8)]:
-        tb = lib.mt_flce_dw_tiles_bytes(V, H)
-        Hp = -(-H // 256) * 256
-        assert tb == 256 * Hp * 2 + (-(-V // 256)) * (Hp // 256) * 256 * 256 * 4
-        assert tb >= V * H * 4 and tb % 256 == 0
-    assert lib.mt_flce_dw_tiles_bytes(0, 64) == 0 and lib.mt_flce_dw_tiles_bytes(10, -1) == 0
-    tb = lib.mt_flce_dw_tiles_bytes(100, 64)
-    # fused_tiles: a tiles buffer below the layout's size
-    assert lib.mt_flce_fused_tiles(16, 16, 8, 64, 100, 64, 64, 1, 0.0, 16, 16, 4, 16, 0, 16, 16,
-                                   16, 64, 16, tb - 16, 256, 16, 1 << 30, None) == 1
-    assert "mt_flce_dw_tiles_bytes" in lib.mt_flce_last_error().decode()
-    # ... fp32 operands: the fused path is bf16 only
-    assert lib.mt_flce_fused_tiles(16, 16, 8, 64, 100, 64, 64, 0, 0.0, 16, 16, 4, 16, 0, 16, 16,
-                                   16, 64, 16, tb, 256, 16, 1 << 30, None) == 3
-    # backward_tiles: fp32 unsupported, a tiles buffer below the layout's size
+    for V, H in [(100, 64), (256, 256), (65600, 1056), (128256, 4096), (1, 8), (151936, 1536),
+                 (768, 256), (767, 256), (300, 1000)]:
+        st, lo, rows, hi = dw_layout(V, H)
+        assert st == 0 and lo == V * H * 2
+        Hp, R = -(-H // 256) * 256, -(-V // 256)
+        tr, pad = Hp * 256 * 4, Hp * 256 * 2
+        if rows > 0:
+            assert pad + rows * tr <= lo < pad + (rows + 1) * tr or rows == R
+        else:
+            assert lo < pad + tr
+        assert hi == (R - rows) * tr
+        assert lo + hi >= V * H * 4
+        for r in range(R):  # narrowing tile row r writes bf16 bytes [256 r H 2, ...)
+            end = min(V, 256 * (r + 1)) * H * 2
+            q = (r + 1) // 2  # first fp32 tile row not yet read when row r is narrowed
+            assert q >= rows or end <= pad + q * tr
+    assert dw_layout(0, 64)[0] == 1 and dw_layout(10, -1)[0] == 1
+    st, lo, rows, hi = dw_layout(100, 64)
+    p = 1 << 20  # aligned dummy addresses, never dereferenced
+    # fused_tiles: lo below V H 2, hi below the layout's, fp32 operands
+    def fused(dt=1, lo_b=lo, hi_ptr=p + (1 << 16), hi_b=hi):
+        return lib.mt_flce_fused_tiles(16, 16, 8, 64, 100, 64, 64, dt, 0.0, 16, 16, 4, 16, 0, 16,
+                                       16, 16, 64, p, lo_b, hi_ptr, hi_b, 0, 256, 16, 1 << 30, None)
+    assert fused(lo_b=lo - 2) == 1
+    assert "V H 2" in lib.mt_flce_last_error().decode()
+    assert fused(hi_b=hi - 16) == 1
+    assert "mt_flce_dw_tiles_layout" in lib.mt_flce_last_error().decode()
+    assert fused(hi_ptr=p + 4096) == 1                 # hi overlaps lo
+    assert "overlap" in lib.mt_flce_last_error().decode()
+    assert fused(dt=0) == 3                            # the fused path is bf16 only
+    # backward_tiles: fp32 unsupported, buffers below the layout's sizes
     bargs = [16, 16, 8, 64, 100, 64, 64]
-    rest = [0.0, 16, 16, 4, 16, 16, 1, 16, 64, 16]
-    assert lib.mt_flce_backward_tiles(*bargs, 0, *rest, tb, 256, 256, 16, 1 << 30, None) == 3
-    assert lib.mt_flce_backward_tiles(*bargs, 1, *rest, tb - 16, 256, 256, 16, 1 << 30,
-                                      None) == 1
-    assert "mt_flce_dw_tiles_bytes" in lib.mt_flce_last_error().decode()
-    # ... chunk sizes must be positive multiples of 256
-    assert lib.mt_flce_backward_tiles(*bargs, 1, *rest, tb, 100, 256, 16, 1 << 30, None) == 1
+    rest = [0.0, 16, 16, 4, 16, 16, 1, 16, 64]
+
+    def btiles(dt=1, lo_b=lo, hi_b=hi, C=256):
+        return lib.mt_flce_backward_tiles(*bargs, dt, *rest, p, lo_b, p + (1 << 16), hi_b, 0, C,
+                                          256, 16, 1 << 30, None)
+    assert btiles(dt=0) == 3
+    assert btiles(hi_b=hi - 16) == 1
+    assert btiles(lo_b=0) == 1
+    assert btiles(C=100) == 1                          # blocks: positive multiples of 256
 
     def narrow(**kw):
-        a = dict(scale=16, t=1 << 20, tb=tb, V=100, H=64, out=1 << 20, ldo=64, dt=1)
+        a = dict(scale=16, lo=p, lo_b=lo, hi=p + (1 << 16), hi_b=hi, V=100, H=64)
         a.update(kw)
-        return lib.mt_flce_narrow_tiles(a["scale"], a["t"], a["tb"], a["V"], a["H"], a["out"],
-                                        a["ldo"], a["dt"], None)
-    assert narrow(dt=0) == 3                           # bf16 output only
-    assert narrow(H=60, ldo=64) == 3                   # H % 8
-    assert narrow(tb=tb - 1) == 1                      # buffer too small
-    assert narrow(ldo=56) == 1                         # ldo < H
-    assert narrow(ldo=264) == 1                        # in place beyond round_up(H, 256)
-    assert "in-place" in lib.mt_flce_last_error().decode()
-    assert narrow(out=(1 << 20) + 4096) == 1           # partial overlap
-    assert "overlaps" in lib.mt_flce_last_error().decode()
-    assert narrow(out=(1 << 20) + 8) == 1              # misaligned
+        return lib.mt_flce_narrow_tiles(a["scale"], a["lo"], a["lo_b"], a["hi"], a["hi_b"],
+                                        a["V"], a["H"], None)
+    H60 = dw_layout(100, 60)
+    assert narrow(H=60, lo_b=H60[1], hi_b=H60[3]) == 3  # H % 8
+    assert narrow(lo_b=lo - 1) == 1                    # buffers too small
+    assert narrow(hi_b=hi - 1) == 1
+    assert narrow(lo=p + 8) == 1                       # misaligned
     assert narrow(scale=None) == 1
+    assert narrow(V=0) == 1
 
 
 @pytest.mark.parametrize("key", [1, 2, 3, 4, 5])
@@ -190,8 +215,8 @@ def test_backward_plan_fits_budget(key):
 @pytest.mark.parametrize("key", [2, 3, 4, 5])
 def test_backward_narrow_plan_fits_budget(key):
     """The narrowing plan: within the budget; one row block (C >= n) keeps
-    dX's accumulator and X^T in the dW buffer (the workspace holds the G
-    block and the counters only); more row blocks have mt_flce_backward's
+    dX's accumulator and X^T in the narrowing scratch (the workspace holds
+    the G block and the counters only); more row blocks have mt_flce_backward's
     workspace.  Config 5 (H = 8192, a 210 MB budget) takes one row block per
     minibatch; fp32 has no narrowing path."""
     cfg = synth.CONFIGS[key]
@@ -216,7 +241,8 @@ def test_backward_narrow_plan_workspace_formula():
     """Over random shapes and budgets: the narrowing plan's blocks are
     multiples of 256 and its workspace is the formula mt_flce_backward_narrow
     checks -- the G block and the counters when one row block's accumulator
-    (as 256 x 256 tiles) and X^T fit in the dW buffer past the bf16 gradient,
+    (as 256 x 256 tiles) and X^T fit in what a bf16 gradient leaves of the
+    fp32 one (they then go to the scratch of mt_flce_narrow_scratch_bytes),
     else the G block, the row-major accumulator (several vocabulary blocks),
     X^T and the counters; within the budget unless nothing fits (the 256 x
     256 fallback)."""
@@ -232,8 +258,13 @@ def test_backward_narrow_plan_workspace_formula():
         budget = int(rng.choice([0, 1, int(rng.integers(1, 1 << 30))]))
         C, Cv, ws = backward_plan(T, n, H, V, torch.bfloat16, budget_bytes=budget, narrow=True)
         assert C % 256 == 0 and Cv % 256 == 0 and C > 0 and Cv > 0
-        tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
-        fits = C >= n and tb >= al(V * H * 2) + al(cd(C, 256) * cd(H, 256) * 65536 * 4) + al(H * C * 2)
+        Hp = cd(H, 256) * 256
+        tb = Hp * 256 * 2 + cd(V, 256) * Hp * 256 * 4  # the fp32 gradient the budget counts
+        need = al(cd(C, 256) * cd(H, 256) * 65536 * 4) + al(H * C * 2)
+        fits = C >= n and tb >= al(V * H * 2) + need
+        # the scratch that holds dX's accumulator and X^T outside the workspace
+        assert int(lib.mt_flce_narrow_scratch_bytes(V, H, C)) == \
+            (need if tb >= al(V * H * 2) + need else 0)
         if fits:
             expect = al(C * Cv * 2) + al(32)
         else:
@@ -263,21 +294,26 @@ def test_forward_keep_host_checks():
 
 
 def test_backward_narrow_host_checks():
-    """mt_flce_backward_narrow refuses fp32, H not a multiple of 8, a dW buffer
-    smaller than mt_flce_dw_tiles_bytes and more than one row block, before
-    touching any pointer."""
+    """mt_flce_backward_narrow refuses fp32, H not a multiple of 8, an output
+    below V H 2 bytes, a scratch below mt_flce_narrow_scratch_bytes and more
+    than one row block, before touching any pointer."""
     lib = _lib.load()
     T, H, V, n = 1000, 128, 5000, 700
-    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
+    need = int(lib.mt_flce_narrow_scratch_bytes(V, H, 768))
+    assert need > 0
     p = 16  # a dummy, aligned, never-dereferenced address
 
-    def call(dtype=1, h=H, ld=H, dwb=tb, C=768, Cv=1024):
+    def call(dtype=1, h=H, ld=H, ob=V * H * 2, sp=p, sb=need, C=768, Cv=1024):
         return lib.mt_flce_backward_narrow(p, p, T, h, V, ld, ld, dtype, 0.0, p, p, n, p, p, 0, p,
-                                           ld, p, dwb, C, Cv, p, 1 << 40, None, None)
+                                           ld, p, ob, sp, sb, C, Cv, p, 1 << 40, None, None)
     assert call(dtype=0) == 3
     assert call(h=100, ld=104) == 3
-    assert call(dwb=tb - 1) == 1
+    assert call(ob=V * H * 2 - 1) == 1
+    assert call(sb=need - 16) == 1
+    assert "mt_flce_narrow_scratch_bytes" in lib.mt_flce_last_error().decode()
+    assert call(sp=None) == 1
     assert call(C=512) == 1
+    assert lib.mt_flce_narrow_scratch_bytes(V, H, 0) == 0
 
 
 def test_backward_plan_budget_override_and_degenerate():
@@ -303,22 +339,29 @@ def test_forward_workspace_is_small():
 
 
 def test_fused_planner_prefers_the_faster_path():
-    """The fused path pays at configs 2, 3 and 4 (same-box step times, fused
-    against general: 23.4 vs 26.6 ms with config 2's dX split over the
-    vocabulary, 115 vs 148 ms, 179 ms against a modelled 226) and not at
-    config 5, whose 5% budget forces 512-row chunks (196.5 vs 189.5 ms)."""
+    """Routing of configs 2-5, against the general path each call would
+    otherwise take.  With the weight gradient wanted in bf16 (the reference's
+    call chain, no accumulator) that is the narrowing plan -- one row block
+    through mt_flce_backward_narrow after mt_flce_forward_keep, or tiles and
+    the narrowing pass -- and with an fp32 accumulator it is
+    mt_flce_backward.  Either way the fused path pays at configs 2, 3 and 4
+    (same-box steps, fused against general: 21.8 vs 25.3 ms at config 2,
+    111-113 vs 143-145 ms at config 3, 173-177 ms against a modelled 226 at
+    config 4) and not at config 5, whose 5% budget forces 512-row chunks
+    (182-189 vs 163-167 ms)."""
     lib = _lib.load()
     want = {2: 1, 3: 1, 4: 1, 5: 0}
     for key, pays_expected in want.items():
         cfg = synth.CONFIGS[key]
         n = int((synth.make_batch(cfg, 0, with_tensors=False)["target"] != -100).sum())
-        c, ws, pays = ctypes.c_int64(), ctypes.c_size_t(), ctypes.c_int()
-        assert lib.mt_flce_fused_plan(cfg.T, n, cfg.H, cfg.V, 1, 0, ctypes.byref(c),
-                                      ctypes.byref(ws), ctypes.byref(pays)) == 0
-        assert pays.value == pays_expected, key
-        assert c.value % 256 == 0 and 0 < ws.value <= 0.05 * cfg.T * cfg.V * 2
+        for acc in (0, 1):
+            c, ws, pays = ctypes.c_int64(), ctypes.c_size_t(), ctypes.c_int()
+            assert lib.mt_flce_fused_plan(cfg.T, n, cfg.H, cfg.V, 1, 0, acc, ctypes.byref(c),
+                                          ctypes.byref(ws), ctypes.byref(pays)) == 0
+            assert pays.value == pays_expected, (key, acc)
+            assert c.value % 256 == 0 and 0 < ws.value <= 0.05 * cfg.T * cfg.V * 2
     c, ws, pays = ctypes.c_int64(), ctypes.c_size_t(), ctypes.c_int()
-    assert lib.mt_flce_fused_plan(100, 50, 64, 100, 0, 0, ctypes.byref(c), ctypes.byref(ws),
+    assert lib.mt_flce_fused_plan(100, 50, 64, 100, 0, 0, 0, ctypes.byref(c), ctypes.byref(ws),
                                   ctypes.byref(pays)) == 3  # fp32: unsupported
 
 

@@ -118,9 +118,10 @@ def test_general_backward_guards(gpu, case, monkeypatch, softcap):
 
 def test_backward_narrow_guards(gpu, case):
     """mt_flce_backward_narrow: one row block and several vocabulary blocks
-    (dX's fp32 accumulator and X^T in the dW buffer's second half, dW written
-    as bf16 rows in its first), with exactly the workspace
-    mt_flce_backward_narrow_plan reports for that blocking."""
+    (dX's fp32 accumulator and X^T in the scratch buffer, dW written as bf16
+    rows into a buffer of exactly V x H bf16), with exactly the workspace
+    mt_flce_backward_narrow_plan and the scratch mt_flce_narrow_scratch_bytes
+    report for that blocking."""
     X, W, y, ri, rl, n = case
     lib = _lib.load()
     s = _stream(gpu)
@@ -138,18 +139,20 @@ def test_backward_narrow_guards(gpu, case):
     assert bws < C * Cv * 2 + H * C * 2  # no accumulator or X^T in the workspace
     grad = torch.rand(T, device=gpu)
     gdx, dX = matrix(gpu, T, H, H + 8, torch.bfloat16)
-    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
-    gdw = Guarded(gpu, tb)
+    sb = int(lib.mt_flce_narrow_scratch_bytes(V, H, C))
+    assert sb > 0
+    gdw = Guarded(gpu, V * H * 2)
+    gsc = Guarded(gpu, sb)
     gws = Guarded(gpu, bws)
     _lib.check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                            _p(ri), _p(rl), n, _p(lse), _p(grad), 1, gdx.ptr,
-                                           H + 8, gdw.ptr, tb, C, Cv, gws.ptr, bws, None, s),
-               "backward_narrow")
+                                           H + 8, gdw.ptr, V * H * 2, gsc.ptr, sb, C, Cv, gws.ptr,
+                                           bws, None, s), "backward_narrow")
     torch.cuda.synchronize()
-    assert gdx.intact() and gdw.intact() and gws.intact()
+    assert gdx.intact() and gdw.intact() and gws.intact() and gsc.intact()
     assert pad_intact(dX, H)
     assert bool(torch.isfinite(dX[:, :H].float()).all())
-    assert bool(torch.isfinite(gdw.view(torch.bfloat16, (tb // 2,))[: V * H].float()).all())
+    assert bool(torch.isfinite(gdw.view(torch.bfloat16, (V * H,)).float()).all())
 
 
 def test_fused_and_rescale_guards(gpu, case):

@@ -73,7 +73,7 @@ def test_patched_llama_matches_reference(gpu, fused):
 
     model = patch_causal_lm(model.to(gpu))
     out = model(input_ids=ids.to(gpu), labels=labels.to(gpu), position_ids=pos.to(gpu),
-                grad_scale=scale if fused else None, num_items_in_batch=n)
+                mt_grad_scale=scale if fused else None, num_items_in_batch=n)
     assert out.logits is None
     loss = out.loss
     assert loss.shape == (ids.numel(),) and loss.dtype == torch.float32

@@ -15,7 +15,7 @@ import threading
 import pytest
 import torch
 
-from mini_trainer_amd import fused_linear_cross_entropy
+from mini_trainer_amd import fused_linear_cross_entropy, path_of
 from mini_trainer_amd.flce import BACKWARD_BUDGET_ENV, FUSED_ENV, fused_plan
 from mini_trainer_amd.none_reduction_losses import (
     liger_fixed_fused_linear_cross_entropy_none_reduction)
@@ -180,7 +180,8 @@ def test_drop_in_reads_grad_scale_kwarg(gpu):
     X, W, y = make_case(256, 64, 512, torch.bfloat16, seed=22)
     Xd, Wd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True)
     loss = liger_fixed_fused_linear_cross_entropy_none_reduction(
-        Xd, Wd, y.to(gpu), None, -100, None, grad_scale=0.25)
+        Xd, Wd, y.to(gpu), None, -100, None, mt_grad_scale=0.25)
+    assert path_of(loss) == "fused"
     (loss.sum() * 0.25).backward()
     check_parity(X, W, y, loss.detach().cpu(), Xd.grad.cpu(), Wd.grad.cpu(),
                  grad=torch.full((256,), 0.25))

@@ -140,3 +140,47 @@ def test_row_ranges_with_a_fitting_weight_keep_the_fused_path(gpu, monkeypatch):
     torch.cuda.synchronize()
     check_parity(X, W, shifted, out.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(),
                  grad=torch.full((1500,), 1.0 / n))
+
+
+@pytest.mark.parametrize("fused", ["1", "0"])
+def test_three_row_ranges_hold_one_weight_gradient(gpu, monkeypatch, fused):
+    """X beyond one buffer's reach in three row ranges (2000 x 128 bf16
+    against a 192 KiB reach: 768 + 768 + 464 rows), the reference's call
+    chain, on the fused kernels ("1") or the general path ("0"): one
+    autograd node whose ranges add into one weight gradient, so the peak
+    beyond inputs and outputs (loss, dX, the fp32 dW the kernels accumulate)
+    is at most one range's workspace; W.grad then owns exactly V x H bf16.
+    Parity against the torch path as everywhere."""
+    print(f"case three row ranges fused={fused}", flush=True)
+    from mini_trainer_amd.flce import backward_plan, fused_plan
+
+    monkeypatch.setenv(REACH_ENV, str(192 << 10))
+    monkeypatch.setenv(FUSED_ENV, fused)
+    T, H, V = 2000, 128, 256
+    X, W, y = make_case(T, H, V, torch.bfloat16, seed=31)
+    n = int((y != -100).sum())
+    Xd, Wd, yd = X.to(gpu).requires_grad_(True), W.to(gpu).requires_grad_(True), y.to(gpu)
+    lib = _lib.load()
+    rng = [(0, 768), (768, 1536), (1536, 2000)]
+    ns = [int((y[a:b] != -100).sum()) for a, b in rng]
+    if fused == "1":
+        ws = max(fused_plan(b - a, k, H, V)[1] for (a, b), k in zip(rng, ns))
+    else:
+        ws = max(backward_plan(b - a, k, H, V, torch.bfloat16, narrow=True)[2] +
+                 lib.mt_flce_forward_workspace_bytes(b - a, k, H, V, _lib.MT_DTYPE_BF16)
+                 for (a, b), k in zip(rng, ns))
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(gpu)
+    base = torch.cuda.memory_allocated(gpu)
+    out = drop_in(Xd, Wd, yd)
+    assert path_of(out) == ("fused_unit" if fused == "1" else "general")
+    (out.float().sum() / n).backward()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(gpu)
+    Hp = -(-H // 256) * 256
+    dw_fp32 = Hp * 256 * 2 + (-(-V // 256)) * Hp * 256 * 4 + Hp * 256 * 4  # + one tile row
+    outputs = T * 4 + T * H * 2 + dw_fp32
+    assert peak - base - outputs <= ws + (256 << 10), (peak - base - outputs, ws)
+    assert Wd.grad.dtype == torch.bfloat16 and Wd.grad.untyped_storage().nbytes() == V * H * 2
+    check_parity(X, W, y, out.detach().cpu(), Xd.grad.cpu(), Wd.grad.float().cpu(),
+                 grad=torch.full((T,), 1.0 / n))

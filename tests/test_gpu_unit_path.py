@@ -180,9 +180,29 @@ def test_narrow_in_place_bit_exact(gpu, V, H, ld):
     assert torch.equal(got, want)
 
 
+def _tiled_buffers(V, H, dev, fill=float("nan")):
+    """The two buffers of mt_flce_dw_tiles_layout, filled with `fill`:
+    (lo: bf16 [V, H], hi: fp32, tile rows held in lo)."""
+    lib = _lib.load()
+    lo_b, rows, hi_b = ctypes.c_size_t(), ctypes.c_int64(), ctypes.c_size_t()
+    _lib.check(lib.mt_flce_dw_tiles_layout(V, H, ctypes.byref(lo_b), ctypes.byref(rows),
+                                           ctypes.byref(hi_b)), "mt_flce_dw_tiles_layout")
+    assert lo_b.value == V * H * 2
+    lo = torch.empty(V, H, dtype=torch.bfloat16, device=dev)
+    lo.view(torch.float32).fill_(fill)
+    hi = torch.full((hi_b.value // 4,), fill, dtype=torch.float32, device=dev)
+    return lo, hi, rows.value
+
+
+def _targs(lo, hi):
+    """(lo, lo bytes, hi, hi bytes) as the C ABI takes them."""
+    return (_p(lo), lo.numel() * 2, _p(hi), hi.numel() * 4)
+
+
 def _fused_abi(dev, X, W, ri, rl, n, C, wsb, tiled):
     """One mt_flce_fused (row-major dW) or mt_flce_fused_tiles call for a
-    unit upstream gradient; returns (loss, lse, dX, dW buffer)."""
+    unit upstream gradient; returns (loss, lse, dX, dW) with dW the
+    row-major fp32 tensor or the (lo, hi, lo_rows) tiles."""
     lib = _lib.load()
     T, H = X.shape
     V = W.shape[0]
@@ -192,12 +212,11 @@ def _fused_abi(dev, X, W, ri, rl, n, C, wsb, tiled):
     dX = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
     if tiled:
-        tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
-        dW = torch.empty(tb // 4, device=dev)
+        dW = _tiled_buffers(V, H, dev)
         _lib.check(lib.mt_flce_fused_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                            _p(ri), _p(rl), n, _p(g), 0, _p(loss), _p(lse),
-                                           _p(dX), H, _p(dW), tb, C, _p(ws), wsb, _stream(dev)),
-                   "mt_flce_fused_tiles")
+                                           _p(dX), H, *_targs(dW[0], dW[1]), 0, C, _p(ws), wsb,
+                                           _stream(dev)), "mt_flce_fused_tiles")
     else:
         dW = torch.empty(V, H, device=dev)
         _lib.check(lib.mt_flce_fused(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
@@ -207,14 +226,18 @@ def _fused_abi(dev, X, W, ri, rl, n, C, wsb, tiled):
     return loss, lse[:n], dX, dW
 
 
-def _untile(buf, V, H):
-    """Row-major fp32 [V, H] from the tiled layout: a pad of 256 * Hp bf16,
-    then tile (tm, tn) at index tm * tiles_n + tn, 256 KiB each, ordered
-    (wave row wm, wave column wn, fragment row fm, fragment column fn,
-    lane / 16, lane % 16, element r) for the element at row
+def _untile(tiles, V, H):
+    """Row-major fp32 [V, H] from the tiled layout (lo, hi, lo_rows): tile
+    rows [0, lo_rows) in lo after a pad of 256 * Hp bf16, the rest in hi;
+    tile (tm, tn) at index tm * tiles_n + tn of that sequence, 256 KiB each,
+    ordered (wave row wm, wave column wn, fragment row fm, fragment column
+    fn, lane / 16, lane % 16, element r) for the element at row
     wm * 128 + fm * 16 + lane % 16, column wn * 128 + fn * 16 + 4 (lane / 16) + r."""
+    lo, hi, rows = tiles
     vt, tn = -(-V // 256), -(-H // 256)
-    t = buf[128 * tn * 256:].view(vt, tn, 2, 2, 8, 8, 4, 16, 4)
+    pad = 128 * tn * 256
+    flat = torch.cat([lo.view(torch.float32).reshape(-1)[pad:pad + rows * tn * 65536], hi])
+    t = flat.view(vt, tn, 2, 2, 8, 8, 4, 16, 4)
     #       dims: tm tn wm wn fm fn lq li r -> rows (tm wm fm li), cols (tn wn fn lq r)
     t = t.permute(0, 2, 4, 7, 1, 3, 5, 6, 8).reshape(vt * 256, tn * 256)
     return t[:V, :H]
@@ -224,13 +247,13 @@ def _untile(buf, V, H):
                                           (300, 64, 256, 0), (200, 72, 100, 0)])
 def test_fused_tiles_match_rows_bit_exact(gpu, T, H, V, budget):
     """mt_flce_fused_tiles against mt_flce_fused on the same inputs: loss,
-    lse and dX the same bits; the tiles, unscrambled, the row-major fp32 dW
-    bit for bit (tails in V and H; budget 1: 256-row chunks accumulating,
-    and at 65600 x 1056 dW over its work queue).  mt_flce_narrow_tiles in
-    place (bf16 rows at the allocation's start) and into a separate buffer
-    with a wider pitch (the columns past H untouched) against torch's fp32
-    multiply rounded to nearest even.  The last case is one partial tile
-    (V < 256, H < 256) with a partial last K stage (H % 64 = 8)."""
+    lse and dX the same bits; the tiles, unscrambled from their two buffers,
+    the row-major fp32 dW bit for bit (tails in V and H; budget 1: 256-row
+    chunks accumulating, and at 65600 x 1056 dW over its work queue).
+    mt_flce_narrow_tiles in place (the bf16 gradient filling lo) against
+    torch's fp32 multiply rounded to nearest even.  The last case is one
+    partial tile (V < 256, H < 256) with a partial last K stage (H % 64 = 8),
+    held wholly in hi."""
     print(f"case tiles T={T} H={H} V={V}", flush=True)
     lib = _lib.load()
     X, W, y = make_case(T, H, V, torch.bfloat16, seed=T + 3)
@@ -243,17 +266,10 @@ def test_fused_tiles_match_rows_bit_exact(gpu, T, H, V, budget):
     assert torch.equal(_untile(d1, V, H), d0)
     scale = torch.tensor([0.37], device=gpu)
     want = (d0 * scale).to(torch.bfloat16)
-    out = torch.full((V, H + 8), 7.0, dtype=torch.bfloat16, device=gpu)
-    tb = d1.numel() * 4
-    _lib.check(lib.mt_flce_narrow_tiles(_p(scale), _p(d1), tb, V, H, _p(out), H + 8,
-                                        _lib.MT_DTYPE_BF16, _stream(gpu)), "narrow out of place")
-    _lib.check(lib.mt_flce_narrow_tiles(_p(scale), _p(d1), tb, V, H, _p(d1), H,
-                                        _lib.MT_DTYPE_BF16, _stream(gpu)), "narrow in place")
+    _lib.check(lib.mt_flce_narrow_tiles(_p(scale), *_targs(d1[0], d1[1]), V, H, _stream(gpu)),
+               "narrow in place")
     torch.cuda.synchronize()
-    assert torch.equal(out[:, :H], want)
-    assert torch.equal(out[:, H:], torch.full((V, 8), 7.0, dtype=torch.bfloat16, device=gpu))
-    got = d1.view(torch.bfloat16)[: V * H].view(V, H)
-    assert torch.equal(got, want)
+    assert torch.equal(d1[0], want)
 
 
 @pytest.mark.parametrize("C,Cv,cap", [(256, 52736, None), (256, 16384, "3"), (512, 65600 + 192, None),
@@ -291,40 +307,43 @@ def test_backward_tiles_match_rows_bit_exact(gpu, monkeypatch, C, Cv, cap):
     _lib.check(lib.mt_flce_backward(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0, _p(ri),
                                     _p(rl), n, _p(lse), _p(g), 1, _p(dX0), H, _p(dW0), H, 0, C, Cv,
                                     _p(ws), wsb, s), "backward")
-    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
     dX1 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
-    dW1 = torch.full((tb // 4,), float("nan"), device=gpu)
+    dW1 = _tiled_buffers(V, H, gpu)
     _lib.check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                           _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX1), H,
-                                          _p(dW1), tb, C, Cv, _p(ws), wsb, s), "backward_tiles")
+                                          *_targs(dW1[0], dW1[1]), 0, C, Cv, _p(ws), wsb, s),
+               "backward_tiles")
     torch.cuda.synchronize()
     assert torch.equal(dX0, dX1)
     assert torch.equal(_untile(dW1, V, H), dW0)
     if C < n:
         return
-    # one row block: mt_flce_backward_narrow (dW narrowed in its epilogue,
-    # dX's accumulator and X^T in the buffer's second half, only the G block
-    # in the workspace) against the tiles narrowed by mt_flce_narrow_tiles
+    # one row block: mt_flce_backward_narrow (dW narrowed in its epilogue
+    # into a bf16 [V, H] of its own size, dX's accumulator and X^T in the
+    # scratch buffer, only the G block in the workspace) against the tiles
+    # narrowed by mt_flce_narrow_tiles
     one = torch.ones(1, device=gpu)
-    want = torch.empty(V, H, dtype=torch.bfloat16, device=gpu)
-    _lib.check(lib.mt_flce_narrow_tiles(_p(one), _p(dW1), tb, V, H, _p(want), H,
-                                        _lib.MT_DTYPE_BF16, s), "narrow_tiles")
+    _lib.check(lib.mt_flce_narrow_tiles(_p(one), *_targs(dW1[0], dW1[1]), V, H, s), "narrow_tiles")
+    want = dW1[0]
     nwsb = al(C * Cv * 2) + al(32)  # the G block and the counters
     nws = torch.empty(nwsb, dtype=torch.uint8, device=gpu)
+    sb = int(lib.mt_flce_narrow_scratch_bytes(V, H, C))
+    assert sb > 0
+    scratch = torch.full((sb,), 255, dtype=torch.uint8, device=gpu)
     dX2 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
-    dW2 = torch.full((tb // 4,), float("nan"), device=gpu)
+    dW2 = torch.full((V, H), float("nan"), dtype=torch.bfloat16, device=gpu)
     _lib.check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                            _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX2), H,
-                                           _p(dW2), tb, C, Cv, _p(nws), nwsb, None, s),
-               "backward_narrow")
+                                           _p(dW2), V * H * 2, _p(scratch), sb, C, Cv, _p(nws),
+                                           nwsb, None, s), "backward_narrow")
     torch.cuda.synchronize()
     assert torch.equal(dX2, dX0)
-    assert torch.equal(dW2.view(torch.bfloat16)[: V * H].view(V, H), want)
+    assert torch.equal(dW2, want)
 
 
 def test_backward_narrow_accumulator_in_workspace(gpu):
-    """One row block and three vocabulary blocks where the dW buffer has no
-    room past the bf16 gradient for dX's accumulator and X^T (V = 1300 < 3 C):
+    """One row block and three vocabulary blocks where a bf16 gradient leaves
+    no room of the fp32 one for dX's accumulator and X^T (V = 1300 < 3 C):
     mt_flce_backward_narrow keeps both in the workspace (the accumulator
     row-major) and still matches mt_flce_backward_tiles + mt_flce_narrow_tiles
     bit for bit, with the workspace mt_flce_backward_narrow_plan reports."""
@@ -349,25 +368,24 @@ def test_backward_narrow_accumulator_in_workspace(gpu):
     assert (C, Cv, wsb) == (1024, 512, budget)
     g = torch.rand(T, device=gpu, generator=torch.Generator(device=gpu).manual_seed(9))
     ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
-    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
     dX1 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
-    dW1 = torch.full((tb // 4,), float("nan"), device=gpu)
+    dW1 = _tiled_buffers(V, H, gpu)
     _lib.check(lib.mt_flce_backward_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                           _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX1), H,
-                                          _p(dW1), tb, C, Cv, _p(ws), wsb, s), "backward_tiles")
+                                          *_targs(dW1[0], dW1[1]), 0, C, Cv, _p(ws), wsb, s),
+               "backward_tiles")
     one = torch.ones(1, device=gpu)
-    want = torch.empty(V, H, dtype=torch.bfloat16, device=gpu)
-    _lib.check(lib.mt_flce_narrow_tiles(_p(one), _p(dW1), tb, V, H, _p(want), H,
-                                        _lib.MT_DTYPE_BF16, s), "narrow_tiles")
+    _lib.check(lib.mt_flce_narrow_tiles(_p(one), *_targs(dW1[0], dW1[1]), V, H, s), "narrow_tiles")
+    assert int(lib.mt_flce_narrow_scratch_bytes(V, H, C)) == 0  # no room: all in the workspace
     dX2 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
-    dW2 = torch.full((tb // 4,), float("nan"), device=gpu)
+    dW2 = torch.full((V, H), float("nan"), dtype=torch.bfloat16, device=gpu)
     _lib.check(lib.mt_flce_backward_narrow(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                            _p(ri), _p(rl), n, _p(lse), _p(g), 1, _p(dX2), H,
-                                           _p(dW2), tb, C, Cv, _p(ws), wsb, None, s),
-               "backward_narrow")
+                                           _p(dW2), V * H * 2, None, 0, C, Cv, _p(ws), wsb, None,
+                                           s), "backward_narrow")
     torch.cuda.synchronize()
     assert torch.equal(dX2, dX1)
-    assert torch.equal(dW2.view(torch.bfloat16)[: V * H].view(V, H), want)
+    assert torch.equal(dW2, dW1[0])
 
 
 @pytest.mark.parametrize("shift,H", [(0.0, 192), (56.0, 192), (0.0, 200)])
@@ -423,31 +441,35 @@ def test_fused_tiles_all_masked_and_narrow_phases(gpu):
     y = torch.full((T,), -100, device=gpu)
     ri, rl, n = prepare_targets(y, V)
     assert n == 0
-    tb = int(lib.mt_flce_dw_tiles_bytes(V, H))
-    dW = torch.full((tb // 4,), float("nan"), device=gpu)
+    dW = _tiled_buffers(V, H, gpu)
+    assert dW[2] > 0  # tile rows in both buffers
     loss = torch.empty(T, device=gpu)
     dX = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
     _lib.check(lib.mt_flce_fused_tiles(_p(X), _p(W), T, H, V, H, H, _lib.MT_DTYPE_BF16, 0.0,
                                        _p(ri), _p(rl), 0, None, 0, _p(loss), None, _p(dX), H,
-                                       _p(dW), tb, 0, None, 0, _stream(gpu)), "all masked")
+                                       *_targs(dW[0], dW[1]), 0, 0, None, 0, _stream(gpu)),
+               "all masked")
     torch.cuda.synchronize()
     assert torch.count_nonzero(_untile(dW, V, H)) == 0 and torch.count_nonzero(dX) == 0
     assert torch.equal(loss, torch.zeros(T, device=gpu))
     g = torch.Generator(device=gpu).manual_seed(2)
-    dW = torch.randn(tb // 4, device=gpu, generator=g)
+    lo, hi, rows = dW
+    lo.view(torch.float32).copy_(torch.randn(lo.numel() // 2, device=gpu, generator=g).view(V, H // 2))
+    hi.copy_(torch.randn(hi.numel(), device=gpu, generator=g))
     scale = torch.tensor([-2.5], device=gpu)
     want = (_untile(dW, V, H) * scale).to(torch.bfloat16)
-    _lib.check(lib.mt_flce_narrow_tiles(_p(scale), _p(dW), tb, V, H, _p(dW), H,
-                                        _lib.MT_DTYPE_BF16, _stream(gpu)), "narrow in place")
+    _lib.check(lib.mt_flce_narrow_tiles(_p(scale), *_targs(lo, hi), V, H, _stream(gpu)),
+               "narrow in place")
     torch.cuda.synchronize()
-    assert torch.equal(dW.view(torch.bfloat16)[: V * H].view(V, H), want)
+    assert torch.equal(lo, want)
 
 
 def test_reference_chain_extra_memory(gpu):
     """The reference chain on the fused kernels allocates, beyond its inputs
-    and required outputs (loss, dX, the fp32 dW tiles whose storage then
-    holds W.grad in bf16 -- half a tile row and the tile grid's padding more
-    than V x H fp32), only the fused workspace."""
+    and required outputs (loss, dX, the fp32 dW tiles -- half a tile row and
+    the tile grid's padding more than V x H fp32), only the fused workspace;
+    W.grad afterwards owns exactly V x H bf16 (the tiles' second buffer is
+    gone)."""
     T, H, V = 4096, 512, 32000
     X, W, y = make_case(T, H, V, torch.bfloat16, seed=51)
     n = int((y != -100).sum())
@@ -464,6 +486,9 @@ def test_reference_chain_extra_memory(gpu):
     outputs = T * 4 + T * H * 2 + V * H * 4
     assert peak - base - outputs <= ws + (4 << 20), (peak - base - outputs, ws)
     assert Wd.grad.dtype == torch.bfloat16 and Wd.grad.is_contiguous()
+    assert Wd.grad.untyped_storage().nbytes() == V * H * 2
+    live = torch.cuda.memory_allocated(gpu) - base
+    assert live <= T * 4 + 2 * T * H * 2 + V * H * 2 + (1 << 20), live  # loss, dX, X.grad, W.grad
 
 
 def test_segment_sums_of_shifted_labels(gpu):

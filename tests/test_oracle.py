@@ -221,3 +221,51 @@ def test_planted_mistakes_are_caught(mistake):
         v = (y != -100).numpy()
         # unrounded logits differ from the bf16 torch path by more than rounding noise of fp32
         assert np.max(np.abs(cl[v] - lb.numpy()[v])) > 1e-4
+
+
+def _bf16_case(seed, T=96, H=200, V=700, w_std=0.2, mask=0.3):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    W = (torch.randn(V, H, generator=g) * w_std).to(torch.bfloat16)
+    y = torch.randint(0, V, (T,), generator=g)
+    y[torch.rand(T, generator=g) < mask] = -100
+    grad = torch.rand(T, generator=g) + 0.25
+    return X, W, y, grad
+
+
+@pytest.mark.parametrize("softcap", [None, 15.0])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_upcast_branch_pinned(softcap, seed):
+    """torch_path(upcast=True) -- the full-size GPU checker -- against the
+    default branch (F.linear in bf16, pinned through the C restatement) and
+    against the float64 closed form, bf16 inputs, softcap and a per-token
+    upstream gradient.  The logits of both branches are the bf16 rounding of
+    the same fp32 products, so the losses agree to fp32 noise; the closed
+    form does not round the logits, hence its looser bound."""
+    X, W, y, grad = _bf16_case(seed)
+    v = y != -100
+    l0, dX0, dW0 = torch_path(X, W, y, grad=grad, softcap=softcap, chunk_rows=40)
+    l1, dX1, dW1 = torch_path(X, W, y, grad=grad, softcap=softcap, chunk_rows=40, upcast=True)
+    assert dX1.dtype == torch.bfloat16 and dW1.dtype == torch.float32
+    assert torch.equal(l1[~v], torch.zeros(int((~v).sum())))
+    assert ((l1 - l0).abs() / l0.abs())[v].max().item() <= 1e-5
+    assert rel_fro(dX1.float(), dX0.float()) <= 1e-3
+    assert rel_fro(dW1, dW0) <= 1e-5
+    bl, bdX, bdW, _ = brute.flce_f64(X.float().numpy(), W.float().numpy(), y.numpy(),
+                                     grad.numpy(), softcap=softcap)
+    vn = v.numpy()
+    assert np.max(np.abs(l1.numpy()[vn] - bl[vn]) / np.abs(bl[vn])) < 1e-2
+    assert rel_fro(dX1.float(), torch.from_numpy(bdX)) < 1e-2
+    assert rel_fro(dW1, torch.from_numpy(bdW)) < 1e-2
+
+
+def test_upcast_branch_planted_missing_rounding_is_caught():
+    """The upcast branch with its `.to(X.dtype)` rounding of the logits
+    dropped -- planted here by handing it fp32 copies of the bf16 inputs,
+    which skips exactly that rounding -- fails the default-branch bound of
+    test_upcast_branch_pinned."""
+    X, W, y, grad = _bf16_case(0)
+    v = y != -100
+    l0, _, _ = torch_path(X, W, y, grad=grad, chunk_rows=40)
+    bad, _, _ = torch_path(X.float(), W.float(), y, grad=grad, chunk_rows=40, upcast=True)
+    assert ((bad - l0).abs() / l0.abs())[v].max().item() > 1e-5
