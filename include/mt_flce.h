@@ -156,7 +156,9 @@ uint64_t mt_flce_max_buffer_bytes(void);
  * results as mt_flce_forward -- bit-identical for bf16 -- for callers that
  * cannot allocate device memory or hand the library a workspace (code under
  * HIP graph capture, tight serving and evaluation loops, harnesses that
- * forbid hipMalloc).  Its scratch (the forward's (max, sum) partials and
+ * forbid hipMalloc; under capture, with the library's profiling hook off
+ * and after one call on the device outside the capture, which looks the
+ * scratch's address up).  Its scratch (the forward's (max, sum) partials and
  * label logits) is a static device array of mt_flce_noalloc_scratch_bytes()
  * bytes (16 MiB) per GPU, held until the process ends; valid rows are
  * processed in chunks that fit it.  A V whose single row of partials does

@@ -9,7 +9,11 @@ import ctypes
 from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p, c_char_p, POINTER
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libmt_flce.so"
+import os
+
+# MT_FLCE_LIB: another build of the same library (the sanitized host-only
+# build of the CPU tests); unset in production.
+LIB_PATH = Path(os.environ.get("MT_FLCE_LIB") or Path(__file__).resolve().parent / "libmt_flce.so")
 ABI_VERSION = 7
 
 MT_DTYPE_F32 = 0

@@ -38,6 +38,54 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libmt_flce.so)")
 
 
+SAN_LIB_PATH = PKG_DIR / "_build" / "libmt_flce_san.so"
+# The CPU tests' build: AddressSanitizer and UndefinedBehaviorSanitizer on
+# the host pass only (the device code is compiled plainly, at -O1, and never
+# runs: the CPU tests exercise the argument checks, planners and error
+# paths, on a machine without a GPU).
+SAN_FLAGS = [
+    f"--offload-arch={ARCH}", "-O1", "-g", "-std=c++17", "-fPIC", "-shared",
+    "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer",
+    "-Xarch_device", "-g0",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def san_is_stale() -> bool:
+    if not SAN_LIB_PATH.exists():
+        return True
+    t = SAN_LIB_PATH.stat().st_mtime
+    return any(p.stat().st_mtime > t for p in DEPENDS if p.exists())
+
+
+def build_sanitized(verbose: bool = False) -> Path:
+    """Compile the sanitized test build (_build/libmt_flce_san.so).  Always
+    recompiles (about a minute).  Load it with the clang ASan runtime
+    preloaded."""
+    SAN_LIB_PATH.parent.mkdir(exist_ok=True)
+    tmp = SAN_LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *SAN_FLAGS, "-o", str(tmp), *map(str, SOURCES)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc (sanitized build) failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, SAN_LIB_PATH)
+    return SAN_LIB_PATH
+
+
+def asan_runtime() -> Path:
+    """The clang ASan runtime matching hipcc (to LD_PRELOAD into Python)."""
+    clang = Path(hipcc()).resolve().parent.parent / "llvm" / "bin" / "clang"
+    if not clang.exists():
+        clang = Path("/opt/rocm/llvm/bin/clang")
+    out = subprocess.run([str(clang), "-print-file-name=libclang_rt.asan-x86_64.so"],
+                         capture_output=True, text=True).stdout.strip()
+    return Path(out)
+
+
 def build_library(verbose: bool = False) -> Path:
     """Compile libmt_flce.so for gfx950.  Always recompiles."""
     tmp = LIB_PATH.with_suffix(".so.tmp")

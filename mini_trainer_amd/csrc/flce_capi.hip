@@ -32,8 +32,15 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// Test hook: MT_FLCE_TEST_FAIL_LAUNCH=<name> makes every check of a launch
+// whose name contains <name> report a failed launch (the kernel itself ran),
+// so that the error path from here to the caller's exception can be tested
+// on a working GPU.  Unset in production.
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
+  const char* hook = std::getenv("MT_FLCE_TEST_FAIL_LAUNCH");
+  if (hook && *hook && std::strstr(what, hook))
+    return fail(MT_ERR_HIP, "%s: injected launch failure (MT_FLCE_TEST_FAIL_LAUNCH)", what);
   if (e != hipSuccess) return fail(MT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
   return MT_OK;
 }
@@ -1213,7 +1220,7 @@ int mt_flce_prepare(const int64_t* labels, int64_t T, int64_t V, int64_t ignore_
 size_t mt_flce_forward_workspace_bytes(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dtype) {
   (void)T;
   (void)H;
-  if (n_valid <= 0 || V <= 0 || !esize_of(dtype)) return 0;
+  if (n_valid <= 0 || V <= 0 || n_valid > INT32_MAX || V > INT32_MAX || !esize_of(dtype)) return 0;
   return forward_ws(plan_forward(n_valid, V, esize_of(dtype)), n_valid);
 }
 
@@ -1406,7 +1413,8 @@ int backward_plan_entry(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dt
                         size_t* workspace_bytes, bool narrow) {
   const int es = esize_of(dtype);
   if (!es) return fail(MT_ERR_INVALID_ARGUMENT, "dtype %d is not MT_DTYPE_F32 or MT_DTYPE_BF16", dtype);
-  if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0)
+  if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0 || T > INT32_MAX || H > INT32_MAX ||
+      V > INT32_MAX)
     return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld n_valid=%lld H=%lld V=%lld", (long long)T,
                 (long long)n_valid, (long long)H, (long long)V);
   if (!chunk_rows || !chunk_vocab || !workspace_bytes)
@@ -1639,7 +1647,8 @@ int mt_flce_fused_plan(int64_t T, int64_t n_valid, int64_t H, int64_t V, int dty
                        size_t* workspace_bytes, int* pays) {
   if (dtype != MT_DTYPE_BF16)
     return fail(MT_ERR_UNSUPPORTED, "the fused path is bf16 only (dtype %d)", dtype);
-  if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0)
+  if (T < 0 || n_valid < 0 || n_valid > T || H <= 0 || V <= 0 || T > INT32_MAX || H > INT32_MAX ||
+      V > INT32_MAX)
     return fail(MT_ERR_INVALID_ARGUMENT, "bad sizes T=%lld n_valid=%lld H=%lld V=%lld", (long long)T,
                 (long long)n_valid, (long long)H, (long long)V);
   if (!chunk_rows || !workspace_bytes || !pays)

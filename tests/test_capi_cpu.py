@@ -384,3 +384,23 @@ def test_buffer_reach_hook(monkeypatch):
     # 256 weight rows of 128 bytes exceed 1000 bytes
     assert call_forward(T=4, n=2) == 3
     assert "256 of them" in lib.mt_flce_last_error().decode()
+
+
+def test_launch_failure_surfaces_as_flce_error(monkeypatch):
+    """A launch the HIP runtime refuses (here: no GPU in this process) comes
+    back as MT_ERR_HIP with the kernel's name and the runtime's text, which
+    the binding raises as FlceError (a RuntimeError); the test hook
+    MT_FLCE_TEST_FAIL_LAUNCH reports the same for a named launch.  CPU only:
+    the call's pointers are dummies that a GPU would fault on."""
+    if torch.cuda.is_available():
+        pytest.skip("launches with dummy pointers: a process without a GPU only")
+    lib = _lib.load()
+    p = 1 << 20
+    rc = lib.mt_flce_prepare(p, 10, 100, -100, 0, p, p, p, None)
+    assert rc == 4
+    with pytest.raises(_lib.FlceError, match="mt_flce_prepare: MT_ERR_HIP: prepare_kernel: "):
+        _lib.check(rc, "mt_flce_prepare")
+    assert issubclass(_lib.FlceError, RuntimeError)
+    monkeypatch.setenv("MT_FLCE_TEST_FAIL_LAUNCH", "prepare")
+    rc = lib.mt_flce_prepare(p, 10, 100, -100, 0, p, p, p, None)
+    assert rc == 4 and "injected launch failure" in lib.mt_flce_last_error().decode()

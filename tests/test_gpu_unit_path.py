@@ -557,3 +557,26 @@ def test_profile_hook_reports_the_fused_step(gpu, monkeypatch, split):
     need = ctypes.c_size_t(0)
     assert lib.mt_flce_profile_report(None, 0, ctypes.byref(need)) == 1 and need.value > 100
     assert "dx_dw_phase" in profile_report()
+
+
+@pytest.mark.parametrize("kernel", ["dx_dw_bf16_kernel", "narrow_tiles_kernel",
+                                    "recompute_kernel"])
+def test_injected_launch_failure_raises_and_recovers(gpu, monkeypatch, kernel):
+    """A launch reported failed (the test hook MT_FLCE_TEST_FAIL_LAUNCH; the
+    kernel itself runs) surfaces from the reference chain as FlceError, a
+    RuntimeError naming the kernel: in the fused forward (dx_dw), in the
+    backward's narrowing, or in the general path's backward (recompute).
+    Without the hook the next call on the same device runs and matches the
+    torch path."""
+    print(f"case injected failure {kernel}", flush=True)
+    X, W, y = make_case(700, 128, 2560, torch.bfloat16, seed=43)
+    n = int((y != -100).sum())
+    monkeypatch.setenv(FUSED_ENV, "0" if kernel == "recompute_kernel" else "1")
+    monkeypatch.setenv("MT_FLCE_TEST_FAIL_LAUNCH", kernel)
+    with pytest.raises(_lib.FlceError, match=f"{kernel}: injected launch failure"):
+        train_py_chain(gpu, X, W, y, 1, n)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("MT_FLCE_TEST_FAIL_LAUNCH")
+    path, loss, dX, dW = train_py_chain(gpu, X, W, y, 1, n)
+    assert path == ("general" if kernel == "recompute_kernel" else "fused_unit")
+    check_parity(X, W, y, loss, dX, dW, grad=torch.full((700,), 1.0 / n))
