@@ -192,6 +192,44 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": 4 * n}), flush=True)
 
 
+def mfma_ceiling(dev, shapes=(0, 1), cu_counts=None, launches: int = 3) -> dict:
+    """The register-only bf16 MFMA stream (mt_flce_probe_mfma) on P CUs:
+    achieved TFLOP/s and its fraction of the dense peak of the P CUs and of
+    the chip, timed with HIP events on the current stream (the stream it is
+    launched on).  Operands: random bf16 in N(0, 1)."""
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    Ps = cu_counts or sorted({max(1, cus // 4), cus // 2, 3 * cus // 4, cus})
+    g = torch.Generator(device=dev).manual_seed(7)
+    ops = torch.randn(max(Ps) * 256 * 16 * 8, device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty(max(Ps) * 256, device=dev)
+    stream = _stream(dev)
+    res = {}
+    for shape in shapes:
+        name = ("v_mfma_f32_16x16x32_bf16", "v_mfma_f32_32x32x16_bf16")[shape]
+        fl_it = float(1 << 20) if shape == 0 else float(1 << 19)
+        iters = 60000 if shape == 0 else 120000
+        rows = {}
+        for P in Ps:
+            call = lambda: _lib.check(lib.mt_flce_probe_mfma(shape, P, iters, _p(ops), _p(out),
+                                                             stream), "mt_flce_probe_mfma")
+            call()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(launches):
+                call()
+            e1.record()
+            torch.cuda.synchronize()
+            s = e0.elapsed_time(e1) / launches / 1e3
+            rate = fl_it * iters * 4 * P / s
+            rows[str(P)] = {"ms_per_launch": s * 1e3, "TFLOPs": rate / 1e12,
+                            "frac_of_P_CU_peak": rate / (PEAK_BF16 * P / cus),
+                            "frac_of_chip_peak": rate / PEAK_BF16}
+        res[name] = rows
+    return res
+
+
 class ForcedPath:
     """Sets MT_FLCE_FUSED for the duration of a block ("0": general path)."""
 
@@ -438,6 +476,9 @@ def main():
                     help="only the reference step (timed, then profiled): no variants, no "
                          "general-forward roofline, no other configurations or comparators "
                          "(what the committed rocprofv3 summaries run)")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only run the register-only MFMA stream (mt_flce_probe_mfma) on 1/4, "
+                         "1/2, 3/4 and all of the CUs, both MFMA shapes, and print its rates")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (the reference point that scales "
                          "FETCH_SIZE / WRITE_SIZE counter readings to bytes) and exit")
@@ -447,6 +488,10 @@ def main():
         args.other_configs = ""
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.mfma_ceiling:
+        _lib.load()
+        print(json.dumps({"mfma_ceiling": mfma_ceiling(torch.device("cuda", 0))}), flush=True)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -562,6 +607,12 @@ def main():
             log(f"config {k}: {others[f'config {k}']['ms_per_step']:.2f} ms "
                 f"({others[f'config {k}']['path']}) in {time.perf_counter() - t1:.1f}s")
         out["other_configs"] = others
+    if not args.step_only:
+        # the chip's ceiling for the GEMMs' MFMA instruction on this box, this run
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        c = mfma_ceiling(dev, shapes=(0,), cu_counts=[cus])["v_mfma_f32_16x16x32_bf16"][str(cus)]
+        out["mfma_ceiling"] = {"what": "register-only v_mfma_f32_16x16x32_bf16 stream on every CU "
+                                       "(mt_flce_probe_mfma)", **c}
     if not args.no_torch_gpu:
         torch.cuda.empty_cache()
         tg = torch_gpu_path(data, W.detach(), WORLD_SIZE / N_total)

@@ -455,6 +455,20 @@ int mt_flce_profile_enable(int enable);
 int mt_flce_profile_report(char* buf, size_t len, size_t* needed);
 
 /*
+ * Measurement hook (no counterpart in the reference): the ceiling the GEMM
+ * kernels are measured against -- a register-only stream of bf16 MFMAs on
+ * `workgroups` workgroups of 256 threads, one per CU (each reserves the
+ * whole LDS), every wave iters x (shape 0: 64 v_mfma_f32_16x16x32_bf16, the
+ * GEMM kernels' instruction; 1: 16 v_mfma_f32_32x32x16_bf16) on independent
+ * accumulators (2^20 and 2^19 flops per wave and iteration).  operands:
+ * workgroups x 256 x 16 x 16 bytes of bf16 operand values (device, 16-byte
+ * aligned, loaded once); out: workgroups x 256 fp32 (the accumulator sums).
+ * No memory traffic inside the loop.  Asynchronous on stream.
+ */
+int mt_flce_probe_mfma(int shape, int64_t workgroups, int32_t iters,
+                       const void* operands, float* out, mt_stream_t stream);
+
+/*
  * Cross-entropy over materialised logits, reduction 'none' -- the HF slot of
  * the reference, hf_fixed_cross_entropy_none_reduction
  * (none_reduction_losses.py:27-36 -> F.cross_entropy(source, target,

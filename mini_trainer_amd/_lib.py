@@ -87,6 +87,7 @@ SIGNATURES = {
                                     c_int64, c_int64, c_void_p, c_int64, c_int, c_void_p]),
     "mt_flce_profile_enable": (c_int, [c_int]),
     "mt_flce_profile_report": (c_int, [c_char_p, c_size_t, POINTER(c_size_t)]),
+    "mt_flce_probe_mfma": (c_int, [c_int, c_int64, ctypes.c_int32, c_void_p, c_void_p, c_void_p]),
     "mt_ce_forward": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p, c_int64,
                               c_void_p, c_void_p, c_void_p]),
     "mt_ce_backward": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p, c_int64,

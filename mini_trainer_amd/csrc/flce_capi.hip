@@ -15,6 +15,7 @@
 #include "../../include/mt_flce.h"
 #include "flce_kernels.h"
 #include "flce_kernels_bf16.h"
+#include "flce_probe.h"
 
 using namespace mtf;
 
@@ -1954,6 +1955,23 @@ int mt_flce_profile_report(char* buf, size_t len, size_t* needed) {
   }
   p.recs.clear();
   return MT_OK;
+}
+
+int mt_flce_probe_mfma(int shape, int64_t workgroups, int32_t iters, const void* operands,
+                       float* out, mt_stream_t stream) {
+  if (shape != 0 && shape != 1) return fail(MT_ERR_INVALID_ARGUMENT, "shape %d: 0 or 1", shape);
+  if (workgroups <= 0 || workgroups > 65536 || iters <= 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "workgroups=%lld (1..65536), iters=%d (> 0)",
+                (long long)workgroups, iters);
+  if (!operands || !out || reinterpret_cast<uintptr_t>(operands) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(out) % 4 != 0)
+    return fail(MT_ERR_INVALID_ARGUMENT, "null or misaligned operands / out");
+  hipStream_t s = (hipStream_t)stream;
+  void (*kern)(const u32x4_t*, float*, int32_t, int32_t) =
+      shape == 0 ? mfma_probe_kernel<0> : mfma_probe_kernel<1>;
+  hipLaunchKernelGGL(kern, dim3((uint32_t)workgroups), dim3(256), 0, s,
+                     static_cast<const u32x4_t*>(operands), out, iters, 0);
+  return check_launch("mfma_probe_kernel");
 }
 
 int mt_ce_forward(const void* logits, int64_t T, int64_t V, int64_t ld, int dtype,

@@ -72,16 +72,27 @@ def run_path(monkeypatch, how, X, W, y, scale, dW=None):
     return loss.detach(), Xd.grad, path_of(loss)
 
 
-def check_all(y, loss, dX, rl, rdX):
+def check_all(y, loss, dX, rl, rdX, dx_tol=1e-2):
     """Every row: ignored rows exactly +0.0 / 0, valid rows' loss within 2e-3
-    relative, dX within 1e-2 relative Frobenius."""
+    relative, dX within dx_tol relative Frobenius (1e-2, the north star's)."""
     valid = y != -100
     assert torch.count_nonzero(loss[~valid]) == 0 and not torch.signbit(loss[~valid]).any()
     assert torch.count_nonzero(dX[~valid]) == 0
     err = ((loss[valid] - rl[valid]).abs() / rl[valid].abs()).max().item()
     assert err <= 2e-3, f"loss max rel err {err:.3e}"
     e = rel_fro(dX.float(), rdX.float())
-    assert e <= 1e-2, f"dX rel fro {e:.3e}"
+    print(f"  loss max rel err {err:.3e}, dX rel fro {e:.3e}", flush=True)
+    assert e <= dx_tol, f"dX rel fro {e:.3e}"
+
+
+# The fused paths keep the exponentials E = exp(z) in bf16 and form G = s E
+# from them, so their dX carries the rounding of E where the torch path
+# rounds G (same relative size: ~3e-3 relative Frobenius at configs 2-5,
+# against ~2e-4 for the general path, which rounds G as torch does); the
+# reference chain on the fused kernels (fused_unit) also rounds its
+# unit-gradient dX to bf16 at the forward and again after the rescale
+# (+~0.4e-3).  This bound keeps those known costs from growing.
+FUSED_DX_TOL = 5e-3
 
 
 def check_vocab_sum(dW):
@@ -113,8 +124,9 @@ def test_full_size(gpu, monkeypatch, key):
         else:
             assert path == how
         print(f"{how} ({path}) done", flush=True)
-        check_all(y, loss, dX, rl, rdX)
+        check_all(y, loss, dX, rl, rdX, FUSED_DX_TOL if path.startswith("fused") else 1e-2)
         e = rel_fro(dW, rdW)
+        print(f"  dW rel fro {e:.3e}", flush=True)
         assert e <= 1e-2, f"{how}: dW rel fro {e:.3e}"
         if how == "fused":
             check_vocab_sum(dW)
@@ -145,7 +157,7 @@ def test_config5_accumulation_full_size(gpu, monkeypatch):
         for how in ("fused", "general", "reference"):
             loss, dX, path = run_path(monkeypatch, how, X, Wl if how == "reference" else W, y,
                                       scale, acc.get(how))
-            check_all(y, loss, dX, rl, rdX)
+            check_all(y, loss, dX, rl, rdX, FUSED_DX_TOL if path.startswith("fused") else 1e-2)
         print(f"minibatch {j} done", flush=True)
 
         # fully masked samples: zero loss sum and zero count
@@ -193,3 +205,25 @@ def test_config1_full_size_against_torch_path(gpu):
     seg_loss, seg_cnt = per_sample_loss_sums(loss.detach(), y.to(gpu), cu.to(gpu))
     np.testing.assert_allclose(seg_loss.double().sum().item(), sl.double().sum().item(), rtol=1e-5)
     assert int(seg_cnt.sum()) == n
+
+
+def test_bench_inputs_config3_reference_chain(gpu, monkeypatch):
+    """The timed workload itself: config 3's inputs exactly as bench.py makes
+    them (synth.make_batch on the CPU, seeded, then copied to the device),
+    through the reference's call chain as bench.py times it; every row
+    against the torch path."""
+    cfg = synth.CONFIGS[3]
+    print("config 3, bench.py's own inputs", flush=True)
+    b = synth.make_batch(cfg, 0)
+    X, W, y = b["X"].to(gpu), b["W"].to(gpu), b["target"].to(gpu)
+    del b
+    n = int((y != -100).sum())
+    scale = 1.0 / n
+    rl, rdX, rdW = oracle(X, W, y, scale)
+    Wl = W.detach().requires_grad_(True)
+    loss, dX, path = run_path(monkeypatch, "reference", X, Wl, y, scale)
+    assert path == "fused_unit"
+    check_all(y, loss, dX, rl, rdX, FUSED_DX_TOL)
+    e = rel_fro(Wl.grad.float(), rdW)
+    print(f"  dW rel fro {e:.3e}", flush=True)
+    assert e <= 1e-2, f"dW rel fro {e:.3e}"
