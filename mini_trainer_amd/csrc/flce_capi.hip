@@ -318,6 +318,32 @@ bool split_phase() {
   return e && e[0] == '1';
 }
 
+// XCD partition of a dX-beside-dW launch (DxArgs::xcds): when dX (one K
+// slice) needs fewer CUs than the chip has and dW (tiled fp32) runs over its
+// work queue,
+// dX's tiles go to as few whole XCDs as hold them (k = ceil(tiles / CUs per
+// XCD) < 8, per_xcd = ceil(tiles / k) each, a contiguous logical range per
+// XCD), the dW workers to the rest.  The grid is two workgroups per CU: the
+// first round fills every CU, and on a dX XCD the second round's
+// workgroups take the CUs dX's tiles leave (dW workers); the second round's
+// workgroups on the other XCDs start only once their CUs free up at the
+// end, find the queue empty and return.  Measured on config 3: an XCD's L2
+// serves only dX or only dW while dX runs (launched as one, the two read
+// 18.5 GB per chunk against 13.9 GB launched apart).  Returns the grid, or
+// 0 to keep workgroups [0, tiles) as dX's.  MT_FLCE_DX_XCD_PARTITION=0
+// turns it off (measurement hook).
+int64_t dx_xcd_partition(DxArgs& x, int64_t dxg, bool queue) {
+  const char* e = std::getenv("MT_FLCE_DX_XCD_PARTITION");
+  if ((e && e[0] == '0') || !queue || x.nsplit != 1) return 0;
+  const int64_t cus = device_cus();
+  if (cus % 8 != 0 || dxg <= 0 || dxg >= cus) return 0;
+  const int64_t per_cu = cus / 8, k = cdiv(dxg, per_cu);
+  if (k >= 8) return 0;
+  x.xcds = (int32_t)k;
+  x.per_xcd = (int32_t)cdiv(dxg, k);
+  return 2 * cus;
+}
+
 int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
                       const DxReduce* red = nullptr) {
   if (!split_phase()) {
@@ -347,9 +373,12 @@ int launch_dx_dw_bf16(const DxArgs& x, const DwArgs& w, hipStream_t stream,
     const int64_t dxg = (int64_t)x.tiles_m * x.tiles_n * x.nsplit;
     const int64_t dw_tiles = (int64_t)w.tiles_m * w.tiles_n, cap = grid_cap();
     const int64_t dwg = w.queue ? device_cus() : (cap > 0 ? std::min(dw_tiles, cap) : dw_tiles);
+    int64_t grid = dxg + dwg;
+    DxArgs xa = x;
+    const int64_t part = out == kDwTiles ? dx_xcd_partition(xa, dxg, w.queue != nullptr) : 0;
+    if (part > 0) grid = part;
     const int ph = prof_begin("dx_dw_phase", fx + fw, 0, stream);
-    hipLaunchKernelGGL(k, dim3((uint32_t)(dxg + dwg)), dim3(kThreadsBf), 0, stream, x, w,
-                       (uint32_t)dxg);
+    hipLaunchKernelGGL(k, dim3((uint32_t)grid), dim3(kThreadsBf), 0, stream, xa, w, (uint32_t)dxg);
     MT_TRY(check_launch("dx_dw_bf16_kernel"));
     if (red) {
       launch_dx_reduce(*red, stream);

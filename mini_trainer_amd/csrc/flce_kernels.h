@@ -495,6 +495,13 @@ struct DxArgs {
   // tiles_m * tiles_n * nsplit (dx_split_reduce_kernel sums the slices)
   int32_t nsplit = 1, kslice = 0;
   int64_t split_stride = 0;
+  // dX beside a work-queue dW in one launch (dx_dw_bf16_kernel), XCD-
+  // partitioned: xcds > 0 gives dX whole XCDs -- workgroup b (on XCD b % 8)
+  // takes logical tile (b % 8) per_xcd + b / 8 when b % 8 < xcds and
+  // b / 8 < per_xcd -- and every other workgroup is a dW worker, so that dX
+  // and dW never share an XCD's L2 while dX runs; 0: workgroups [0, tiles)
+  // are dX's (xcd_remap order)
+  int32_t xcds = 0, per_xcd = 0;
 };
 
 // dX of a K-split fused chunk: row t < cn, columns h .. h + 3 of the sum of

@@ -584,6 +584,9 @@ __device__ __forceinline__ void dx_epilogue_bf16(const f32x4_t (&acc)[8][8], con
 // single tile the loop compiles to the MFMAs, LDS reads and DMA only.
 // Workgroup b of nb (b = blockIdx.x unless the launch holds dW as well).
 template <int kMode>
+__device__ __forceinline__ void dx_bf16_tile(char* lds, const DxArgs& a, uint32_t tile);
+
+template <int kMode>
 __device__ __forceinline__ void dx_bf16_body(char* lds, DxArgs a, uint32_t b, uint32_t nb) {
   // K split (nsplit > 1): workgroup b takes slice b % nsplit of tile b / nsplit:
   // the slice's first vocabulary entry becomes K = 0 of E and of W, and its
@@ -601,7 +604,12 @@ __device__ __forceinline__ void dx_bf16_body(char* lds, DxArgs a, uint32_t b, ui
     a.kv = min(a.kslice, a.kv - k0);
     a.accbuf += (int64_t)z * a.split_stride;
   }
-  const uint32_t tile = xcd_remap(b, nb);
+  dx_bf16_tile<kMode>(lds, a, xcd_remap(b, nb));
+}
+
+// One dX output tile (logical id `tile`, none if past the grid).
+template <int kMode>
+__device__ __forceinline__ void dx_bf16_tile(char* lds, const DxArgs& a, uint32_t tile) {
   const int ntiles = tile < (uint32_t)(a.tiles_m * a.tiles_n) ? 1 : 0;
   const EpiCoordsBf ec0;
   KcOp A;
@@ -1067,6 +1075,21 @@ MT_GEMM_BF16_KERNEL void dw_bf16_kernel(DwArgs a) {
 template <int kMode, bool kQueue, int kOut>
 MT_GEMM_BF16_KERNEL void dx_dw_bf16_kernel(DxArgs x, DwArgs w, uint32_t dx_blocks) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  if constexpr (kQueue && kOut == kDwTiles) {  // (the other outputs spill with this path in)
+    if (x.xcds > 0) {
+      // XCD-partitioned (DxArgs::xcds; one K slice, work-queue dW): the
+      // hardware places workgroup b on XCD b % 8, so dX's tiles fill whole
+      // XCDs while the dW workers take the rest and, as dX's workgroups end,
+      // the later workgroups of the grid on those XCDs
+      const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+      const uint32_t t = xcd * (uint32_t)x.per_xcd + slot;
+      if (xcd < (uint32_t)x.xcds && slot < (uint32_t)x.per_xcd && t < dx_blocks)
+        dx_bf16_tile<kMode>(lds, x, t);
+      else
+        dw_bf16_body<kQueue, kOut>(lds, w, 0, 1);
+      return;
+    }
+  }
   if (blockIdx.x < dx_blocks)
     dx_bf16_body<kMode>(lds, x, blockIdx.x, dx_blocks);
   else
