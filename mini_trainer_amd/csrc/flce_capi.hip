@@ -198,6 +198,15 @@ inline uint32_t persistent_grid(int64_t tiles) {
   return (uint32_t)std::min(tiles, cap > 0 ? std::min(cap, device_cus()) : device_cus());
 }
 inline int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
+
+// Grid of a bf16 logits launch over a.tiles_m x a.vt_total tiles whose
+// vocabulary block has `vn` rows: persistent over the full tile columns (the
+// kernel's kTail form runs the partial last column's tiles in the workgroups
+// that get one full tile fewer; at least one workgroup for it).
+uint32_t fwd_grid(const FwdArgs& a, int64_t vn) {
+  const int64_t full = (int64_t)a.tiles_m * (a.vt_total - (vn % 256 != 0 ? 1 : 0));
+  return full > 0 ? persistent_grid(full) : persistent_grid(a.tiles_m);
+}
 inline size_t align_up(size_t a) { return (a + kAlign - 1) / kAlign * kAlign; }
 
 int esize_of(int dtype) { return dtype == MT_DTYPE_BF16 ? 2 : (dtype == MT_DTYPE_F32 ? 4 : 0); }
@@ -699,8 +708,7 @@ int launch_forward(const void* X, const void* W, int64_t Tn, int64_t H, int64_t 
       void (*kern)(FwdArgs) = kb ? kerns_keep[ktail] : kerns[softcap > 0.f][vn % 256 != 0][ktail];
       const int pf = prof_begin(kb ? "fwd_bf16_kernel<keep>" : "fwd_bf16_kernel",
                                 2.0 * H * (double)vn * n_valid, 0, stream);
-      hipLaunchKernelGGL(kern, dim3(persistent_grid(p.tiles_m * a.vt_total)), dim3(kThreadsBf), 0,
-                         stream, a);
+      hipLaunchKernelGGL(kern, dim3(fwd_grid(a, vn)), dim3(kThreadsBf), 0, stream, a);
       prof_end(pf, stream);
       MT_TRY(check_launch("fwd_bf16_kernel"));
       v0 += vn;
@@ -1127,7 +1135,7 @@ int launch_fused(const void* X, const void* W, int64_t Tn, int64_t H, int64_t V,
          {fwd_bf16_kernel<true, kStoreLogits, true, false>,
           fwd_bf16_kernel<true, kStoreLogits, true, true>}}};
     const int ci = softcap > 0.f, ti = V % 256 != 0, ki = H % kBKBf != 0;
-    const dim3 fgrid(persistent_grid(tm * vt));
+    const dim3 fgrid(fwd_grid(a, V));
     const int pf = prof_begin("fwd_bf16_kernel<store_e>", 2.0 * H * (double)V * cn, 0, stream);
     hipLaunchKernelGGL(kerns_e[ci][ti][ki], fgrid, dim3(kThreadsBf), 0, stream, a);
     prof_end(pf, stream);

@@ -291,18 +291,11 @@ __device__ __forceinline__ void fwd_epilogue_exp_bf16(const f32x4_t (&acc)[8][8]
   }
 }
 
-// kTail: V is not a multiple of 256, so the last vocabulary tile masks its
-// columns past V (without it the epilogue skips that select per logit).
-// kKTail: H is not a multiple of 64, so the last K stage is partial.
-// run_if (non-null): the launch does nothing unless *run_if != 0 (the fused
-// path's recomputation of a chunk whose exponentials are out of range);
-// guard_reset (non-null): set to 0 (its readers run after this launch).
-template <bool kCap, int kStore, bool kTail, bool kKTail>
-MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
-  if (a.run_if && *a.run_if == 0) return;
-  if (a.guard_reset && blockIdx.x == 0 && threadIdx.x == 0) *a.guard_reset = 0;
-  const TileSeq seq((uint32_t)(a.tiles_m * a.vt_total));
+// Forward body over ntiles logits tiles; map(k, tm, tv) gives tile k's row
+// tile and vocabulary tile.  kTail: the tiles have columns past V (the
+// epilogue masks them).
+template <bool kCap, int kStore, bool kTail, bool kKTail, class Map>
+__device__ __forceinline__ void fwd_bf16_body(char* lds, const FwdArgs& a, int ntiles, Map map) {
   const EpiCoordsBf ec0;
   const int KT = (a.H + kBKBf - 1) / kBKBf;
   const uint32_t c_lim = (uint32_t)(a.H - (KT - 1) * kBKBf) / 8u;
@@ -314,10 +307,10 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
     B.set_tail(c_lim);
   }
   mainloop_bf16<false, kKTail>(
-      lds, A, B, KT, seq.count(),
+      lds, A, B, KT, ntiles,
       [&](int k) __attribute__((always_inline)) {
         uint32_t tm, tv;
-        grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, kFwdGroupBf, tm, tv);
+        map(k, tm, tv);
         const int32_t row0 = (int32_t)tm * 256, vrow0 = (int32_t)tv * 256;
         A.set_rows(make_rsrc(a.X, a.x_range), [&](uint32_t r) __attribute__((always_inline)) {
           int32_t rr = row0 + (int32_t)r;
@@ -333,7 +326,7 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
       [&](int k, f32x4_t(&acc)[8][8], char* scratch) __attribute__((always_inline)) {
         const EpiCoordsBf ec = fresh(ec0);
         uint32_t tm, tv;
-        grouped_tile(seq.logical(k), a.tiles_m, a.vt_total, kFwdGroupBf, tm, tv);
+        map(k, tm, tv);
         const int32_t row0 = (int32_t)tm * 256;
         int32_t rglob[8], lbl[8];
         float m2[8], d[8];
@@ -353,6 +346,45 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
         __syncthreads();
       },
       ZeroInit(), c_lim);
+}
+
+// kTail: V is not a multiple of 256.  Only the last vocabulary tile column
+// has columns past V, and only its tiles take the masked epilogue, in a
+// tile loop of their own (a select per logit in every tile cost 10k cycles
+// per tile, measured, and the masked and unmasked epilogues in one tile loop
+// spilled): the persistent schedule covers the full columns, and the
+// workgroups that get one full tile fewer in it (their logical start lies
+// in [r, r + tiles_m), r = full tiles mod grid) each run one tile of the
+// last column first (rel, rel + grid, ... when tiles_m exceeds the grid).
+// kKTail: H is not a multiple of 64, so the last K stage is partial.
+// run_if (non-null): the launch does nothing unless *run_if != 0 (the fused
+// path's recomputation of a chunk whose exponentials are out of range);
+// guard_reset (non-null): set to 0 (its readers run after this launch).
+template <bool kCap, int kStore, bool kTail, bool kKTail>
+MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBf];
+  if (a.run_if && *a.run_if == 0) return;
+  if (a.guard_reset && blockIdx.x == 0 && threadIdx.x == 0) *a.guard_reset = 0;
+  const uint32_t vt_full = (uint32_t)a.vt_total - (kTail ? 1u : 0u);
+  const TileSeq seq((uint32_t)a.tiles_m * vt_full);
+  if constexpr (kTail) {
+    const uint32_t P = gridDim.x, r = seq.total % P;
+    const uint32_t rel = seq.first >= r ? seq.first - r : seq.first + P - r;
+    const uint32_t tm_n = (uint32_t)a.tiles_m;
+    if (rel < tm_n) {
+      fwd_bf16_body<kCap, kStore, true, kKTail>(
+          lds, a, (int)((tm_n - rel + P - 1) / P),
+          [&](int k, uint32_t& tm, uint32_t& tv) __attribute__((always_inline)) {
+            tm = rel + (uint32_t)k * P;
+            tv = vt_full;
+          });
+      __syncthreads();
+    }
+  }
+  fwd_bf16_body<kCap, kStore, false, kKTail>(
+      lds, a, seq.count(), [&](int k, uint32_t& tm, uint32_t& tv) __attribute__((always_inline)) {
+        grouped_tile(seq.logical(k), a.tiles_m, vt_full, kFwdGroupBf, tm, tv);
+      });
 }
 
 // Backward recompute epilogue of the bf16 kernel, one fragment row at a
