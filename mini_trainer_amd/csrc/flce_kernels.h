@@ -141,6 +141,21 @@ __device__ __forceinline__ void fwd_tile_update(const f32x4_t (&acc)[8][NFN], fl
   fwd_tile_epilogue<T, NFN, kCap>(acc, m2, d, rel, rglob, ncol0, a, any_hit);
 }
 
+// x of lane l ^ 16 and of lane l ^ 32, from one lane swap and a select
+// (v_permlane16_swap / v_permlane32_swap with x as both operands hand back
+// rows (0, 0, 2, 2) and (1, 1, 3, 3) of 16 lanes, or halves (lo, lo) and
+// (hi, hi)) instead of an LDS permute and its wait.
+__device__ __forceinline__ float xor16(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (lane_id() & 16u) ? p[0] : p[1]);
+}
+__device__ __forceinline__ float xor32(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (lane_id() & 32u) ? p[0] : p[1]);
+}
+
 // Merge the four lanes that share a row, then the WC waves (wn = 0 .. WC - 1)
 // that share the row through LDS, and write this split's (max, sum) partial
 // of every row.
@@ -150,8 +165,8 @@ __device__ __forceinline__ void fwd_final_merge(char* lds, float (&m2)[8], float
                                                 const EpiCoordsT<NFN, WC>& ec, const FwdArgs& a) {
 #pragma unroll
   for (int fm = 0; fm < 8; ++fm) {
-    lse_merge(m2[fm], d[fm], __shfl_xor(m2[fm], 16), __shfl_xor(d[fm], 16));
-    lse_merge(m2[fm], d[fm], __shfl_xor(m2[fm], 32), __shfl_xor(d[fm], 32));
+    lse_merge(m2[fm], d[fm], xor16(m2[fm]), xor16(d[fm]));
+    lse_merge(m2[fm], d[fm], xor32(m2[fm]), xor32(d[fm]));
   }
   float* red = reinterpret_cast<float*>(lds);  // [WC - 1][256 rows][2]
   __syncthreads();
