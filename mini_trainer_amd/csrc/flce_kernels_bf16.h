@@ -708,6 +708,9 @@ __device__ __forceinline__ rsrc_t dw_tiled_rsrc(const DwArgs& a, int32_t m0, int
                                      : a.dW_hi + (int64_t)(tm - a.lo_rows) * a.tiles_n * 65536;
   return make_rsrc(base + (int64_t)(h0 / 256) * 65536, 262144u);
 }
+// Cache policy of the tiled dW's accesses: non-temporal (streamed past the
+// caches that hold the GEMM operand panels).
+constexpr int kDwCpol = 2;
 __device__ __forceinline__ uint32_t dw_tiled_off(const EpiCoordsBf& ec, int fm, int fn) {
   return ((((ec.wm * 2u + ec.wn) * 64u + (uint32_t)fm * 8u + (uint32_t)fn) * 64u) + ec.lane) * 16u;
 }
@@ -755,7 +758,7 @@ __device__ __forceinline__ void dw_load_acc(f32x4_t (&acc)[8][8], const DwArgs& 
 #pragma unroll
       for (int fn = 0; fn < 8; ++fn)
         acc[fm][fn] = load ? __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                          r, dw_tiled_off(ec, fm, fn), 0, 0))
+                                                          r, dw_tiled_off(ec, fm, fn), 0, kDwCpol))
                            : f32x4_t{0.f, 0.f, 0.f, 0.f};
     return;
   }
@@ -867,7 +870,7 @@ __device__ __forceinline__ void dw_store_acc(const f32x4_t (&acc)[8][8], const D
 #pragma unroll
       for (int fn = 0; fn < 8; ++fn)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[fm][fn]), r,
-                                               dw_tiled_off(ec, fm, fn), 0, 0);
+                                               dw_tiled_off(ec, fm, fn), 0, kDwCpol);
       sched_fence();
     }
     return;
@@ -922,7 +925,7 @@ __device__ __forceinline__ void dw_store_then_load(f32x4_t (&acc)[8][8], const D
 #pragma unroll
       for (int fn = 0; fn < 8; ++fn)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[fm][fn]), r,
-                                               dw_tiled_off(ec, fm, fn), 0, 0);
+                                               dw_tiled_off(ec, fm, fn), 0, kDwCpol);
       sched_fence();
     }
 #pragma unroll
@@ -930,7 +933,7 @@ __device__ __forceinline__ void dw_store_then_load(f32x4_t (&acc)[8][8], const D
 #pragma unroll
       for (int fn = 0; fn < 8; ++fn)
         acc[fm][fn] = load ? __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                          nr, dw_tiled_off(ec, fm, fn), 0, 0))
+                                                          nr, dw_tiled_off(ec, fm, fn), 0, kDwCpol))
                            : f32x4_t{0.f, 0.f, 0.f, 0.f};
       sched_fence();
     }
