@@ -362,8 +362,8 @@ def test_real_vocab_tail_qwen(gpu):
     check_parity(X, W, y, loss, dX, dW)
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_persistent_multi_tile(gpu, monkeypatch, fused):
+@pytest.mark.parametrize("fused,cap", [(False, "3"), (True, "3"), (False, "2"), (True, "2")])
+def test_persistent_multi_tile(gpu, monkeypatch, fused, cap):
     # A grid of 3 workgroups makes the persistent bf16 GEMMs (logits,
     # recompute, dW) walk several tiles per workgroup: tile-to-tile
     # pipelining through the LDS ring, the next tile's fragments re-read after
@@ -371,8 +371,12 @@ def test_persistent_multi_tile(gpu, monkeypatch, fused):
     # all exercised at small sizes (dX keeps one workgroup per tile).  The
     # multi-block backward budget adds dX accumulation modes, and with the
     # cap standing in for a 3-CU GPU the general path runs dX and the
-    # persistent dW one after the other instead of side by side.
-    monkeypatch.setenv("MT_FLCE_GRID_CAP", "3")
+    # persistent dW one after the other instead of side by side.  V = 2300
+    # leaves a partial last vocabulary tile: its 3 row tiles run first in the
+    # workgroups with one full tile fewer, under a 2-workgroup grid two of
+    # them in one workgroup.
+    print(f"case persistent multi-tile fused={fused} cap={cap}", flush=True)
+    monkeypatch.setenv("MT_FLCE_GRID_CAP", cap)
     if fused:
         monkeypatch.setenv("MT_FLCE_FUSED", "1")
     else:
