@@ -7,6 +7,8 @@ north-star tolerances (loss 2e-3 relative in bf16 and 1e-5 in fp32, dX and dW
     40 bf16; H = 100 fp32), on the general, fused and unit-gradient paths;
   * H not a whole 16-byte chunk (H = 1001 bf16, 1002 fp32): zero columns
     appended on the host;
+  * V below one 256-column tile (V = 200, 37): every logits tile is a tail
+    tile;
   * a weight beyond one buffer's reach (vocabulary blocks on the forward and
     the general backward; the fused planner declines it) and X beyond it
     (row ranges on the host), under the MT_FLCE_MAX_BUFFER_BYTES test hook
@@ -60,6 +62,20 @@ def test_partial_last_k_stage_bf16(gpu, monkeypatch, H, how):
     assert path == {"general": "general", "fused": "fused", "unit": "fused_unit"}[how]
     n = int((y != -100).sum())
     check_parity(X, W, y, loss, dX, dW, grad=torch.full((600,), 1.0 / n))
+
+
+@pytest.mark.parametrize("V", [200, 37])
+@pytest.mark.parametrize("how", ["general", "fused", "unit"])
+def test_vocabulary_below_one_tile(gpu, monkeypatch, V, how):
+    """V < 256: no full vocabulary tile at all, so every logits tile is a
+    tail tile, run by the workgroups of the tail loop alone."""
+    print(f"case vocabulary below one tile V={V} {how}", flush=True)
+    monkeypatch.setenv(FUSED_ENV, "0" if how == "general" else "1")
+    X, W, y = make_case(700, 128, V, torch.bfloat16, seed=V, w_std=0.2)
+    path, loss, dX, dW = run(gpu, X, W, y, how)
+    assert path == {"general": "general", "fused": "fused", "unit": "fused_unit"}[how]
+    n = int((y != -100).sum())
+    check_parity(X, W, y, loss, dX, dW, grad=torch.full((700,), 1.0 / n))
 
 
 def test_partial_last_k_stage_softcap(gpu, monkeypatch):
