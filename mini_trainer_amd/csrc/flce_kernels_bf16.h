@@ -71,8 +71,10 @@ struct TileSeq {
 // fused_row_scale_kernel), which saves the pass over S that forms G.
 // Row tiles per group of the forward's tile walk: W (the larger operand) is
 // streamed once per group, so wider groups cut its re-reads (8: 2% faster
-// than 4 at config 3; 16 is no better and costs L2 hits).
-constexpr uint32_t kFwdGroupBf = 8;
+// than 4 at config 3; 12, a config-3 chunk's whole 12 row tiles, a further
+// 0.4% in three same-box rotations against 8 and 6, and the same as 8 and
+// 16 at config 4's 23 row tiles).
+constexpr uint32_t kFwdGroupBf = 12;
 
 // Forward tile epilogue of the bf16 kernels, one fragment row fm at a time
 // (a scheduling fence after each keeps a single row group's values in
