@@ -70,11 +70,13 @@ struct TileSeq {
 // then s E with a per-row factor s applied downstream (see
 // fused_row_scale_kernel), which saves the pass over S that forms G.
 // Row tiles per group of the forward's tile walk: W (the larger operand) is
-// streamed once per group, so wider groups cut its re-reads (8: 2% faster
-// than 4 at config 3; 12, a config-3 chunk's whole 12 row tiles, a further
-// 0.4% in three same-box rotations against 8 and 6, and the same as 8 and
-// 16 at config 4's 23 row tiles).
-constexpr uint32_t kFwdGroupBf = 12;
+// streamed once per group, so wider groups cut its re-reads.  Up to 12 row
+// tiles walk as one group, more in groups of 8.  Measured in same-box
+// rotations: 8 against 4, 2% faster at config 3; a config-3 chunk's 12 row
+// tiles as one group, a further 0.4% against 8 and 6; config 5's 26 row
+// tiles in groups of 12, 0.8% slower than in groups of 8; config 4's 23
+// the same in groups of 8, 12 and 16.
+__device__ __forceinline__ uint32_t fwd_group(uint32_t tiles_m) { return tiles_m <= 12u ? tiles_m : 8u; }
 
 // Forward tile epilogue of the bf16 kernels, one fragment row fm at a time
 // (a scheduling fence after each keeps a single row group's values in
@@ -391,7 +393,7 @@ MT_GEMM_BF16_KERNEL void fwd_bf16_kernel(FwdArgs a) {
   }
   fwd_bf16_body<kCap, kStore, false, kKTail>(
       lds, a, seq.count(), [&](int k, uint32_t& tm, uint32_t& tv) __attribute__((always_inline)) {
-        grouped_tile(seq.logical(k), a.tiles_m, vt_full, kFwdGroupBf, tm, tv);
+        grouped_tile(seq.logical(k), a.tiles_m, vt_full, fwd_group((uint32_t)a.tiles_m), tm, tv);
       });
 }
 
